@@ -1,0 +1,228 @@
+/*
+ * manta_rocm.h -- C ABI of libmanta_rocm.so, the MI355X (gfx950) backend for
+ * Manta's retrieval hot path: packed q8/q4 candidate scoring (dot, cosine,
+ * l2_distance with dequantization fused into the kernel), top-k selection, and
+ * the embed pipeline (gather -> @matmul -> masked mean_pool -> normalize).
+ *
+ * The reference (odvcencio/manta, Go) reaches its CUDA device through a cgo C
+ * preamble in runtime/backends/cuda/native_linux.go.  This header is the
+ * equivalent surface for a `runtime/backends/rocm` cgo package; each entry
+ * point names the reference function it takes over.
+ *
+ * Conventions (same as the reference shim, native_linux.go:30-75,620-624):
+ *   - every fallible call returns MANTA_ROCM_OK (0) or an error code and, on
+ *     error, stores a malloc'd message in *err (if err != NULL) that the
+ *     caller releases with manta_rocm_free_error;
+ *   - MANTA_ROCM_UNSUPPORTED marks a shape the device path does not take;
+ *     the Go side then runs the host reference with
+ *     execution_mode=host_fallback, as cuda.go:248-257 does;
+ *   - a runtime is bound to one device and owns one HIP stream; calls are
+ *     asynchronous on that stream unless they return host data; one runtime
+ *     must not be used from two threads at once (the reference's
+ *     deviceRuntime has the same rule, cuda.go:69-71);
+ *   - "_dev" pointers are device addresses (from manta_rocm_malloc or any
+ *     HIP allocation on the runtime's device); other pointers are host.
+ *
+ * Packed formats (this library's contract; the reference has only
+ * f32-backed fake-quantized q4/q8, runtime/backend/tensor.go:49-71):
+ *   q8 rows   [n, d] int8 codes + f32 scale per row.
+ *   q4 blocks [n, d/2] bytes, two's-complement nibbles, low nibble first,
+ *             blocks of 32 along d, f16 scale per block ([n, d/32]).
+ */
+#ifndef MANTA_ROCM_H
+#define MANTA_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MANTA_ROCM_ABI_VERSION 1
+
+enum {
+    MANTA_ROCM_OK = 0,
+    MANTA_ROCM_ERROR = 1,
+    MANTA_ROCM_UNSUPPORTED = 2,
+};
+
+/* Score builtins: the kernel body op names dot / cosine / l2_distance
+ * (compiler/compiler.go:803-842, classified at native_linux.go:1734-1750). */
+enum {
+    MANTA_ROCM_DOT = 0,
+    MANTA_ROCM_COSINE = 1,
+    MANTA_ROCM_L2_DISTANCE = 2,
+};
+
+/* Selection order.  LARGEST is topKTensor's order (value desc, index asc;
+ * runtime/backend/tensor_ops.go:1539-1551).  SMALLEST (value asc, index asc)
+ * is the smallest-k extension an l2 rerank needs. */
+enum {
+    MANTA_ROCM_LARGEST = 0,
+    MANTA_ROCM_SMALLEST = 1,
+};
+
+enum {
+    MANTA_ROCM_Q8_ROWS = 8,
+    MANTA_ROCM_Q4_BLOCKS = 4,
+};
+
+/* Projection kinds for the embed pipeline. */
+enum {
+    MANTA_ROCM_PROJ_F16 = 0,    /* f16 [d, e] */
+    MANTA_ROCM_PROJ_Q8_COL = 1, /* int8 [d, e] + f32 scale per output column */
+};
+
+typedef struct MantaRocm MantaRocm;
+typedef struct MantaRocmCandidates MantaRocmCandidates;
+
+typedef struct {
+    uint64_t kernel_launches;
+    uint64_t bytes_uploaded;
+    uint64_t bytes_downloaded;
+    uint64_t workspace_bytes;
+    uint64_t candidate_bytes;
+} MantaRocmStats;
+
+int manta_rocm_abi_version(void);
+
+/* ---- runtime ---------------------------------------------------------- */
+
+/* Number of visible HIP devices (0 when none). */
+int manta_rocm_device_count(int* out, char** err);
+
+/* Replaces mantaCudaRuntimeCreate (native_linux.go:108-169): binds device
+ * `device`, creates the runtime's stream. */
+int manta_rocm_create(int device, MantaRocm** out, char** err);
+
+/* Replaces mantaCudaRuntimeDestroy (native_linux.go:171-189). */
+void manta_rocm_destroy(MantaRocm* rt);
+
+/* Replaces mantaCudaFreeCString (native_linux.go:620-624). */
+void manta_rocm_free_error(char* msg);
+
+/* Use an external HIP stream (hipStream_t) for all later work, or NULL for
+ * the runtime's own stream.  No reference counterpart (the CUDA shim always
+ * uses the legacy stream, native_linux.go:391). */
+int manta_rocm_set_stream(MantaRocm* rt, void* hip_stream, char** err);
+
+/* Replaces mantaCudaSynchronize (native_linux.go:341-353). */
+int manta_rocm_synchronize(MantaRocm* rt, char** err);
+
+/* Replaces mantaCudaMemAlloc / mantaCudaMemFree (native_linux.go:285-311). */
+int manta_rocm_malloc(MantaRocm* rt, void** out_dev, size_t bytes, char** err);
+int manta_rocm_free(MantaRocm* rt, void* dev, char** err);
+
+/* Replace mantaCudaMemcpyHtoD / DtoH (native_linux.go:313-339); download
+ * synchronizes the stream first. */
+int manta_rocm_upload(MantaRocm* rt, void* dst_dev, const void* src, size_t bytes, char** err);
+int manta_rocm_download(MantaRocm* rt, void* dst, const void* src_dev, size_t bytes, char** err);
+
+/* Counters in the spirit of matMulStatsSnapshot (native_linux.go:1474-1481). */
+int manta_rocm_stats(const MantaRocm* rt, MantaRocmStats* out);
+
+/* Per-kernel-family device timing.  With timing on, every launch is
+ * bracketed by HIP events on the runtime's stream.  manta_rocm_timing
+ * synchronizes, folds the finished events into totals and reports the launch
+ * count and summed milliseconds of one family ("q8_scan", "q4_scan",
+ * "topk_merge", "embed", ...; NULL = all), optionally clearing the totals.
+ * Extends the reference's matmul counters (recordMatMulRun,
+ * native_linux.go:1483-1497) with device time. */
+int manta_rocm_set_timing(MantaRocm* rt, int on, char** err);
+int manta_rocm_timing(MantaRocm* rt, const char* name, uint64_t* count, double* total_ms, int reset,
+                      char** err);
+
+/* ---- packing and candidate binding ------------------------------------ */
+
+/* Host packers for f32 rows (the values a reference q8/q4 tensor carries).
+ * Replace the per-tensor fake quantization grid (cuda quantizeBufferInPlace,
+ * native_linux.go:2588-2619) with per-row / per-block packed storage. */
+int manta_rocm_pack_q8_rows(const float* x, int64_t n, int64_t d, int8_t* codes, float* scales,
+                            char** err);
+int manta_rocm_pack_q4_blocks(const float* x, int64_t n, int64_t d, uint8_t* packed,
+                              uint16_t* scales, char** err);
+
+/* Make a device-resident candidate matrix from packed host arrays:
+ * `sets` independent [n, d] matrices (sets == 1: one matrix shared by every
+ * query, the [Q,D] x [N,D] form; sets == Q: one per query, the reference's
+ * batched [Q,D] x [Q,N,D] form, tensor_ops.go:1511-1519).  Computes the
+ * per-row norm constants.  Takes over the role of bindResidentMatMulParams
+ * (cuda.go:129-169) for score inputs, which the reference re-uploads as f32
+ * on every call (native_linux.go:1705-1714). */
+int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* scales, int64_t sets,
+                            int64_t n, int64_t d, MantaRocmCandidates** out, char** err);
+int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16_t* scales,
+                              int64_t sets, int64_t n, int64_t d, MantaRocmCandidates** out,
+                              char** err);
+void manta_rocm_unbind(MantaRocmCandidates* cands);
+int manta_rocm_candidates_info(const MantaRocmCandidates* cands, int* format, int64_t* sets,
+                               int64_t* n, int64_t* d);
+
+/* ---- scoring ------------------------------------------------------------ */
+
+/* Full score matrix.  queries_dev: f16 [nq, d]; out_scores_dev: f32 [nq, n].
+ * Replaces runScoreKernel (native_linux.go:1694-1732) and the host
+ * dotRows / cosineRows / l2DistanceRows (tensor_ops.go:1366-1490) for packed
+ * candidates. */
+int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* cands, int op,
+                     const uint16_t* queries_dev, int64_t nq, float* out_scores_dev, char** err);
+
+/* Fused scoring + top-k: the score matrix is never written.  out_ids_dev
+ * int32 [nq, k]; out_scores_dev f32 [nq, k] (may be NULL); out_acc_dev int64
+ * [nq, k] (may be NULL): the exact integer accumulator of each selected row
+ * (q8 candidates only).  Replaces launch_kernel(score) followed by the host
+ * topk step (tensor_ops.go:119-135, 1523-1592).  Errors like topKTensor when
+ * k <= 0 or k > n. */
+int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* cands, int op, int order,
+                          const uint16_t* queries_dev, int64_t nq, int64_t k,
+                          int32_t* out_ids_dev, float* out_scores_dev, int64_t* out_acc_dev,
+                          char** err);
+
+/* top-k over an f32 score matrix [rows, cols] (rows == 1 is the rank-1
+ * form).  Replaces topKTensor (tensor_ops.go:1523-1592). */
+int manta_rocm_topk(MantaRocm* rt, const float* scores_dev, int64_t rows, int64_t cols, int64_t k,
+                    int order, int32_t* out_ids_dev, float* out_values_dev, char** err);
+
+/* ---- embed pipeline ---------------------------------------------------- */
+
+/* gatherTensor, f16 table [vocab, d] x int32 indices [nidx] -> f16
+ * [nidx, d] (tensor_ops.go:794-877).  An out-of-range index is reported as
+ * "gather index %d out of range" (the first offending position's value). */
+int manta_rocm_gather_rows_f16(MantaRocm* rt, const uint16_t* table_dev, int64_t vocab, int64_t d,
+                               const int32_t* idx_dev, int64_t nidx, uint16_t* out_dev,
+                               char** err);
+
+/* matmulTensor [m,k] x [k,n] with f16 operands and f32 accumulation, f32
+ * out (tensor_ops.go:981-1062; the CUDA path is cublasSgemm,
+ * native_linux.go:509-549).  rhs is f16 or q8-per-column (proj_kind). */
+int manta_rocm_matmul_f16(MantaRocm* rt, const uint16_t* lhs_dev, int64_t m, int64_t k,
+                          const void* rhs_dev, int proj_kind, const float* col_scale_dev,
+                          int64_t n, float* out_dev, char** err);
+
+/* meanPoolMaskedTensor rank 3: f32 [b,t,c] with int32 mask [b,t] -> f32
+ * [b,c] (tensor_ops.go:1210-1275). */
+int manta_rocm_mean_pool_masked(MantaRocm* rt, const float* x_dev, const int32_t* mask_dev,
+                                int64_t b, int64_t t, int64_t c, float* out_dev, char** err);
+
+/* normalizeRows: f32 [rows, cols] in place (tensor_ops.go:1114-1138, the
+ * CUDA row-wise kernel at compiler/compiler.go:731-745). */
+int manta_rocm_normalize_rows(MantaRocm* rt, float* x_dev, int64_t rows, int64_t cols,
+                              char** err);
+
+/* The whole embed entry point in one fused launch sequence:
+ * gather(table, tokens) -> @matmul(proj) -> mean_pool(mask) -> normalize,
+ * f16 output [b, e].  The [b,t,e] intermediate never reaches HBM.  Takes over
+ * the host gather + cuBLAS + host mean_pool chain of
+ * EmbeddingModel.EmbedBatch (runtime/embedding_model.go:422; stack in
+ * tensor_ops.go:31-47, native_linux.go:3608-3670, tensor_ops.go:1210). */
+int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens_dev, const int32_t* mask_dev,
+                            int64_t b, int64_t t, const uint16_t* table_dev, int64_t vocab,
+                            int64_t d, const void* proj_dev, int proj_kind,
+                            const float* col_scale_dev, int64_t e, uint16_t* out_dev,
+                            char** err);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,172 @@
+// device_common.hpp -- device helpers shared by the gfx950 kernels.
+//
+//  * exact f32 arithmetic for the scoring epilogues (every op rounded on its
+//    own, no contraction), so GPU scores equal the CPU contract bit for bit;
+//  * 64-bit selection keys giving topKTensor's total order
+//    (runtime/backend/tensor_ops.go:1539-1551: value desc, index asc);
+//  * a workgroup-wide top-k reservoir in LDS (threshold filter + bitonic
+//    compaction) used by the fused scoring kernels and by the merge pass.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+namespace manta {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct QConst {
+    float a;  // e8: qmax      e16: qs
+    float b;  // e16: |q|
+    float c;  // e16: |q|^2
+    float d;
+};
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ uint16_t f2h(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// C roundf: half away from zero.  x - trunc(x) is exact for every finite x.
+__device__ __forceinline__ float round_half_away(float x) {
+    float t = __builtin_truncf(x);
+    float d = x - t;
+    if (__builtin_fabsf(d) >= 0.5f) t += __builtin_copysignf(1.0f, x);
+    return t;
+}
+
+__device__ __forceinline__ float fmul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float fadd_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float fsub_rn(float a, float b) { return __fsub_rn(a, b); }
+__device__ __forceinline__ float fdiv_rn(float a, float b) { return __fdiv_rn(a, b); }
+__device__ __forceinline__ float fsqrt_rn(float a) { return __fsqrt_rn(a); }
+
+// Order-preserving map float -> u32 with -0 folded onto +0 (the reference
+// compares with <, >, so -0 and +0 tie and fall through to the index).
+__device__ __forceinline__ uint32_t float_order(float s) {
+    uint32_t b = __float_as_uint(s);
+    if (b == 0x80000000u) b = 0u;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float order_float(uint32_t o) {
+    uint32_t b = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+    return __uint_as_float(b);
+}
+
+// Larger key == better.  Valid keys are never 0 (the low word ~idx has its
+// top bit set for idx < 2^31), so 0 is the "empty" key.
+__device__ __forceinline__ uint64_t make_key(float score, uint32_t idx, int smallest) {
+    uint32_t o = float_order(score);
+    if (smallest) o = ~o;
+    return ((uint64_t)o << 32) | (uint64_t)(~idx);
+}
+
+__device__ __forceinline__ uint32_t key_index(uint64_t key) { return ~(uint32_t)key; }
+
+__device__ __forceinline__ float key_score(uint64_t key, int smallest) {
+    uint32_t o = (uint32_t)(key >> 32);
+    if (smallest) o = ~o;
+    return order_float(o);
+}
+
+// ---------------------------------------------------------------- top-k
+
+// LDS state of a block reservoir: keys[cap] (cap a power of two), count and
+// threshold.  Invariant between rounds: keys[0..cnt) are distinct offered
+// keys; if cnt == k after a compaction they are the k best seen so far and
+// tau is the k-th, otherwise tau == 0 and nothing was dropped.
+struct TopKShared {
+    int cnt;
+    int pad;
+    uint64_t tau;
+};
+
+__device__ __forceinline__ int next_pow2(int x) {
+    int p = 2;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+// Bitonic sort, descending, of keys[0..S) (S a power of two) by the whole
+// workgroup.  Ends with a barrier.
+__device__ inline void block_sort_desc(uint64_t* keys, int S) {
+    const int tid = threadIdx.x;
+    const int nt = blockDim.x;
+    for (int size = 2; size <= S; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < (S >> 1); i += nt) {
+                int lo = 2 * i - (i & (stride - 1));
+                int hi = lo + stride;
+                bool desc = (lo & size) == 0;
+                uint64_t a = keys[lo];
+                uint64_t b = keys[hi];
+                if (desc ? (a < b) : (a > b)) {
+                    keys[lo] = b;
+                    keys[hi] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__device__ __forceinline__ void topk_init(uint64_t* keys, TopKShared* st) {
+    if (threadIdx.x == 0) {
+        st->cnt = 0;
+        st->tau = 0;
+    }
+    __syncthreads();
+}
+
+// Offer one key per thread (0 = nothing).  Keys above the threshold are
+// appended; one LDS atomic per wave.  Caller guarantees room for
+// blockDim.x more keys, and calls block_sync afterwards.
+__device__ __forceinline__ void topk_offer(uint64_t key, uint64_t tau, uint64_t* keys,
+                                           TopKShared* st) {
+    const int lane = threadIdx.x & 63;
+    bool take = key > tau;
+    uint64_t mask = __ballot(take);
+    if (mask == 0) return;
+    int leader = __ffsll((unsigned long long)mask) - 1;
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&st->cnt, __popcll(mask));
+    base = __shfl(base, leader);
+    if (take) {
+        uint64_t below = lane ? (mask & ((~0ull) >> (64 - lane))) : 0ull;
+        keys[base + __popcll(below)] = key;
+    }
+}
+
+// Keep the best k of the reservoir (sorted, descending, in keys[0..)).
+// Must be called by the whole workgroup after a barrier.
+__device__ inline void topk_compact(uint64_t* keys, TopKShared* st, int k) {
+    int c = st->cnt;
+    int S = next_pow2(c < 2 ? 2 : c);
+    for (int i = c + (int)threadIdx.x; i < S; i += blockDim.x) keys[i] = 0;
+    __syncthreads();
+    block_sort_desc(keys, S);
+    if (threadIdx.x == 0) {
+        int m = c < k ? c : k;
+        st->cnt = m;
+        st->tau = (m == k) ? keys[k - 1] : 0ull;
+    }
+    __syncthreads();
+}
+
+// Compact when another round of blockDim.x offers might not fit.
+// The barrier after reading the count keeps every thread's decision equal:
+// no thread starts the next round's appends before all have read it.
+__device__ __forceinline__ void topk_maybe_compact(uint64_t* keys, TopKShared* st, int k,
+                                                   int cap) {
+    int c = st->cnt;
+    __syncthreads();
+    if (c + (int)blockDim.x > cap) topk_compact(keys, st, k);
+}
+
+}  // namespace manta

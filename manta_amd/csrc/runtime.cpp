@@ -1,0 +1,772 @@
+// runtime.cpp -- implementation of the C ABI in include/manta_rocm.h.
+//
+// Host side of the rocm backend: argument validation with the reference's
+// error conditions and wording, device memory, candidate binding, workspace
+// management and the launch sequences of each entry point.  The reference
+// counterpart is the cgo preamble and deviceRuntime of
+// runtime/backends/cuda/native_linux.go; the semantic checks mirror
+// runtime/backend/tensor_ops.go (scoreLayout :1499-1521, topKTensor
+// :1523-1534, gatherTensor :794-877).
+#include "manta_rocm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "pack.hpp"
+
+using manta::QConst;
+using manta::ScanArgs;
+
+struct TimedLaunch {
+    const char* name;
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+
+struct MantaRocm {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    MantaRocmStats stats{};
+    // per-kernel-family timing (manta_rocm_set_timing)
+    bool timing = false;
+    std::vector<TimedLaunch> pending;
+    std::vector<hipEvent_t> event_pool;
+    std::map<std::string, std::pair<uint64_t, double>> totals;
+};
+
+struct MantaRocmCandidates {
+    MantaRocm* rt = nullptr;
+    int format = 0;
+    int64_t sets = 0, n = 0, d = 0;
+    int pitch = 0;  // bytes per row in device memory
+    int nb = 0;     // q4 blocks per row
+    void* codes = nullptr;
+    void* scales = nullptr;
+    float* dnorm = nullptr;
+    float* dd = nullptr;
+    size_t bytes = 0;
+};
+
+namespace {
+
+constexpr int64_t kMaxDim = 1024;     // exactness bound of the int32 / f32 accumulators
+constexpr int64_t kMaxDeviceK = 2048;  // reservoir capacity bound (LDS)
+
+char* dup_printf(const char* fmt, va_list ap) {
+    va_list ap2;
+    va_copy(ap2, ap);
+    int n = vsnprintf(nullptr, 0, fmt, ap2);
+    va_end(ap2);
+    if (n < 0) return nullptr;
+    char* out = (char*)malloc((size_t)n + 1);
+    if (!out) return nullptr;
+    vsnprintf(out, (size_t)n + 1, fmt, ap);
+    return out;
+}
+
+int fail(char** err, int code, const char* fmt, ...) {
+    if (err) {
+        va_list ap;
+        va_start(ap, fmt);
+        *err = dup_printf(fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+int hip_fail(char** err, const char* what, hipError_t e) {
+    return fail(err, MANTA_ROCM_ERROR, "%s: %s (%s)", what, hipGetErrorName(e),
+                hipGetErrorString(e));
+}
+
+#define HIP_TRY(call, what)                                  \
+    do {                                                     \
+        hipError_t e_ = (call);                              \
+        if (e_ != hipSuccess) return hip_fail(err, what, e_); \
+    } while (0)
+
+hipEvent_t pooled_event(MantaRocm* rt) {
+    if (!rt->event_pool.empty()) {
+        hipEvent_t e = rt->event_pool.back();
+        rt->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Every kernel launch goes through here: counts it and, when timing is on,
+// brackets it with events on the runtime's stream.
+#define LAUNCH_TRY(call, what)                                                  \
+    do {                                                                        \
+        hipEvent_t ea_ = nullptr, eb_ = nullptr;                                \
+        if (rt->timing) {                                                       \
+            ea_ = pooled_event(rt);                                             \
+            if (ea_) (void)hipEventRecord(ea_, rt->stream);                     \
+        }                                                                       \
+        HIP_TRY((call), what);                                                  \
+        if (rt->timing && ea_) {                                                \
+            eb_ = pooled_event(rt);                                             \
+            if (eb_) {                                                          \
+                (void)hipEventRecord(eb_, rt->stream);                          \
+                rt->pending.push_back(TimedLaunch{what, ea_, eb_});             \
+            } else {                                                            \
+                rt->event_pool.push_back(ea_);                                  \
+            }                                                                   \
+        }                                                                       \
+        rt->stats.kernel_launches++;                                            \
+    } while (0)
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+int ensure_workspace(MantaRocm* rt, size_t bytes, char** err) {
+    if (bytes <= rt->ws_bytes) return MANTA_ROCM_OK;
+    if (rt->ws) {
+        HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+        HIP_TRY(hipFree(rt->ws), "hipFree");
+        rt->ws = nullptr;
+        rt->ws_bytes = 0;
+    }
+    size_t want = align_up(bytes, (size_t)1 << 20);
+    HIP_TRY(hipMalloc(&rt->ws, want), "hipMalloc(workspace)");
+    rt->ws_bytes = want;
+    rt->stats.workspace_bytes = want;
+    return MANTA_ROCM_OK;
+}
+
+// Carve a workspace into aligned slices.
+struct Carver {
+    char* base;
+    size_t off = 0;
+    explicit Carver(void* b) : base((char*)b) {}
+    template <class T>
+    T* take(size_t count) {
+        off = align_up(off, 256);
+        T* p = (T*)(base + off);
+        off += count * sizeof(T);
+        return p;
+    }
+};
+
+int cap_for_k(int64_t k) {
+    int cap = 512;
+    while (cap < k + 256) cap <<= 1;
+    return cap;
+}
+
+// Row consts over many rows, spread over host threads.
+template <class F>
+void parallel_rows(int64_t rows, F f) {
+    unsigned hw = std::thread::hardware_concurrency();
+    int64_t nt = std::min<int64_t>(hw ? hw : 4, 16);
+    if (rows < 65536) nt = 1;
+    if (nt <= 1) {
+        f(0, rows);
+        return;
+    }
+    std::vector<std::thread> th;
+    int64_t per = (rows + nt - 1) / nt;
+    for (int64_t t = 0; t < nt; t++) {
+        int64_t a = t * per, b = std::min(rows, a + per);
+        if (a >= b) break;
+        th.emplace_back([=] { f(a, b); });
+    }
+    for (auto& x : th) x.join();
+}
+
+int set_device(MantaRocm* rt, char** err) {
+    HIP_TRY(hipSetDevice(rt->device), "hipSetDevice");
+    return MANTA_ROCM_OK;
+}
+
+#define RT_CHECK(rt)                                                          \
+    do {                                                                      \
+        if (!(rt)) return fail(err, MANTA_ROCM_ERROR, "nil rocm runtime");    \
+        int rc_ = set_device((rt), err);                                      \
+        if (rc_) return rc_;                                                  \
+    } while (0)
+
+int free_candidates_memory(MantaRocmCandidates* c) {
+    if (!c) return 0;
+    if (c->codes) (void)hipFree(c->codes);
+    if (c->scales) (void)hipFree(c->scales);
+    if (c->dnorm) (void)hipFree(c->dnorm);
+    if (c->dd) (void)hipFree(c->dd);
+    c->codes = c->scales = nullptr;
+    c->dnorm = c->dd = nullptr;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int manta_rocm_abi_version(void) { return MANTA_ROCM_ABI_VERSION; }
+
+void manta_rocm_free_error(char* msg) { free(msg); }
+
+int manta_rocm_device_count(int* out, char** err) {
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil output");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) {
+        *out = 0;
+        return MANTA_ROCM_OK;
+    }
+    if (e != hipSuccess) {
+        *out = 0;
+        return hip_fail(err, "hipGetDeviceCount", e);
+    }
+    *out = n;
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_create(int device, MantaRocm** out, char** err) {
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil output");
+    *out = nullptr;
+    int n = 0;
+    int rc = manta_rocm_device_count(&n, err);
+    if (rc) return rc;
+    if (n == 0) return fail(err, MANTA_ROCM_UNSUPPORTED, "no ROCm device available");
+    if (device < 0 || device >= n)
+        return fail(err, MANTA_ROCM_ERROR, "rocm device %d out of range (%d devices)", device, n);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "device %d is %s; libmanta_rocm is built for gfx950",
+                    device, prop.gcnArchName);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    MantaRocm* rt = new MantaRocm();
+    rt->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&rt->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete rt;
+        return hip_fail(err, "hipStreamCreate", e);
+    }
+    rt->stream = rt->own_stream;
+    *out = rt;
+    return MANTA_ROCM_OK;
+}
+
+void manta_rocm_destroy(MantaRocm* rt) {
+    if (!rt) return;
+    (void)hipSetDevice(rt->device);
+    (void)hipStreamSynchronize(rt->stream);
+    for (auto& t : rt->pending) {
+        (void)hipEventDestroy(t.start);
+        (void)hipEventDestroy(t.stop);
+    }
+    for (auto e : rt->event_pool) (void)hipEventDestroy(e);
+    if (rt->ws) (void)hipFree(rt->ws);
+    if (rt->own_stream) (void)hipStreamDestroy(rt->own_stream);
+    delete rt;
+}
+
+int manta_rocm_set_stream(MantaRocm* rt, void* hip_stream, char** err) {
+    RT_CHECK(rt);
+    HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    rt->stream = hip_stream ? (hipStream_t)hip_stream : rt->own_stream;
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_synchronize(MantaRocm* rt, char** err) {
+    RT_CHECK(rt);
+    HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_malloc(MantaRocm* rt, void** out_dev, size_t bytes, char** err) {
+    RT_CHECK(rt);
+    if (!out_dev) return fail(err, MANTA_ROCM_ERROR, "nil output");
+    *out_dev = nullptr;
+    HIP_TRY(hipMalloc(out_dev, bytes ? bytes : 1), "hipMalloc");
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_free(MantaRocm* rt, void* dev, char** err) {
+    RT_CHECK(rt);
+    if (!dev) return MANTA_ROCM_OK;
+    HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    HIP_TRY(hipFree(dev), "hipFree");
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_upload(MantaRocm* rt, void* dst_dev, const void* src, size_t bytes, char** err) {
+    RT_CHECK(rt);
+    if (bytes == 0) return MANTA_ROCM_OK;
+    if (!dst_dev || !src) return fail(err, MANTA_ROCM_ERROR, "nil upload pointer");
+    HIP_TRY(hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, rt->stream),
+            "hipMemcpyHtoD");
+    HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    rt->stats.bytes_uploaded += bytes;
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_download(MantaRocm* rt, void* dst, const void* src_dev, size_t bytes, char** err) {
+    RT_CHECK(rt);
+    if (bytes == 0) return MANTA_ROCM_OK;
+    if (!dst || !src_dev) return fail(err, MANTA_ROCM_ERROR, "nil download pointer");
+    HIP_TRY(hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, rt->stream),
+            "hipMemcpyDtoH");
+    HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    rt->stats.bytes_downloaded += bytes;
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_set_timing(MantaRocm* rt, int on, char** err) {
+    RT_CHECK(rt);
+    rt->timing = on != 0;
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_timing(MantaRocm* rt, const char* name, uint64_t* count, double* total_ms, int reset,
+                      char** err) {
+    RT_CHECK(rt);
+    HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    for (auto& t : rt->pending) {
+        float ms = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&ms, t.start, t.stop), "hipEventElapsedTime");
+        auto& tot = rt->totals[t.name];
+        tot.first += 1;
+        tot.second += ms;
+        rt->event_pool.push_back(t.start);
+        rt->event_pool.push_back(t.stop);
+    }
+    rt->pending.clear();
+    uint64_t c = 0;
+    double ms = 0.0;
+    for (auto& kv : rt->totals) {
+        if (name && kv.first != name) continue;
+        c += kv.second.first;
+        ms += kv.second.second;
+    }
+    if (count) *count = c;
+    if (total_ms) *total_ms = ms;
+    if (reset) rt->totals.clear();
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_stats(const MantaRocm* rt, MantaRocmStats* out) {
+    if (!rt || !out) return MANTA_ROCM_ERROR;
+    *out = rt->stats;
+    return MANTA_ROCM_OK;
+}
+
+// ------------------------------------------------------------ packing
+
+int manta_rocm_pack_q8_rows(const float* x, int64_t n, int64_t d, int8_t* codes, float* scales,
+                            char** err) {
+    if (n < 0 || d <= 0) return fail(err, MANTA_ROCM_ERROR, "pack_q8_rows: bad shape [%lld,%lld]",
+                                     (long long)n, (long long)d);
+    if (!x || !codes || !scales) return fail(err, MANTA_ROCM_ERROR, "pack_q8_rows: nil pointer");
+    parallel_rows(n, [&](int64_t a, int64_t b) {
+        for (int64_t r = a; r < b; r++) scales[r] = manta::pack_q8_row(x + r * d, d, codes + r * d);
+    });
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_pack_q4_blocks(const float* x, int64_t n, int64_t d, uint8_t* packed,
+                              uint16_t* scales, char** err) {
+    if (n < 0 || d <= 0 || d % 32 != 0)
+        return fail(err, MANTA_ROCM_ERROR,
+                    "pack_q4_blocks: d must be a positive multiple of 32 (got %lld)", (long long)d);
+    if (!x || !packed || !scales) return fail(err, MANTA_ROCM_ERROR, "pack_q4_blocks: nil pointer");
+    parallel_rows(n, [&](int64_t a, int64_t b) {
+        for (int64_t r = a; r < b; r++)
+            manta::pack_q4_row(x + r * d, d, packed + r * (d / 2), scales + r * (d / 32));
+    });
+    return MANTA_ROCM_OK;
+}
+
+// ------------------------------------------------------------- binding
+
+int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* scales, int64_t sets,
+                            int64_t n, int64_t d, MantaRocmCandidates** out, char** err) {
+    RT_CHECK(rt);
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil output");
+    *out = nullptr;
+    if (sets <= 0 || n <= 0 || d <= 0)
+        return fail(err, MANTA_ROCM_ERROR, "bind_q8_rows: bad shape [%lld,%lld,%lld]",
+                    (long long)sets, (long long)n, (long long)d);
+    if (d > kMaxDim)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "bind_q8_rows: d=%lld exceeds the device limit %lld",
+                    (long long)d, (long long)kMaxDim);
+    if (n >= ((int64_t)1 << 31))
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "bind_q8_rows: n=%lld exceeds int32 ids", (long long)n);
+    if (!codes || !scales) return fail(err, MANTA_ROCM_ERROR, "bind_q8_rows: nil pointer");
+    const int64_t rows = sets * n;
+    const int pitch = (int)align_up((size_t)d, 16);
+    std::vector<float> dnorm((size_t)rows), dd((size_t)rows);
+    parallel_rows(rows, [&](int64_t a, int64_t b) {
+        for (int64_t r = a; r < b; r++)
+            manta::q8_row_consts(codes + r * d, scales[r], d, &dnorm[(size_t)r], &dd[(size_t)r]);
+    });
+    auto* c = new MantaRocmCandidates();
+    c->rt = rt;
+    c->format = MANTA_ROCM_Q8_ROWS;
+    c->sets = sets;
+    c->n = n;
+    c->d = d;
+    c->pitch = pitch;
+    c->bytes = (size_t)rows * pitch + (size_t)rows * 12;
+    hipError_t e = hipMalloc(&c->codes, (size_t)rows * pitch);
+    if (e == hipSuccess) e = hipMalloc(&c->scales, (size_t)rows * 4);
+    if (e == hipSuccess) e = hipMalloc((void**)&c->dnorm, (size_t)rows * 4);
+    if (e == hipSuccess) e = hipMalloc((void**)&c->dd, (size_t)rows * 4);
+    if (e == hipSuccess) {
+        if (pitch == d) {
+            e = hipMemcpy(c->codes, codes, (size_t)rows * d, hipMemcpyHostToDevice);
+        } else {
+            std::vector<int8_t> tmp((size_t)rows * pitch, 0);
+            for (int64_t r = 0; r < rows; r++) std::memcpy(&tmp[(size_t)(r * pitch)], codes + r * d, (size_t)d);
+            e = hipMemcpy(c->codes, tmp.data(), tmp.size(), hipMemcpyHostToDevice);
+        }
+    }
+    if (e == hipSuccess) e = hipMemcpy(c->scales, scales, (size_t)rows * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(c->dnorm, dnorm.data(), (size_t)rows * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(c->dd, dd.data(), (size_t)rows * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        free_candidates_memory(c);
+        delete c;
+        return hip_fail(err, "bind_q8_rows", e);
+    }
+    rt->stats.bytes_uploaded += c->bytes;
+    rt->stats.candidate_bytes += c->bytes;
+    *out = c;
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16_t* scales,
+                              int64_t sets, int64_t n, int64_t d, MantaRocmCandidates** out,
+                              char** err) {
+    RT_CHECK(rt);
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil output");
+    *out = nullptr;
+    if (sets <= 0 || n <= 0 || d <= 0)
+        return fail(err, MANTA_ROCM_ERROR, "bind_q4_blocks: bad shape [%lld,%lld,%lld]",
+                    (long long)sets, (long long)n, (long long)d);
+    if (d % 32 != 0)
+        return fail(err, MANTA_ROCM_ERROR, "bind_q4_blocks: d must be a multiple of 32 (got %lld)",
+                    (long long)d);
+    if (d > kMaxDim)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "bind_q4_blocks: d=%lld exceeds the device limit %lld",
+                    (long long)d, (long long)kMaxDim);
+    if (n >= ((int64_t)1 << 31))
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "bind_q4_blocks: n=%lld exceeds int32 ids", (long long)n);
+    if (!packed || !scales) return fail(err, MANTA_ROCM_ERROR, "bind_q4_blocks: nil pointer");
+    const int64_t rows = sets * n;
+    const int pitch = (int)(d / 2);
+    const int nb = (int)(d / 32);
+    std::vector<float> dnorm((size_t)rows), dd((size_t)rows);
+    parallel_rows(rows, [&](int64_t a, int64_t b) {
+        for (int64_t r = a; r < b; r++)
+            manta::q4_row_consts(packed + r * pitch, scales + r * nb, d, &dnorm[(size_t)r], &dd[(size_t)r]);
+    });
+    auto* c = new MantaRocmCandidates();
+    c->rt = rt;
+    c->format = MANTA_ROCM_Q4_BLOCKS;
+    c->sets = sets;
+    c->n = n;
+    c->d = d;
+    c->pitch = pitch;
+    c->nb = nb;
+    c->bytes = (size_t)rows * (pitch + nb * 2 + 8);
+    hipError_t e = hipMalloc(&c->codes, (size_t)rows * pitch);
+    if (e == hipSuccess) e = hipMalloc(&c->scales, (size_t)rows * nb * 2);
+    if (e == hipSuccess) e = hipMalloc((void**)&c->dnorm, (size_t)rows * 4);
+    if (e == hipSuccess) e = hipMalloc((void**)&c->dd, (size_t)rows * 4);
+    if (e == hipSuccess) e = hipMemcpy(c->codes, packed, (size_t)rows * pitch, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(c->scales, scales, (size_t)rows * nb * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(c->dnorm, dnorm.data(), (size_t)rows * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(c->dd, dd.data(), (size_t)rows * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        free_candidates_memory(c);
+        delete c;
+        return hip_fail(err, "bind_q4_blocks", e);
+    }
+    rt->stats.bytes_uploaded += c->bytes;
+    rt->stats.candidate_bytes += c->bytes;
+    *out = c;
+    return MANTA_ROCM_OK;
+}
+
+void manta_rocm_unbind(MantaRocmCandidates* cands) {
+    if (!cands) return;
+    if (cands->rt) {
+        (void)hipSetDevice(cands->rt->device);
+        (void)hipStreamSynchronize(cands->rt->stream);
+        cands->rt->stats.candidate_bytes -= std::min<uint64_t>(cands->rt->stats.candidate_bytes, cands->bytes);
+    }
+    free_candidates_memory(cands);
+    delete cands;
+}
+
+int manta_rocm_candidates_info(const MantaRocmCandidates* c, int* format, int64_t* sets, int64_t* n,
+                               int64_t* d) {
+    if (!c) return MANTA_ROCM_ERROR;
+    if (format) *format = c->format;
+    if (sets) *sets = c->sets;
+    if (n) *n = c->n;
+    if (d) *d = c->d;
+    return MANTA_ROCM_OK;
+}
+
+// ------------------------------------------------------------- scoring
+
+namespace {
+
+struct QueryPlan {
+    int8_t* c8 = nullptr;
+    int8_t* hi = nullptr;
+    int8_t* lo = nullptr;
+    int8_t* phi = nullptr;  // q4 permuted digits
+    int8_t* plo = nullptr;
+    QConst* qc = nullptr;
+};
+
+// Workspace bytes for the query codes of nq queries.
+size_t query_bytes(const MantaRocmCandidates* c, int64_t nq) {
+    size_t per = (size_t)std::max<int64_t>(c->pitch, c->d);
+    return (size_t)nq * per * 5 + (size_t)nq * sizeof(QConst) + 6 * 256;
+}
+
+void carve_queries(Carver& cv, const MantaRocmCandidates* c, int64_t nq, QueryPlan& qp) {
+    size_t per = (size_t)std::max<int64_t>(c->pitch, c->d);
+    qp.c8 = cv.take<int8_t>((size_t)nq * per);
+    qp.hi = cv.take<int8_t>((size_t)nq * per);
+    qp.lo = cv.take<int8_t>((size_t)nq * per);
+    qp.phi = cv.take<int8_t>((size_t)nq * per);
+    qp.plo = cv.take<int8_t>((size_t)nq * per);
+    qp.qc = cv.take<QConst>((size_t)nq);
+}
+
+int encode_queries(MantaRocm* rt, const MantaRocmCandidates* c, int op, const uint16_t* q, int64_t nq,
+                   QueryPlan& qp, char** err) {
+    const bool e16 = !(c->format == MANTA_ROCM_Q8_ROWS && op == MANTA_ROCM_DOT);
+    if (c->format == MANTA_ROCM_Q8_ROWS) {
+        LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, c->pitch, e16 ? 1 : 0, qp.c8,
+                                              qp.hi, qp.lo, qp.qc, rt->stream),
+                   "query_encode");
+    } else {
+        LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, (int)c->d, 1, qp.c8, qp.hi,
+                                              qp.lo, qp.qc, rt->stream),
+                   "query_encode");
+        LAUNCH_TRY(manta::launch_q4_permute(qp.hi, qp.phi, (int)c->d, (int)nq, rt->stream),
+                   "q4_permute");
+        LAUNCH_TRY(manta::launch_q4_permute(qp.lo, qp.plo, (int)c->d, (int)nq, rt->stream),
+                   "q4_permute");
+    }
+    return MANTA_ROCM_OK;
+}
+
+ScanArgs scan_args(const MantaRocmCandidates* c, const QueryPlan& qp, int64_t nq) {
+    ScanArgs a{};
+    a.codes = (const int8_t*)c->codes;
+    a.scales = c->scales;
+    a.dnorm = c->dnorm;
+    a.dd = c->dd;
+    a.n = c->n;
+    a.pitch = c->pitch;
+    a.nb = c->nb;
+    a.set_stride = (c->sets == 1) ? 0 : c->n;
+    a.qc8 = qp.c8;
+    if (c->format == MANTA_ROCM_Q8_ROWS) {
+        a.qhi = qp.hi;
+        a.qlo = qp.lo;
+    } else {
+        a.qhi = qp.phi;
+        a.qlo = qp.plo;
+    }
+    a.qconst = qp.qc;
+    (void)nq;
+    return a;
+}
+
+int check_score_args(const MantaRocmCandidates* c, int op, const void* q, int64_t nq, char** err) {
+    if (!c) return fail(err, MANTA_ROCM_ERROR, "nil score input");
+    if (op < MANTA_ROCM_DOT || op > MANTA_ROCM_L2_DISTANCE)
+        return fail(err, MANTA_ROCM_ERROR, "unknown score op %d", op);
+    if (!q) return fail(err, MANTA_ROCM_ERROR, "nil score input");
+    if (nq <= 0) return fail(err, MANTA_ROCM_ERROR, "score expects at least one query");
+    if (c->sets != 1 && c->sets != nq)
+        return fail(err, MANTA_ROCM_ERROR, "score mismatch [%lld,%lld] x [%lld,%lld,%lld]", (long long)nq,
+                    (long long)c->d, (long long)c->sets, (long long)c->n, (long long)c->d);
+    if (nq > 65535) return fail(err, MANTA_ROCM_UNSUPPORTED, "more than 65535 queries in one call");
+    return MANTA_ROCM_OK;
+}
+
+int choose_rounds(int64_t tiles, int64_t nq) {
+    int64_t r = tiles * nq / 2048;
+    return (int)std::max<int64_t>(1, std::min<int64_t>(64, r));
+}
+
+int launch_scan(MantaRocm* rt, const MantaRocmCandidates* c, int op, const ScanArgs& a, dim3 grid,
+                size_t lds, char** err) {
+    if (c->format == MANTA_ROCM_Q8_ROWS)
+        LAUNCH_TRY(manta::launch_q8_scan(op, a, grid, lds, rt->stream), "q8_scan");
+    else
+        LAUNCH_TRY(manta::launch_q4_scan(op, a, grid, lds, rt->stream), "q4_scan");
+    return MANTA_ROCM_OK;
+}
+
+}  // namespace
+
+int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* c, int op, const uint16_t* q,
+                     int64_t nq, float* out, char** err) {
+    RT_CHECK(rt);
+    int rc = check_score_args(c, op, q, nq, err);
+    if (rc) return rc;
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil score output");
+    rc = ensure_workspace(rt, query_bytes(c, nq), err);
+    if (rc) return rc;
+    Carver cv(rt->ws);
+    QueryPlan qp;
+    carve_queries(cv, c, nq, qp);
+    rc = encode_queries(rt, c, op, q, nq, qp, err);
+    if (rc) return rc;
+    ScanArgs a = scan_args(c, qp, nq);
+    const int64_t tiles = (c->n + 255) / 256;
+    a.rounds = choose_rounds(tiles, nq);
+    a.out_scores = out;
+    const int64_t parts = (tiles + a.rounds - 1) / a.rounds;
+    return launch_scan(rt, c, op, a, dim3((unsigned)parts, (unsigned)nq), 0, err);
+}
+
+int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order,
+                          const uint16_t* q, int64_t nq, int64_t k, int32_t* out_ids,
+                          float* out_scores, int64_t* out_acc, char** err) {
+    RT_CHECK(rt);
+    int rc = check_score_args(c, op, q, nq, err);
+    if (rc) return rc;
+    if (order != MANTA_ROCM_LARGEST && order != MANTA_ROCM_SMALLEST)
+        return fail(err, MANTA_ROCM_ERROR, "unknown topk order %d", order);
+    if (k <= 0 || k > c->n)
+        return fail(err, MANTA_ROCM_ERROR, "topk limit %lld out of range for row width %lld",
+                    (long long)k, (long long)c->n);
+    if (k > kMaxDeviceK)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "topk limit %lld exceeds the device maximum %lld",
+                    (long long)k, (long long)kMaxDeviceK);
+    if (!out_ids) return fail(err, MANTA_ROCM_ERROR, "nil topk output");
+    if (out_acc && c->format != MANTA_ROCM_Q8_ROWS)
+        return fail(err, MANTA_ROCM_ERROR, "accumulator output needs q8 candidates");
+    const int64_t tiles = (c->n + 255) / 256;
+    const int rounds = choose_rounds(tiles, nq);
+    const int64_t parts = (tiles + rounds - 1) / rounds;
+    const int cap = cap_for_k(k);
+    size_t need = query_bytes(c, nq) + (size_t)nq * parts * k * 8 + 256;
+    rc = ensure_workspace(rt, need, err);
+    if (rc) return rc;
+    Carver cv(rt->ws);
+    QueryPlan qp;
+    carve_queries(cv, c, nq, qp);
+    uint64_t* partial = cv.take<uint64_t>((size_t)nq * parts * k);
+    rc = encode_queries(rt, c, op, q, nq, qp, err);
+    if (rc) return rc;
+    ScanArgs a = scan_args(c, qp, nq);
+    a.rounds = rounds;
+    a.partial = partial;
+    a.k = (int)k;
+    a.cap = cap;
+    a.smallest = order == MANTA_ROCM_SMALLEST;
+    rc = launch_scan(rt, c, op, a, dim3((unsigned)parts, (unsigned)nq), (size_t)cap * 8, err);
+    if (rc) return rc;
+    LAUNCH_TRY(manta::launch_topk_merge(partial, nq, parts * k, (int)k, cap, a.smallest, out_ids,
+                                        out_scores, rt->stream),
+               "topk_merge");
+    if (out_acc) {
+        const bool e16 = op != MANTA_ROCM_DOT;
+        LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch,
+                                            c->sets == 1 ? 0 : c->n, c->n, out_ids, (int)k, (int)nq,
+                                            e16 ? 1 : 0, qp.c8, qp.hi, qp.lo, out_acc, rt->stream),
+                   "q8_rescore");
+    }
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_topk(MantaRocm* rt, const float* scores, int64_t rows, int64_t cols, int64_t k,
+                    int order, int32_t* out_ids, float* out_values, char** err) {
+    RT_CHECK(rt);
+    if (!scores) return fail(err, MANTA_ROCM_ERROR, "nil topk input");
+    if (rows <= 0 || cols <= 0) return fail(err, MANTA_ROCM_ERROR, "topk expects rank-1 or rank-2 scores");
+    if (order != MANTA_ROCM_LARGEST && order != MANTA_ROCM_SMALLEST)
+        return fail(err, MANTA_ROCM_ERROR, "unknown topk order %d", order);
+    if (k <= 0 || k > cols) {
+        if (rows == 1)
+            return fail(err, MANTA_ROCM_ERROR, "topk limit %lld out of range for %lld scores",
+                        (long long)k, (long long)cols);
+        return fail(err, MANTA_ROCM_ERROR, "topk limit %lld out of range for row width %lld",
+                    (long long)k, (long long)cols);
+    }
+    if (k > kMaxDeviceK)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "topk limit %lld exceeds the device maximum %lld",
+                    (long long)k, (long long)kMaxDeviceK);
+    if (rows > 65535) return fail(err, MANTA_ROCM_UNSUPPORTED, "more than 65535 score rows");
+    if (!out_ids) return fail(err, MANTA_ROCM_ERROR, "nil topk output");
+    const int64_t tiles = (cols + 255) / 256;
+    int64_t want_parts = std::max<int64_t>(1, 1024 / rows);
+    int64_t rounds = std::max<int64_t>(1, (tiles + want_parts - 1) / want_parts);
+    rounds = std::min<int64_t>(rounds, std::max<int64_t>(1, tiles));
+    const int64_t seg = rounds * 256;
+    const int64_t parts = (cols + seg - 1) / seg;
+    const int cap = cap_for_k(k);
+    int rc = ensure_workspace(rt, (size_t)rows * parts * k * 8 + 256, err);
+    if (rc) return rc;
+    uint64_t* partial = (uint64_t*)rt->ws;
+    const int smallest = order == MANTA_ROCM_SMALLEST;
+    LAUNCH_TRY(manta::launch_topk_rows_partial(scores, rows, cols, seg, (int)parts, (int)k, cap,
+                                               smallest, partial, rt->stream),
+               "topk_partial");
+    LAUNCH_TRY(manta::launch_topk_merge(partial, rows, parts * k, (int)k, cap, smallest, out_ids,
+                                        out_values, rt->stream),
+               "topk_merge");
+    return MANTA_ROCM_OK;
+}
+
+// ------------------------------------------------------------ embed (pending)
+
+int manta_rocm_gather_rows_f16(MantaRocm* rt, const uint16_t*, int64_t, int64_t, const int32_t*,
+                               int64_t, uint16_t*, char** err) {
+    RT_CHECK(rt);
+    return fail(err, MANTA_ROCM_UNSUPPORTED, "gather: device path not built yet");
+}
+
+int manta_rocm_matmul_f16(MantaRocm* rt, const uint16_t*, int64_t, int64_t, const void*, int,
+                          const float*, int64_t, float*, char** err) {
+    RT_CHECK(rt);
+    return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: device path not built yet");
+}
+
+int manta_rocm_mean_pool_masked(MantaRocm* rt, const float*, const int32_t*, int64_t, int64_t,
+                                int64_t, float*, char** err) {
+    RT_CHECK(rt);
+    return fail(err, MANTA_ROCM_UNSUPPORTED, "mean_pool: device path not built yet");
+}
+
+int manta_rocm_normalize_rows(MantaRocm* rt, float*, int64_t, int64_t, char** err) {
+    RT_CHECK(rt);
+    return fail(err, MANTA_ROCM_UNSUPPORTED, "normalize: device path not built yet");
+}
+
+int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t*, const int32_t*, int64_t, int64_t,
+                            const uint16_t*, int64_t, int64_t, const void*, int, const float*,
+                            int64_t, uint16_t*, char** err) {
+    RT_CHECK(rt);
+    return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: device path not built yet");
+}
+
+}  // extern "C"

@@ -1,0 +1,279 @@
+"""Python face of the rocm backend (ctypes over libmanta_rocm.so).
+
+Mirrors the operator surface the reference's Go backend offers for the
+retrieval hot path (runtime/backend/tensor_ops.go: dotRows, cosineRows,
+l2DistanceRows, topKTensor, gatherTensor, matmulTensor,
+meanPoolMaskedTensor, normalizeRows) over packed q8/q4 candidates held in
+device memory.  All compute runs in the HIP library; this module only moves
+buffers and checks shapes.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+from ._lib import call, load
+
+DTYPES = {np.dtype(np.float32), np.dtype(np.uint16), np.dtype(np.int8), np.dtype(np.uint8),
+          np.dtype(np.int32), np.dtype(np.int64)}
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    call("manta_rocm_device_count", C.byref(n))
+    return n.value
+
+
+class DeviceArray:
+    """A device allocation with a numpy dtype and shape."""
+
+    def __init__(self, rt: "Runtime", shape, dtype):
+        self.rt = rt
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        ptr = C.c_void_p()
+        call("manta_rocm_malloc", rt.handle, C.byref(ptr), C.c_size_t(max(self.nbytes, 1)))
+        self.ptr = ptr
+
+    @property
+    def addr(self) -> int:
+        return int(self.ptr.value or 0)
+
+    def upload(self, host: np.ndarray) -> "DeviceArray":
+        host = np.ascontiguousarray(host, dtype=self.dtype)
+        if host.nbytes != self.nbytes:
+            raise ValueError("upload size mismatch: %d vs %d" % (host.nbytes, self.nbytes))
+        call("manta_rocm_upload", self.rt.handle, self.ptr, host.ctypes.data_as(C.c_void_p),
+             C.c_size_t(self.nbytes))
+        return self
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        call("manta_rocm_download", self.rt.handle, out.ctypes.data_as(C.c_void_p), self.ptr,
+             C.c_size_t(self.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr is not None and self.ptr.value:
+            call("manta_rocm_free", self.rt.handle, self.ptr)
+        self.ptr = C.c_void_p()
+
+    def __del__(self):  # best effort; explicit free() is preferred
+        try:
+            if self.ptr is not None and self.ptr.value and self.rt.handle:
+                self.free()
+        except Exception:
+            pass
+
+
+class Candidates:
+    """Device-resident packed candidate matrix ([sets, n, d])."""
+
+    def __init__(self, rt: "Runtime", handle: C.c_void_p, fmt: int, sets: int, n: int, d: int):
+        self.rt, self.handle, self.format = rt, handle, fmt
+        self.sets, self.n, self.d = sets, n, d
+
+    def close(self) -> None:
+        if self.handle is not None and self.handle.value:
+            load().manta_rocm_unbind(self.handle)
+        self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _ptr(a: Optional[DeviceArray]):
+    return a.ptr if a is not None else None
+
+
+class Runtime:
+    """One HIP device + stream (MantaRocm*)."""
+
+    def __init__(self, device: int = 0):
+        load()
+        h = C.c_void_p()
+        call("manta_rocm_create", C.c_int(device), C.byref(h))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle is not None and self.handle.value:
+            load().manta_rocm_destroy(self.handle)
+        self.handle = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ------------------------------------------------------------ memory
+    def empty(self, shape, dtype) -> DeviceArray:
+        return DeviceArray(self, shape, dtype)
+
+    def to_device(self, host: np.ndarray, dtype=None) -> DeviceArray:
+        host = np.ascontiguousarray(host, dtype=dtype or host.dtype)
+        return DeviceArray(self, host.shape, host.dtype).upload(host)
+
+    def synchronize(self) -> None:
+        call("manta_rocm_synchronize", self.handle)
+
+    def set_stream(self, stream_ptr: int) -> None:
+        call("manta_rocm_set_stream", self.handle, C.c_void_p(stream_ptr))
+
+    def set_timing(self, on: bool) -> None:
+        call("manta_rocm_set_timing", self.handle, C.c_int(1 if on else 0))
+
+    def timing(self, name=None, reset=False):
+        """(launch count, summed device ms) of one kernel family."""
+        cnt = C.c_uint64()
+        ms = C.c_double()
+        call("manta_rocm_timing", self.handle, name.encode() if name else None, C.byref(cnt),
+             C.byref(ms), C.c_int(1 if reset else 0))
+        return cnt.value, ms.value
+
+    def stats(self) -> dict:
+        s = _lib.Stats()
+        load().manta_rocm_stats(self.handle, C.byref(s))
+        return {f: getattr(s, f) for f, _ in _lib.Stats._fields_}
+
+    # ------------------------------------------------------------ binding
+    def bind_q8(self, codes: np.ndarray, scales: np.ndarray) -> Candidates:
+        """codes int8 [n,d] or [sets,n,d]; scales f32 [n] or [sets,n]."""
+        codes = np.ascontiguousarray(codes, dtype=np.int8)
+        scales = np.ascontiguousarray(scales, dtype=np.float32)
+        if codes.ndim == 2:
+            codes = codes[None]
+            scales = scales.reshape(1, -1)
+        sets, n, d = codes.shape
+        if scales.shape != (sets, n):
+            raise ValueError("q8 scales shape %s does not match codes %s" % (scales.shape, codes.shape))
+        h = C.c_void_p()
+        call("manta_rocm_bind_q8_rows", self.handle, codes.ctypes.data_as(C.c_void_p),
+             scales.ctypes.data_as(C.c_void_p), C.c_int64(sets), C.c_int64(n), C.c_int64(d),
+             C.byref(h))
+        return Candidates(self, h, _lib.Q8_ROWS, sets, n, d)
+
+    def bind_q4(self, packed: np.ndarray, scales: np.ndarray, d: int) -> Candidates:
+        """packed uint8 [n,d/2] or [sets,n,d/2]; scales f16 bits [n,d/32] or [sets,...]."""
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint16)
+        if packed.ndim == 2:
+            packed = packed[None]
+            scales = scales[None]
+        sets, n, half = packed.shape
+        if half * 2 != d or scales.shape != (sets, n, d // 32):
+            raise ValueError("q4 shapes do not match d=%d" % d)
+        h = C.c_void_p()
+        call("manta_rocm_bind_q4_blocks", self.handle, packed.ctypes.data_as(C.c_void_p),
+             scales.ctypes.data_as(C.c_void_p), C.c_int64(sets), C.c_int64(n), C.c_int64(d),
+             C.byref(h))
+        return Candidates(self, h, _lib.Q4_BLOCKS, sets, n, d)
+
+    # ------------------------------------------------------------ scoring
+    def score(self, cands: Candidates, op: str, queries: DeviceArray,
+              out: Optional[DeviceArray] = None) -> DeviceArray:
+        nq = queries.shape[0] if len(queries.shape) == 2 else 1
+        if out is None:
+            out = self.empty((nq, cands.n), np.float32)
+        call("manta_rocm_score", self.handle, cands.handle, C.c_int(_lib.OPS[op]), queries.ptr,
+             C.c_int64(nq), out.ptr)
+        return out
+
+    def score_topk(self, cands: Candidates, op: str, queries: DeviceArray, k: int,
+                   smallest: bool = False, with_scores: bool = True, with_acc: bool = False,
+                   out=None):
+        nq = queries.shape[0] if len(queries.shape) == 2 else 1
+        if out is None:
+            ids = self.empty((nq, k), np.int32)
+            sc = self.empty((nq, k), np.float32) if with_scores else None
+            acc = self.empty((nq, k), np.int64) if with_acc else None
+        else:
+            ids, sc, acc = out
+        call("manta_rocm_score_topk", self.handle, cands.handle, C.c_int(_lib.OPS[op]),
+             C.c_int(_lib.SMALLEST if smallest else _lib.LARGEST), queries.ptr, C.c_int64(nq),
+             C.c_int64(k), ids.ptr, _ptr(sc), _ptr(acc))
+        return ids, sc, acc
+
+    def topk(self, scores: DeviceArray, k: int, smallest: bool = False):
+        rows, cols = (1, scores.shape[0]) if len(scores.shape) == 1 else scores.shape
+        ids = self.empty((rows, k), np.int32)
+        vals = self.empty((rows, k), np.float32)
+        call("manta_rocm_topk", self.handle, scores.ptr, C.c_int64(rows), C.c_int64(cols),
+             C.c_int64(k), C.c_int(_lib.SMALLEST if smallest else _lib.LARGEST), ids.ptr, vals.ptr)
+        return ids, vals
+
+    # ------------------------------------------------------------ embed
+    def gather_rows_f16(self, table: DeviceArray, idx: DeviceArray) -> DeviceArray:
+        vocab, d = table.shape
+        nidx = int(np.prod(idx.shape))
+        out = self.empty((nidx, d), np.uint16)
+        call("manta_rocm_gather_rows_f16", self.handle, table.ptr, C.c_int64(vocab), C.c_int64(d),
+             idx.ptr, C.c_int64(nidx), out.ptr)
+        return out
+
+    def matmul_f16(self, lhs: DeviceArray, rhs: DeviceArray, col_scale: Optional[DeviceArray] = None
+                   ) -> DeviceArray:
+        m, k = lhs.shape
+        k2, n = rhs.shape
+        if k2 != k:
+            raise ValueError("matmul mismatch %s x %s" % (lhs.shape, rhs.shape))
+        kind = _lib.PROJ_Q8_COL if rhs.dtype == np.int8 else _lib.PROJ_F16
+        out = self.empty((m, n), np.float32)
+        call("manta_rocm_matmul_f16", self.handle, lhs.ptr, C.c_int64(m), C.c_int64(k), rhs.ptr,
+             C.c_int(kind), _ptr(col_scale), C.c_int64(n), out.ptr)
+        return out
+
+    def mean_pool_masked(self, x: DeviceArray, mask: DeviceArray) -> DeviceArray:
+        b, t, c = x.shape
+        out = self.empty((b, c), np.float32)
+        call("manta_rocm_mean_pool_masked", self.handle, x.ptr, mask.ptr, C.c_int64(b),
+             C.c_int64(t), C.c_int64(c), out.ptr)
+        return out
+
+    def normalize_rows(self, x: DeviceArray) -> DeviceArray:
+        rows, cols = x.shape[0] if len(x.shape) == 2 else x.shape[0] * x.shape[1], x.shape[-1]
+        call("manta_rocm_normalize_rows", self.handle, x.ptr, C.c_int64(rows), C.c_int64(cols))
+        return x
+
+    def embed_pooled(self, tokens: DeviceArray, mask: DeviceArray, table: DeviceArray,
+                     proj: DeviceArray, col_scale: Optional[DeviceArray] = None,
+                     out: Optional[DeviceArray] = None) -> DeviceArray:
+        b, t = tokens.shape
+        vocab, d = table.shape
+        d2, e = proj.shape
+        if d2 != d:
+            raise ValueError("matmul mismatch [%d,%d,%d] x %s" % (b, t, d, proj.shape))
+        kind = _lib.PROJ_Q8_COL if proj.dtype == np.int8 else _lib.PROJ_F16
+        if out is None:
+            out = self.empty((b, e), np.uint16)
+        call("manta_rocm_embed_pooled", self.handle, tokens.ptr, mask.ptr, C.c_int64(b),
+             C.c_int64(t), table.ptr, C.c_int64(vocab), C.c_int64(d), proj.ptr, C.c_int(kind),
+             _ptr(col_scale), C.c_int64(e), out.ptr)
+        return out
+
+
+def pack_q8_rows(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = x.shape
+    codes = np.empty((n, d), np.int8)
+    scales = np.empty((n,), np.float32)
+    call("manta_rocm_pack_q8_rows", x.ctypes.data_as(C.c_void_p), C.c_int64(n), C.c_int64(d),
+         codes.ctypes.data_as(C.c_void_p), scales.ctypes.data_as(C.c_void_p))
+    return codes, scales
+
+
+def pack_q4_blocks(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = x.shape
+    packed = np.empty((n, d // 2), np.uint8)
+    scales = np.empty((n, d // 32), np.uint16)
+    call("manta_rocm_pack_q4_blocks", x.ctypes.data_as(C.c_void_p), C.c_int64(n), C.c_int64(d),
+         packed.ctypes.data_as(C.c_void_p), scales.ctypes.data_as(C.c_void_p))
+    return packed, scales

@@ -1,0 +1,72 @@
+"""The C-ABI library loads on a CPU-only host and exports every entry point
+include/manta_rocm.h declares (no compute calls without a GPU)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from manta_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "manta_rocm.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(manta_rocm_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert "manta_rocm_score_topk" in syms and "manta_rocm_embed_pooled" in syms
+    assert len(syms) >= 25
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_python_signatures_cover_header():
+    assert set(declared_symbols()) == set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_device_count_without_gpu():
+    lib = _lib.load()
+    assert lib.manta_rocm_abi_version() == 1
+    n = C.c_int(-1)
+    err = C.c_char_p()
+    rc = lib.manta_rocm_device_count(C.byref(n), C.byref(err))
+    assert rc in (0, 1)
+    assert n.value >= 0
+
+
+def test_pack_entry_points_are_host_only_and_match_oracle():
+    import numpy as np
+    from manta_amd import rocm, synth
+    from oracle import oracle as orc
+
+    x = synth.normal_f32(5, 0, 257, 96, 1.0, normalize=True)
+    x[3] = 0.0
+    c8, s8 = rocm.pack_q8_rows(x)
+    oc8, os8 = orc.pack_q8_rows(x)
+    np.testing.assert_array_equal(c8, oc8)
+    np.testing.assert_array_equal(s8, os8)
+    p4, s4 = rocm.pack_q4_blocks(x)
+    op4, os4 = orc.pack_q4_blocks(x)
+    np.testing.assert_array_equal(p4, op4)
+    np.testing.assert_array_equal(s4, os4)
+    with pytest.raises(_lib.MantaRocmError, match="multiple of 32"):
+        rocm.pack_q4_blocks(x[:, :40])
+
+
+def test_create_without_device_reports_unsupported():
+    from manta_amd import rocm
+
+    if rocm.device_count() > 0:
+        pytest.skip("a device is present")
+    with pytest.raises(_lib.Unsupported, match="no ROCm device"):
+        rocm.Runtime(0)

@@ -1,0 +1,158 @@
+"""GPU parity of packed scoring and top-k against the CPU oracle.
+
+Bar: scores, ids and integer accumulators bit-exact with the oracle's
+restatement of the packed contract on identical seeded inputs; the
+reference's own tiny vectors within its 5e-4.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from manta_amd import synth
+from manta_amd._lib import MantaRocmError
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_known_answers.json")))
+
+
+def _q8_case(seed, nq, n, d, sets, normalize=True):
+    q = synth.normal_f16(100 + seed, 0, nq, d, 1.0, normalize=normalize)
+    codes = np.empty((sets, n, d), np.int8)
+    scales = np.empty((sets, n), np.float32)
+    for s in range(sets):
+        codes[s], scales[s] = synth.q8_rows(100 + seed, 1 + s, n, d, normalize=normalize)
+    return q, codes, scales
+
+
+def _oracle_codes(codes, sets):
+    return codes[0] if sets == 1 else codes
+
+
+def test_reference_runtime_vectors_on_device(rt):
+    for case in GOLD["score_runtime"]:
+        q = orc.f32_to_f16(np.asarray(case["q"], np.float32).reshape(1, -1))
+        docs = np.asarray(case["docs"], np.float32)
+        codes, scales = orc.pack_q8_rows(docs)
+        cands = rt.bind_q8(codes, scales)
+        qd = rt.to_device(q)
+        got = rt.score(cands, case["op"], qd).download()[0]
+        want = orc.score_q8(case["op"], q, codes, scales)[0]
+        np.testing.assert_array_equal(got, want)
+        if "want" in case:
+            np.testing.assert_allclose(got, case["want"], rtol=0, atol=5e-4)
+        else:
+            ids, sc, _ = rt.score_topk(cands, case["op"], qd, case["topk"])
+            np.testing.assert_array_equal(ids.download()[0], case["want_ids"])
+            np.testing.assert_allclose(sc.download()[0], case["want_scores"], rtol=0, atol=5e-4)
+        cands.close()
+
+
+@pytest.mark.parametrize("op", ["dot", "cosine", "l2_distance"])
+@pytest.mark.parametrize("d", [64, 128, 256, 384, 100, 48])
+def test_q8_score_matrix_bit_exact(rt, op, d):
+    nq, n = 3, 1000
+    q, codes, scales = _q8_case(d, nq, n, d, sets=1, normalize=(op != "l2_distance"))
+    cands = rt.bind_q8(codes[0], scales[0])
+    got = rt.score(cands, op, rt.to_device(q)).download()
+    want = orc.score_q8(op, q, codes[0], scales[0])
+    np.testing.assert_array_equal(got, want)
+    cands.close()
+
+
+@pytest.mark.parametrize("op,smallest", [("dot", False), ("cosine", False), ("l2_distance", True),
+                                         ("l2_distance", False), ("dot", True)])
+@pytest.mark.parametrize("sets", [1, 4])
+@pytest.mark.parametrize("n,k", [(1, 1), (300, 7), (4097, 10), (20000, 100)])
+def test_q8_score_topk_bit_exact(rt, op, smallest, sets, n, k):
+    nq, d = 4, 256
+    q, codes, scales = _q8_case(n + k, nq, n, d, sets)
+    cands = rt.bind_q8(codes[0] if sets == 1 else codes, scales[0] if sets == 1 else scales)
+    ids, sc, acc = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
+    ids, sc, acc = ids.download(), sc.download(), acc.download()
+    want_s, want_acc = orc.score_q8(op, q, _oracle_codes(codes, sets), scales[0] if sets == 1 else scales,
+                                    with_acc=True)
+    want_ids = orc.topk(want_s, k, smallest=smallest)
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_array_equal(sc, np.take_along_axis(want_s, want_ids, 1))
+    np.testing.assert_array_equal(acc, np.take_along_axis(want_acc, want_ids, 1))
+    cands.close()
+
+
+@pytest.mark.parametrize("op", ["dot", "cosine", "l2_distance"])
+@pytest.mark.parametrize("d", [32, 384])
+def test_q4_score_and_topk_bit_exact(rt, op, d):
+    nq, n, k = 3, 3000, 50
+    q = synth.normal_f16(7, 0, nq, d, 1.0, normalize=True)
+    packed, s4 = synth.q4_rows(7, 1, n, d, normalize=True)
+    cands = rt.bind_q4(packed, s4, d)
+    qd = rt.to_device(q)
+    got = rt.score(cands, op, qd).download()
+    want = orc.score_q4(op, q, packed, s4, d)
+    np.testing.assert_array_equal(got, want)
+    smallest = op == "l2_distance"
+    ids, sc, _ = rt.score_topk(cands, op, qd, k, smallest=smallest)
+    want_ids = orc.topk(want, k, smallest=smallest)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want, want_ids, 1))
+    cands.close()
+
+
+@pytest.mark.parametrize("rows,cols,k", [(1, 4, 3), (2, 3, 2), (1, 65536, 10), (3, 100000, 1000),
+                                         (7, 5000, 1), (2, 600, 600)])
+@pytest.mark.parametrize("smallest", [False, True])
+def test_topk_matrix_with_ties(rt, rows, cols, k, smallest):
+    rng = np.random.default_rng(rows * 7919 + cols + k)
+    # few distinct values -> many ties resolved by index; include -0.0 / +0.0
+    vals = rng.integers(-20, 20, size=(rows, cols)).astype(np.float32) / 8.0
+    vals[vals == 0] = np.where(rng.random((vals == 0).sum()) < 0.5, -0.0, 0.0)
+    ids, v = rt.topk(rt.to_device(vals), k, smallest=smallest)
+    want = orc.topk(vals, k, smallest=smallest)
+    np.testing.assert_array_equal(ids.download(), want)
+    np.testing.assert_array_equal(v.download(), np.take_along_axis(vals, want, 1))
+
+
+def test_reference_topk_vectors_on_device(rt):
+    for case in GOLD["topk"]:
+        s = np.asarray(case["scores"], np.float32)
+        s2 = s.reshape(1, -1) if s.ndim == 1 else s
+        ids, _ = rt.topk(rt.to_device(s2), case["k"])
+        np.testing.assert_array_equal(ids.download().reshape(np.shape(case["want"])), case["want"])
+
+
+def test_errors_match_reference(rt):
+    codes, scales = synth.q8_rows(1, 1, 10, 64, normalize=True)
+    cands = rt.bind_q8(codes, scales)
+    q = rt.to_device(synth.normal_f16(1, 0, 1, 64, 1.0, normalize=True))
+    with pytest.raises(MantaRocmError, match="topk limit 11 out of range for row width 10"):
+        rt.score_topk(cands, "dot", q, 11)
+    with pytest.raises(MantaRocmError, match="topk limit 0 out of range"):
+        rt.score_topk(cands, "dot", q, 0)
+    s = rt.to_device(np.zeros((1, 4), np.float32))
+    with pytest.raises(MantaRocmError, match="topk limit 5 out of range for 4 scores"):
+        rt.topk(s, 5)
+    per_query = rt.bind_q8(np.stack([codes, codes]), np.stack([scales, scales]))
+    q3 = rt.to_device(synth.normal_f16(1, 0, 3, 64, 1.0, normalize=True))
+    with pytest.raises(MantaRocmError, match="score mismatch"):
+        rt.score(per_query, "dot", q3)
+    cands.close()
+    per_query.close()
+
+
+@pytest.mark.slow
+def test_config0_full_size_bit_exact(rt):
+    """BASELINE config 0 at its full shape: ids, scores and int32
+    accumulators bit-exact with the oracle."""
+    q, codes, scales = synth.config0()
+    cands = rt.bind_q8(codes[0], scales[0])
+    ids, sc, acc = rt.score_topk(cands, "dot", rt.to_device(q), 10, with_acc=True)
+    want_s, want_acc = orc.score_q8("dot", q, codes[0], scales[0], with_acc=True)
+    want_ids = orc.topk(want_s, 10)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    np.testing.assert_array_equal(acc.download(), np.take_along_axis(want_acc, want_ids, 1))
+    assert np.all(np.abs(acc.download()) < 2 ** 31)
+    cands.close()
