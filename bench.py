@@ -64,6 +64,22 @@ def cpu_baseline(codes, scales, queries, budget_s: float) -> dict:
     }
 
 
+def copy_calibration(mib: int) -> int:
+    """A plain copy kernel of known size: under rocprofv3 --pmc its
+    FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters (bytes read =
+    bytes written = mib MiB per launch)."""
+    import torch
+
+    n = mib * 1024 * 1024 // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": n * 4, "launches": 10}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -72,7 +88,11 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=32, help="C0 problems per step")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (PMC scaling run)")
     args = ap.parse_args()
+    if args.copy_calibration_mb:
+        return copy_calibration(args.copy_calibration_mb)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (candidate rows "
               "would shard across GPUs with a KB-scale top-k merge; see DESIGN.md). "

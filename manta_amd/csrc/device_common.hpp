@@ -44,7 +44,9 @@ __device__ __forceinline__ float fmul_rn(float a, float b) { return __fmul_rn(a,
 __device__ __forceinline__ float fadd_rn(float a, float b) { return __fadd_rn(a, b); }
 __device__ __forceinline__ float fsub_rn(float a, float b) { return __fsub_rn(a, b); }
 __device__ __forceinline__ float fdiv_rn(float a, float b) { return __fdiv_rn(a, b); }
-__device__ __forceinline__ float fsqrt_rn(float a) { return __fsqrt_rn(a); }
+// __fsqrt_rn lowers to the bare v_sqrt_f32 (about 1 ulp); llvm.sqrt.f32 with
+// -fhip-fp32-correctly-rounded-divide-sqrt is the correctly rounded sequence.
+__device__ __forceinline__ float fsqrt_rn(float a) { return __builtin_sqrtf(a); }
 
 // Order-preserving map float -> u32 with -0 folded onto +0 (the reference
 // compares with <, >, so -0 and +0 tie and fall through to the index).
