@@ -64,6 +64,19 @@ def cpu_baseline(codes, scales, queries, budget_s: float) -> dict:
     }
 
 
+def profiled_traffic(name: str):
+    """HBM bytes per launch measured by rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE,
+    copy-kernel calibrated) and recorded in the committed profile summary."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def copy_calibration(mib: int) -> int:
     """A plain copy kernel of known size: under rocprofv3 --pmc its
     FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters (bytes read =
@@ -173,7 +186,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": profiled_traffic("q8_scan_c0_batched.md") if args.sets == 32 else None,
+            "traffic_source": "profiles/q8_scan_c0_batched.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
             "avg_launch_us": scan_avg_s * 1e6,
             "bytes_per_launch": bytes_per_launch,
         },
