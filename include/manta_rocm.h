@@ -187,8 +187,9 @@ int manta_rocm_topk(MantaRocm* rt, const float* scores_dev, int64_t rows, int64_
 /* ---- embed pipeline ---------------------------------------------------- */
 
 /* gatherTensor, f16 table [vocab, d] x int32 indices [nidx] -> f16
- * [nidx, d] (tensor_ops.go:794-877).  An out-of-range index is reported as
- * "gather index %d out of range" (the first offending position's value). */
+ * [nidx, d] (tensor_ops.go:794-877).  An out-of-range index leaves a zero
+ * row and is reported by the next synchronizing call as "gather index %d out
+ * of range". */
 int manta_rocm_gather_rows_f16(MantaRocm* rt, const uint16_t* table_dev, int64_t vocab, int64_t d,
                                const int32_t* idx_dev, int64_t nidx, uint16_t* out_dev,
                                char** err);
@@ -212,7 +213,12 @@ int manta_rocm_normalize_rows(MantaRocm* rt, float* x_dev, int64_t rows, int64_t
 
 /* The whole embed entry point in one fused launch sequence:
  * gather(table, tokens) -> @matmul(proj) -> mean_pool(mask) -> normalize,
- * f16 output [b, e].  The [b,t,e] intermediate never reaches HBM.  Takes over
+ * f16 output [b, e].  mask_dev may be NULL (every position valid).  Token
+ * ids are checked at every position, masked or not, like gatherTensor; an
+ * out-of-range id is reported by the next synchronizing call
+ * (manta_rocm_synchronize / manta_rocm_download) as
+ * "gather index %d out of range".  Requires d % 8 == 0, e even (e % 4 for a
+ * q8 projection) and e <= 4096, else MANTA_ROCM_UNSUPPORTED.  The [b,t,e] intermediate never reaches HBM.  Takes over
  * the host gather + cuBLAS + host mean_pool chain of
  * EmbeddingModel.EmbedBatch (runtime/embedding_model.go:422; stack in
  * tensor_ops.go:31-47, native_linux.go:3608-3670, tensor_ops.go:1210). */

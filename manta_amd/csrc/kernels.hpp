@@ -42,6 +42,35 @@ hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride,
                              const int32_t* ids, int k, int nq, int e16, const int8_t* qc8,
                              const int8_t* qhi, const int8_t* qlo, int64_t* out, hipStream_t s);
 
+// Arguments of the embed GEMM kernels (kernels_embed.hip).
+struct EmbedArgs {
+    const int32_t* tokens;      // [batches*T] (pooled) or [M] (gathered matmul)
+    const int32_t* mask;        // [batches*T] or nullptr (all positions valid)
+    const void* table;          // f16 [vocab][K]
+    int64_t vocab;
+    const void* A;              // plain f16 lhs [M][K]
+    int64_t M;                  // rows of a plain / gathered matmul
+    int64_t T;                  // positions per sequence (pooled)
+    int64_t batches;            // sequences (pooled)
+    int tiles_per_seq;          // ceil(T / 64)
+    int K;
+    int N;
+    const void* B;              // f16 [K][N] or int8 [K][N]
+    const float* colscale;      // [N] for int8 B
+    float* Y;                   // f32 [M][N] (matmul)
+    float* P;                   // f32 [batches][tiles_per_seq][N] (pooled partial sums)
+    unsigned long long* err;    // first out-of-range gather index
+};
+
+hipError_t launch_embed_gemm(const EmbedArgs& a, bool gather, bool q8b, bool pool, hipStream_t s);
+hipError_t launch_embed_finalize(const float* P, int tiles, const int32_t* mask, int64_t B, int64_t T,
+                                 int N, uint16_t* out, hipStream_t s);
+hipError_t launch_gather_rows_f16(const uint16_t* table, int64_t vocab, int64_t d, const int32_t* idx,
+                                  int64_t nidx, uint16_t* out, unsigned long long* err, hipStream_t s);
+hipError_t launch_mean_pool_masked(const float* x, const int32_t* mask, int64_t B, int64_t T, int64_t C,
+                                   float* out, hipStream_t s);
+hipError_t launch_normalize_rows(float* x, int64_t rows, int64_t cols, hipStream_t s);
+
 hipError_t launch_topk_rows_partial(const float* scores, int64_t rows, int64_t cols, int64_t seg,
                                     int parts, int k, int cap, int smallest, uint64_t* partial,
                                     hipStream_t s);

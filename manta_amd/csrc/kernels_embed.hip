@@ -1,0 +1,341 @@
+// kernels_embed.hip -- the embed pipeline on gfx950:
+//   gather(table, tokens) -> @matmul(proj) -> masked mean_pool -> normalize
+// (reference steps: gatherTensor tensor_ops.go:751-979, matmulTensor
+// :981-1062, meanPoolMaskedTensor :1210-1275, normalizeRows :1114-1138).
+//
+// GEMM core: 64 x 128 output tile per workgroup (4 waves, each 32 x 64 =
+// two 32x32 MFMA tiles), K staged through LDS in chunks of 64 with
+// v_mfma_f32_32x32x16_f16 (f32 accumulate).  The A tile is either a plain
+// f16 matrix or rows gathered straight from the embedding table by token id
+// (the [B,T,D] gather never reaches HBM).  The projection chunk is written
+// to LDS transposed (n-major, k contiguous) so both MFMA operands are single
+// 16-byte LDS reads; a q8 projection is widened int8 -> f16 exactly and its
+// per-column scale applied in the epilogue.  In pooled mode the epilogue
+// sums the masked rows of its tile per column and writes one partial per
+// (sequence, row tile); a finalize kernel adds the partials in a fixed
+// order, divides by the count and L2-normalizes.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace manta {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int EM = 64;       // rows per tile
+constexpr int EN = 128;      // columns per tile
+constexpr int EK = 64;       // K per LDS chunk
+constexpr int LDA = EK + 8;  // halfs per LDS row (pad against bank conflicts)
+constexpr int LDB = EK + 8;
+
+// Records the first out-of-range gather index (flag bit 32 | index).
+__device__ __forceinline__ void report_bad_index(unsigned long long* err, int idx) {
+    if (err) atomicCAS(err, 0ull, (1ull << 32) | (unsigned long long)(uint32_t)idx);
+}
+
+template <bool GATHER, bool Q8B, bool POOL>
+__global__ __launch_bounds__(256) void embed_gemm_kernel(EmbedArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[EM * LDA];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[EN * LDB];
+    __shared__ float red[2][EN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;  // 32-row half of the tile
+    const int wn = wave & 1;   // 64-column half of the tile
+    const int n0 = blockIdx.y * EN;
+
+    // Row tile -> (sequence, first position) in pooled/gather mode, else m0.
+    int64_t seq = 0, t0 = 0, m0 = 0;
+    if (POOL) {
+        seq = blockIdx.x / a.tiles_per_seq;
+        t0 = (int64_t)(blockIdx.x % a.tiles_per_seq) * EM;
+    } else {
+        m0 = (int64_t)blockIdx.x * EM;
+    }
+
+    // Each thread stages two 16-byte A segments per chunk: rows r0 and r0+32.
+    const int seg_col = tid & 7;  // 16-byte column within the 128-byte chunk row
+    const int r0 = tid >> 3;      // 0..31
+    const _Float16* arow[2];
+    bool arow_live[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int r = r0 + h * 32;
+        arow[h] = nullptr;
+        arow_live[h] = false;
+        if (POOL) {
+            const int64_t t = t0 + r;
+            if (t < a.T) {
+                const int64_t pos = seq * a.T + t;
+                int idx = a.tokens[pos];
+                if (idx < 0 || idx >= a.vocab) {
+                    report_bad_index(a.err, idx);
+                } else if (!a.mask || a.mask[pos] != 0) {
+                    arow[h] = (const _Float16*)a.table + (int64_t)idx * a.K;
+                    arow_live[h] = true;
+                }
+            }
+        } else {
+            const int64_t m = m0 + r;
+            if (m < a.M) {
+                if (GATHER) {
+                    int idx = a.tokens[m];
+                    if (idx < 0 || idx >= a.vocab) {
+                        report_bad_index(a.err, idx);
+                    } else {
+                        arow[h] = (const _Float16*)a.table + (int64_t)idx * a.K;
+                        arow_live[h] = true;
+                    }
+                } else {
+                    arow[h] = (const _Float16*)a.A + m * a.K;
+                    arow_live[h] = true;
+                }
+            }
+        }
+    }
+
+    f16v acc[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+
+    for (int k0 = 0; k0 < a.K; k0 += EK) {
+        // ---- stage A: 64 rows x 64 k
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int k = k0 + seg_col * 8;
+            h8 v = (h8)(_Float16)0.0f;
+            if (arow_live[h] && k < a.K) v = *(const h8*)(arow[h] + k);
+            *(h8*)&As[(r0 + h * 32) * LDA + seg_col * 8] = v;
+        }
+        // ---- stage B transposed: Bs[n][k]
+        if (!Q8B) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int u = tid + 256 * j;
+                const int kg = u >> 6;   // 0..7: k group of 8
+                const int np = u & 63;   // pair of columns
+                const int n = n0 + 2 * np;
+                h8 c0, c1;
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++) {
+                    const int k = k0 + kg * 8 + kk;
+                    uint32_t w = 0;
+                    if (k < a.K && n < a.N) w = *(const uint32_t*)((const uint16_t*)a.B + (int64_t)k * a.N + n);
+                    c0[kk] = __builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+                    c1[kk] = __builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+                }
+                *(h8*)&Bs[(2 * np) * LDB + kg * 8] = c0;
+                *(h8*)&Bs[(2 * np + 1) * LDB + kg * 8] = c1;
+            }
+        } else {
+            const int kg = tid >> 5;  // 0..7
+            const int nq = tid & 31;  // quad of columns
+            const int n = n0 + 4 * nq;
+            h8 c[4];
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+                const int k = k0 + kg * 8 + kk;
+                uint32_t w = 0;
+                if (k < a.K && n < a.N) w = *(const uint32_t*)((const int8_t*)a.B + (int64_t)k * a.N + n);
+#pragma unroll
+                for (int q = 0; q < 4; q++) c[q][kk] = (_Float16)(int)(int8_t)((w >> (8 * q)) & 0xFF);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) *(h8*)&Bs[(4 * nq + q) * LDB + kg * 8] = c[q];
+        }
+        __syncthreads();
+        // ---- 4 MFMA k-steps of 16
+#pragma unroll
+        for (int s = 0; s < EK / 16; s++) {
+            const int kofs = s * 16 + (lane >> 5) * 8;
+            h8 av = *(const h8*)&As[(wm * 32 + (lane & 31)) * LDA + kofs];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                h8 bv = *(const h8*)&Bs[(wn * 64 + t * 32 + (lane & 31)) * LDB + kofs];
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[t], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    // Output element (tile t, acc r): row 8*(r/4) + 4*(lane/32) + r%4 of the
+    // wave's 32 rows, column lane%32 of the tile.
+    if (!POOL) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int n = n0 + wn * 64 + t * 32 + (lane & 31);
+            if (n >= a.N) continue;
+            const float cs = Q8B ? a.colscale[n] : 1.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < a.M) a.Y[m * a.N + n] = Q8B ? acc[t][r] * cs : acc[t][r];
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int64_t tt = t0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            bool live = tt < a.T && (!a.mask || a.mask[seq * a.T + tt] != 0);
+            if (live) s += acc[t][r];
+        }
+        s += __shfl_xor(s, 32);
+        if (lane < 32) red[wm][wn * 64 + t * 32 + lane] = s;
+    }
+    __syncthreads();
+    if (tid < EN) {
+        const int n = n0 + tid;
+        if (n < a.N) {
+            float v = red[0][tid] + red[1][tid];
+            if (Q8B) v *= a.colscale[n];
+            a.P[((int64_t)seq * a.tiles_per_seq + (blockIdx.x % a.tiles_per_seq)) * a.N + n] = v;
+        }
+    }
+}
+
+// Sum the row-tile partials of one sequence in order, divide by the number
+// of unmasked positions (count 0 -> zeros), L2-normalize (f64 sum of
+// squares, f32 norm, zero norm leaves the row unchanged) and round to f16.
+__global__ __launch_bounds__(256) void embed_finalize_kernel(const float* __restrict__ P, int tiles,
+                                                             const int32_t* __restrict__ mask,
+                                                             int64_t T, int N, uint16_t* __restrict__ out) {
+    __shared__ float row[4096];
+    __shared__ double red[256];
+    __shared__ int cnt_red[256];
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x;
+    int cnt = 0;
+    for (int64_t t = tid; t < T; t += 256) cnt += (!mask || mask[b * T + t] != 0) ? 1 : 0;
+    cnt_red[tid] = cnt;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (tid < s) cnt_red[tid] += cnt_red[tid + s];
+        __syncthreads();
+    }
+    const int count = cnt_red[0];
+    const float inv = count ? 1.0f / (float)count : 0.0f;
+    double ss = 0.0;
+    for (int c = tid; c < N; c += 256) {
+        float v = 0.0f;
+        for (int s = 0; s < tiles; s++) v += P[(b * tiles + s) * N + c];
+        v = count ? v * inv : 0.0f;
+        row[c] = v;
+        ss += (double)v * (double)v;
+    }
+    red[tid] = ss;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (tid < s) red[tid] += red[tid + s];
+        __syncthreads();
+    }
+    const float norm = (float)__builtin_sqrt(red[0]);
+    for (int c = tid; c < N; c += 256) {
+        float v = row[c];
+        if (norm != 0.0f) v = v / norm;
+        out[b * N + c] = f2h(v);
+    }
+}
+
+// gatherTensor rank-2 table x indices: one 16-byte (or 2-byte tail) copy per
+// thread; an out-of-range index leaves a zero row and is reported.
+__global__ void gather_rows_f16_kernel(const uint16_t* __restrict__ table, int64_t vocab, int64_t d,
+                                       const int32_t* __restrict__ idx, int64_t nidx,
+                                       uint16_t* __restrict__ out, unsigned long long* err) {
+    const int64_t row = blockIdx.x;
+    const int id = idx[row];
+    const bool ok = id >= 0 && id < vocab;
+    if (!ok && threadIdx.x == 0) report_bad_index(err, id);
+    for (int64_t c = threadIdx.x; c < d; c += blockDim.x)
+        out[row * d + c] = ok ? table[(int64_t)id * d + c] : (uint16_t)0;
+}
+
+// meanPoolMaskedTensor rank 3: one thread per (b, c), positions summed in
+// order, then multiplied by 1/float(count) -- the reference's exact order.
+__global__ void mean_pool_masked_kernel(const float* __restrict__ x, const int32_t* __restrict__ mask,
+                                        int64_t B, int64_t T, int64_t C, float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B * C) return;
+    const int64_t b = i / C, c = i % C;
+    float s = 0.0f;
+    int64_t count = 0;
+    for (int64_t t = 0; t < T; t++) {
+        if (mask[b * T + t] == 0) continue;
+        count++;
+        s += x[(b * T + t) * C + c];
+    }
+    if (count) s *= 1.0f / (float)count;
+    out[i] = count ? s : 0.0f;
+}
+
+// normalizeRows: one thread per row, f64 sum of squares in column order,
+// f32 norm, f32 division; zero rows unchanged -- the reference's order.
+__global__ void normalize_rows_kernel(float* __restrict__ x, int64_t rows, int64_t cols) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    float* p = x + r * cols;
+    double s = 0.0;
+    for (int64_t c = 0; c < cols; c++) {
+        double v = (double)p[c];
+        s = __dadd_rn(s, __dmul_rn(v, v));
+    }
+    const float norm = (float)__builtin_sqrt(s);
+    if (norm == 0.0f) return;
+    for (int64_t c = 0; c < cols; c++) p[c] = fdiv_rn(p[c], norm);
+}
+
+// ----------------------------------------------------------------- hosts
+
+hipError_t launch_embed_gemm(const EmbedArgs& a, bool gather, bool q8b, bool pool, hipStream_t s) {
+    const int64_t rows_tiles = pool ? a.batches * a.tiles_per_seq : (a.M + EM - 1) / EM;
+    dim3 grid((unsigned)rows_tiles, (unsigned)((a.N + EN - 1) / EN));
+#define MANTA_EG(G, Q, P) \
+    if (gather == G && q8b == Q && pool == P) { \
+        hipLaunchKernelGGL((embed_gemm_kernel<G, Q, P>), grid, dim3(256), 0, s, a); \
+        return hipGetLastError(); \
+    }
+    MANTA_EG(true, false, true)
+    MANTA_EG(true, true, true)
+    MANTA_EG(false, false, false)
+    MANTA_EG(false, true, false)
+    MANTA_EG(true, false, false)
+    MANTA_EG(true, true, false)
+#undef MANTA_EG
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_embed_finalize(const float* P, int tiles, const int32_t* mask, int64_t B, int64_t T,
+                                 int N, uint16_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(embed_finalize_kernel, dim3((unsigned)B), dim3(256), 0, s, P, tiles, mask, T, N, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_rows_f16(const uint16_t* table, int64_t vocab, int64_t d, const int32_t* idx,
+                                  int64_t nidx, uint16_t* out, unsigned long long* err, hipStream_t s) {
+    hipLaunchKernelGGL(gather_rows_f16_kernel, dim3((unsigned)nidx), dim3(128), 0, s, table, vocab, d, idx,
+                       nidx, out, err);
+    return hipGetLastError();
+}
+
+hipError_t launch_mean_pool_masked(const float* x, const int32_t* mask, int64_t B, int64_t T, int64_t C,
+                                   float* out, hipStream_t s) {
+    const int64_t total = B * C;
+    hipLaunchKernelGGL(mean_pool_masked_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x,
+                       mask, B, T, C, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_normalize_rows(float* x, int64_t rows, int64_t cols, hipStream_t s) {
+    hipLaunchKernelGGL(normalize_rows_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, x, rows,
+                       cols);
+    return hipGetLastError();
+}
+
+}  // namespace manta

@@ -41,6 +41,9 @@ struct MantaRocm {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     MantaRocmStats stats{};
+    // first out-of-range gather index seen by a device gather (flag | index)
+    unsigned long long* err_word = nullptr;
+    bool gather_pending = false;
     // per-kernel-family timing (manta_rocm_set_timing)
     bool timing = false;
     std::vector<TimedLaunch> pending;
@@ -194,6 +197,24 @@ int set_device(MantaRocm* rt, char** err) {
     return MANTA_ROCM_OK;
 }
 
+// Device gathers record their first out-of-range index instead of faulting;
+// the next synchronizing call reports it with gatherTensor's wording
+// (tensor_ops.go:804-806) and clears it.
+int check_gather_error(MantaRocm* rt, char** err) {
+    if (!rt->gather_pending) return MANTA_ROCM_OK;
+    rt->gather_pending = false;
+    unsigned long long w = 0;
+    HIP_TRY(hipMemcpyAsync(&w, rt->err_word, sizeof(w), hipMemcpyDeviceToHost, rt->stream),
+            "hipMemcpy(error word)");
+    HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    if (w == 0) return MANTA_ROCM_OK;
+    const unsigned long long zero = 0;
+    HIP_TRY(hipMemcpyAsync(rt->err_word, &zero, sizeof(zero), hipMemcpyHostToDevice, rt->stream),
+            "hipMemcpy(error word)");
+    HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    return fail(err, MANTA_ROCM_ERROR, "gather index %d out of range", (int)(uint32_t)(w & 0xFFFFFFFFull));
+}
+
 #define RT_CHECK(rt)                                                          \
     do {                                                                      \
         if (!(rt)) return fail(err, MANTA_ROCM_ERROR, "nil rocm runtime");    \
@@ -259,6 +280,13 @@ int manta_rocm_create(int device, MantaRocm** out, char** err) {
         return hip_fail(err, "hipStreamCreate", e);
     }
     rt->stream = rt->own_stream;
+    e = hipMalloc((void**)&rt->err_word, sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMemset(rt->err_word, 0, sizeof(unsigned long long));
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(rt->own_stream);
+        delete rt;
+        return hip_fail(err, "hipMalloc(error word)", e);
+    }
     *out = rt;
     return MANTA_ROCM_OK;
 }
@@ -273,6 +301,7 @@ void manta_rocm_destroy(MantaRocm* rt) {
     }
     for (auto e : rt->event_pool) (void)hipEventDestroy(e);
     if (rt->ws) (void)hipFree(rt->ws);
+    if (rt->err_word) (void)hipFree(rt->err_word);
     if (rt->own_stream) (void)hipStreamDestroy(rt->own_stream);
     delete rt;
 }
@@ -287,7 +316,7 @@ int manta_rocm_set_stream(MantaRocm* rt, void* hip_stream, char** err) {
 int manta_rocm_synchronize(MantaRocm* rt, char** err) {
     RT_CHECK(rt);
     HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
-    return MANTA_ROCM_OK;
+    return check_gather_error(rt, err);
 }
 
 int manta_rocm_malloc(MantaRocm* rt, void** out_dev, size_t bytes, char** err) {
@@ -325,7 +354,7 @@ int manta_rocm_download(MantaRocm* rt, void* dst, const void* src_dev, size_t by
             "hipMemcpyDtoH");
     HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
     rt->stats.bytes_downloaded += bytes;
-    return MANTA_ROCM_OK;
+    return check_gather_error(rt, err);
 }
 
 int manta_rocm_set_timing(MantaRocm* rt, int on, char** err) {
@@ -737,36 +766,116 @@ int manta_rocm_topk(MantaRocm* rt, const float* scores, int64_t rows, int64_t co
     return MANTA_ROCM_OK;
 }
 
-// ------------------------------------------------------------ embed (pending)
+// ---------------------------------------------------------------- embed
 
-int manta_rocm_gather_rows_f16(MantaRocm* rt, const uint16_t*, int64_t, int64_t, const int32_t*,
-                               int64_t, uint16_t*, char** err) {
-    RT_CHECK(rt);
-    return fail(err, MANTA_ROCM_UNSUPPORTED, "gather: device path not built yet");
+namespace {
+
+int check_proj(int proj_kind, const void* proj, const float* col_scale, int64_t k, int64_t n, char** err) {
+    if (!proj) return fail(err, MANTA_ROCM_ERROR, "nil matmul input");
+    if (proj_kind != MANTA_ROCM_PROJ_F16 && proj_kind != MANTA_ROCM_PROJ_Q8_COL)
+        return fail(err, MANTA_ROCM_ERROR, "unknown projection kind %d", proj_kind);
+    if (proj_kind == MANTA_ROCM_PROJ_Q8_COL && !col_scale)
+        return fail(err, MANTA_ROCM_ERROR, "q8 projection needs per-column scales");
+    if (k <= 0 || n <= 0) return fail(err, MANTA_ROCM_ERROR, "matmul mismatch: empty operand");
+    if (k % 8 != 0)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: inner dimension %lld is not a multiple of 8",
+                    (long long)k);
+    if (n % (proj_kind == MANTA_ROCM_PROJ_Q8_COL ? 4 : 2) != 0)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: output width %lld not supported", (long long)n);
+    if (n > 4096 || k > (1 << 20))
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: shape beyond the device path");
+    return MANTA_ROCM_OK;
 }
 
-int manta_rocm_matmul_f16(MantaRocm* rt, const uint16_t*, int64_t, int64_t, const void*, int,
-                          const float*, int64_t, float*, char** err) {
+}  // namespace
+
+int manta_rocm_gather_rows_f16(MantaRocm* rt, const uint16_t* table, int64_t vocab, int64_t d,
+                               const int32_t* idx, int64_t nidx, uint16_t* out, char** err) {
     RT_CHECK(rt);
-    return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: device path not built yet");
+    if (!table || !idx || !out) return fail(err, MANTA_ROCM_ERROR, "nil gather input");
+    if (vocab <= 0 || d <= 0 || nidx <= 0)
+        return fail(err, MANTA_ROCM_ERROR, "gather expects i32 indices");
+    if (nidx > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "gather: too many indices");
+    LAUNCH_TRY(manta::launch_gather_rows_f16(table, vocab, d, idx, nidx, out, rt->err_word, rt->stream),
+               "gather");
+    rt->gather_pending = true;
+    return MANTA_ROCM_OK;
 }
 
-int manta_rocm_mean_pool_masked(MantaRocm* rt, const float*, const int32_t*, int64_t, int64_t,
-                                int64_t, float*, char** err) {
+int manta_rocm_matmul_f16(MantaRocm* rt, const uint16_t* lhs, int64_t m, int64_t k, const void* rhs,
+                          int proj_kind, const float* col_scale, int64_t n, float* out, char** err) {
     RT_CHECK(rt);
-    return fail(err, MANTA_ROCM_UNSUPPORTED, "mean_pool: device path not built yet");
+    if (!lhs || !out) return fail(err, MANTA_ROCM_ERROR, "nil matmul input");
+    if (m <= 0) return fail(err, MANTA_ROCM_ERROR, "matmul mismatch: empty operand");
+    int rc = check_proj(proj_kind, rhs, col_scale, k, n, err);
+    if (rc) return rc;
+    if ((m + 63) / 64 > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: too many rows");
+    manta::EmbedArgs a{};
+    a.A = lhs;
+    a.M = m;
+    a.K = (int)k;
+    a.N = (int)n;
+    a.B = rhs;
+    a.colscale = col_scale;
+    a.Y = out;
+    LAUNCH_TRY(manta::launch_embed_gemm(a, false, proj_kind == MANTA_ROCM_PROJ_Q8_COL, false, rt->stream),
+               "matmul");
+    return MANTA_ROCM_OK;
 }
 
-int manta_rocm_normalize_rows(MantaRocm* rt, float*, int64_t, int64_t, char** err) {
+int manta_rocm_mean_pool_masked(MantaRocm* rt, const float* x, const int32_t* mask, int64_t b,
+                                int64_t t, int64_t c, float* out, char** err) {
     RT_CHECK(rt);
-    return fail(err, MANTA_ROCM_UNSUPPORTED, "normalize: device path not built yet");
+    if (!x) return fail(err, MANTA_ROCM_ERROR, "nil mean_pool input");
+    if (!mask) return fail(err, MANTA_ROCM_ERROR, "nil mean_pool mask");
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil mean_pool output");
+    if (b <= 0 || t <= 0 || c <= 0) return fail(err, MANTA_ROCM_ERROR, "mean_pool expects rank-2 or rank-3 tensor input");
+    LAUNCH_TRY(manta::launch_mean_pool_masked(x, mask, b, t, c, out, rt->stream), "mean_pool");
+    return MANTA_ROCM_OK;
 }
 
-int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t*, const int32_t*, int64_t, int64_t,
-                            const uint16_t*, int64_t, int64_t, const void*, int, const float*,
-                            int64_t, uint16_t*, char** err) {
+int manta_rocm_normalize_rows(MantaRocm* rt, float* x, int64_t rows, int64_t cols, char** err) {
     RT_CHECK(rt);
-    return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: device path not built yet");
+    if (!x) return fail(err, MANTA_ROCM_ERROR, "nil normalize input");
+    if (rows <= 0 || cols <= 0) return MANTA_ROCM_OK;
+    LAUNCH_TRY(manta::launch_normalize_rows(x, rows, cols, rt->stream), "normalize");
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t* mask, int64_t b,
+                            int64_t t, const uint16_t* table, int64_t vocab, int64_t d, const void* proj,
+                            int proj_kind, const float* col_scale, int64_t e, uint16_t* out, char** err) {
+    RT_CHECK(rt);
+    if (!tokens || !table || !out) return fail(err, MANTA_ROCM_ERROR, "nil embed input");
+    if (b <= 0 || t <= 0 || vocab <= 0)
+        return fail(err, MANTA_ROCM_ERROR, "embed: bad shape [%lld,%lld] x [%lld,%lld]", (long long)b,
+                    (long long)t, (long long)vocab, (long long)d);
+    int rc = check_proj(proj_kind, proj, col_scale, d, e, err);
+    if (rc) return rc;
+    const int64_t tiles = (t + 63) / 64;
+    if (b * tiles > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: batch too large");
+    rc = ensure_workspace(rt, (size_t)(b * tiles * e) * sizeof(float) + 256, err);
+    if (rc) return rc;
+    manta::EmbedArgs a{};
+    a.tokens = tokens;
+    a.mask = mask;
+    a.table = table;
+    a.vocab = vocab;
+    a.T = t;
+    a.batches = b;
+    a.tiles_per_seq = (int)tiles;
+    a.K = (int)d;
+    a.N = (int)e;
+    a.B = proj;
+    a.colscale = col_scale;
+    a.P = (float*)rt->ws;
+    a.err = rt->err_word;
+    LAUNCH_TRY(manta::launch_embed_gemm(a, true, proj_kind == MANTA_ROCM_PROJ_Q8_COL, true, rt->stream),
+               "embed");
+    LAUNCH_TRY(manta::launch_embed_finalize(a.P, (int)tiles, mask, b, t, (int)e, out, rt->stream),
+               "embed_finalize");
+    rt->gather_pending = true;
+    return MANTA_ROCM_OK;
 }
 
 }  // extern "C"
