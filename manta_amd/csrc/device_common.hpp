@@ -145,20 +145,125 @@ __device__ __forceinline__ void topk_offer(uint64_t key, uint64_t tau, uint64_t*
     }
 }
 
-// Keep the best k of the reservoir (sorted, descending, in keys[0..)).
-// Must be called by the whole workgroup after a barrier.
+constexpr int kMaxCap = 4096;  // largest reservoir (keys per thread <= kMaxCap / 256)
+
+// Scratch of the block radix select.
+struct SelectShared {
+    int hist[256];
+    int digit;
+    int above;
+    int wpos;
+    int pad;
+    uint64_t minkey;
+};
+
+// Keep the best k of the reservoir: a radix select over the 64-bit keys
+// (8-bit digits, most significant first) finds the prefix shared by the k-th
+// largest key; the keys at or above it -- exactly k, keys being distinct --
+// are moved to keys[0..k) in no particular order and tau becomes the
+// smallest of them.  Whole workgroup (blockDim.x == 256), after a barrier.
 __device__ inline void topk_compact(uint64_t* keys, TopKShared* st, int k) {
-    int c = st->cnt;
-    int S = next_pow2(c < 2 ? 2 : c);
-    for (int i = c + (int)threadIdx.x; i < S; i += blockDim.x) keys[i] = 0;
-    __syncthreads();
-    block_sort_desc(keys, S);
-    if (threadIdx.x == 0) {
-        int m = c < k ? c : k;
-        st->cnt = m;
-        st->tau = (m == k) ? keys[k - 1] : 0ull;
+    __shared__ SelectShared ss;
+    const int tid = threadIdx.x;
+    const int c = st->cnt;
+    if (c <= k) {
+        // nothing to drop; tau stays 0 unless exactly k keys are held
+        if (tid == 0) ss.minkey = ~0ull;
+        __syncthreads();
+        if (c == k) {
+            for (int i = tid; i < c; i += 256) atomicMin(&ss.minkey, keys[i]);
+        }
+        __syncthreads();
+        if (tid == 0) st->tau = (c == k) ? ss.minkey : 0ull;
+        __syncthreads();
+        return;
+    }
+    uint64_t prefix = 0, pmask = 0;
+    int remaining = k;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        for (int i = tid; i < 256; i += 256) ss.hist[i] = 0;
+        __syncthreads();
+        for (int i = tid; i < c; i += 256) {
+            const uint64_t key = keys[i];
+            if ((key & pmask) == prefix) atomicAdd(&ss.hist[(int)((key >> shift) & 0xFF)], 1);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            // lane l owns digits 255-4l .. 252-4l (descending)
+            int h[4];
+            int sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                h[j] = ss.hist[255 - 4 * tid - j];
+                sum += h[j];
+            }
+            int incl = sum;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                int t = __shfl_up(incl, off);
+                if (tid >= off) incl += t;
+            }
+            int cum = incl - sum;  // keys with a larger digit
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (cum < remaining && cum + h[j] >= remaining) {
+                    ss.digit = 255 - 4 * tid - j;
+                    ss.above = cum;
+                }
+                cum += h[j];
+            }
+        }
+        __syncthreads();
+        const int d = ss.digit;
+        remaining -= ss.above;
+        prefix |= (uint64_t)d << shift;
+        pmask |= 0xFFull << shift;
+        const bool all_in = ss.hist[d] == remaining;
+        __syncthreads();
+        if (all_in) break;  // every key with this prefix is kept
+    }
+    // compact: keys whose masked prefix is >= prefix (exactly k of them).
+    // All reads finish (barrier) before the first write.
+    uint64_t v[kMaxCap / 256];
+    uint32_t keep = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxCap / 256; j++) {
+        const int i = tid + 256 * j;
+        v[j] = 0;
+        if (i < c) {
+            v[j] = keys[i];
+            if ((v[j] & pmask) >= prefix) keep |= 1u << j;
+        }
+    }
+    if (tid == 0) {
+        ss.wpos = 0;
+        ss.minkey = ~0ull;
     }
     __syncthreads();
+    uint64_t lo = ~0ull;
+#pragma unroll
+    for (int j = 0; j < kMaxCap / 256; j++) {
+        if (keep & (1u << j)) {
+            const int pos = atomicAdd(&ss.wpos, 1);
+            keys[pos] = v[j];
+            lo = v[j] < lo ? v[j] : lo;
+        }
+    }
+    if (keep) atomicMin(&ss.minkey, lo);
+    __syncthreads();
+    if (tid == 0) {
+        st->cnt = k;
+        st->tau = ss.minkey;
+    }
+    __syncthreads();
+}
+
+// Sort keys[0..n) descending (n <= kMaxCap), zero-padding to a power of two.
+__device__ inline void topk_sort(uint64_t* keys, int n) {
+    const int S = next_pow2(n < 2 ? 2 : n);
+    for (int i = n + (int)threadIdx.x; i < S; i += blockDim.x) keys[i] = 0;
+    __syncthreads();
+    block_sort_desc(keys, S);
 }
 
 // Compact when another round of blockDim.x offers might not fit.

@@ -56,8 +56,10 @@ __global__ __launch_bounds__(256) void topk_merge_kernel(const uint64_t* __restr
         topk_maybe_compact(keys, &st, k, cap);
     }
     topk_compact(keys, &st, k);
+    const int kept = st.cnt;
+    topk_sort(keys, kept);
     for (int i = threadIdx.x; i < k; i += blockDim.x) {
-        uint64_t key = i < st.cnt ? keys[i] : 0ull;
+        uint64_t key = i < kept ? keys[i] : 0ull;
         ids[row * k + i] = key ? (int32_t)key_index(key) : -1;
         if (values) values[row * k + i] = key ? key_score(key, smallest) : 0.0f;
     }

@@ -67,7 +67,7 @@ struct MantaRocmCandidates {
 namespace {
 
 constexpr int64_t kMaxDim = 1024;     // exactness bound of the int32 / f32 accumulators
-constexpr int64_t kMaxDeviceK = 2048;  // reservoir capacity bound (LDS)
+constexpr int64_t kMaxDeviceK = 2048;  // reservoir capacity bound (LDS, cap <= 4096)
 
 char* dup_printf(const char* fmt, va_list ap) {
     va_list ap2;
