@@ -146,6 +146,7 @@ __device__ __forceinline__ void topk_offer(uint64_t key, uint64_t tau, uint64_t*
 }
 
 constexpr int kMaxCap = 4096;  // largest reservoir (keys per thread <= kMaxCap / 256)
+static_assert(kMaxCap == 4096, "reservoir bound shared with kernels.hpp");
 
 // Scratch of the block radix select.
 struct SelectShared {

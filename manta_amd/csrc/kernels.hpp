@@ -11,36 +11,41 @@ enum { OP_DOT = 0, OP_COSINE = 1, OP_L2 = 2 };
 
 struct QConst;
 
+constexpr int kMaxQueryDim = 1024;  // longest query / row the device path takes
+constexpr int kMaxCapKeys = 4096;   // largest LDS key reservoir (32 KB)
+
 // Arguments of the streaming scan kernels (one query per blockIdx.y).
 struct ScanArgs {
-    const int8_t* codes;   // q8: [sets][n][pitch] int8; q4: [sets][n][pitch] packed bytes
-    const void* scales;    // q8: f32 [sets][n]; q4: f16 [sets][n][nb]
-    const float* dnorm;    // [sets][n]
-    const float* dd;       // [sets][n]
+    const int8_t* codes;      // q8: [sets][n][pitch] int8; q4: [sets][n][pitch] packed bytes
+    const void* scales;       // q8: f32 [sets][n]; q4: f16 [sets][n][nb]
+    const float* dnorm;       // [sets][n]
+    const float* dd;          // [sets][n]
     int64_t n;
-    int pitch;             // bytes per row
-    int nb;                // q4 blocks per row
-    int64_t set_stride;    // rows between consecutive queries' sets (0: shared)
-    const int8_t* qc8;     // E8 codes [nq][pitch]
-    const int8_t* qhi;     // E16 high digits (q4: permuted, [nq][d])
-    const int8_t* qlo;     // E16 low digits
-    const QConst* qconst;  // [nq]
-    int rounds;            // rounds of 256 rows per workgroup
-    float* out_scores;     // score-matrix mode, else nullptr
-    uint64_t* partial;     // top-k mode: [nq][gridDim.x][k]
+    int pitch;                // bytes per row
+    int nb;                   // q4 blocks per row
+    int d;                    // query length
+    int64_t set_stride;       // rows between consecutive queries' sets (0: shared)
+    const uint16_t* queries;  // f16 [nq][d]
+    int rounds;               // rounds of 256 rows per workgroup
+    float* out_scores;        // score-matrix mode, else nullptr
+    uint64_t* partial;        // top-k mode: [nq][gridDim.x][k]
+    uint32_t* tickets;        // [nq], zero between calls
+    int32_t* out_ids;         // [nq][k]
+    float* out_topk_scores;   // [nq][k] or nullptr
     int k;
-    int cap;               // reservoir capacity (power of two, >= k + 256)
+    int cap;                  // reservoir capacity (power of two, >= k + 256)
+    int lds_keys;             // keys the dynamic LDS holds (>= cap; merge fast path)
+    int mid_compact;          // 0: cap >= k + rounds*256, no compaction between rounds
     int smallest;
 };
 
 hipError_t launch_query_encode(const uint16_t* q, int nq, int d, int pitch, int e16, int8_t* c8,
                                int8_t* hi, int8_t* lo, QConst* qc, hipStream_t s);
-hipError_t launch_q4_permute(const int8_t* src, int8_t* dst, int d, int nq, hipStream_t s);
 hipError_t launch_q8_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s);
 hipError_t launch_q4_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s);
-hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride, int64_t n,
-                             const int32_t* ids, int k, int nq, int e16, const int8_t* qc8,
-                             const int8_t* qhi, const int8_t* qlo, int64_t* out, hipStream_t s);
+hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride, int64_t n, int d,
+                             const uint16_t* queries, const int32_t* ids, int k, int nq, int e16,
+                             int64_t* out, hipStream_t s);
 
 // Arguments of the embed GEMM kernels (kernels_embed.hip).
 struct EmbedArgs {

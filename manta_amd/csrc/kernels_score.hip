@@ -1,15 +1,16 @@
 // kernels_score.hip -- packed-candidate scoring for gfx950 (streaming path).
 //
-// One workgroup (256 threads, 4 waves) scores 256 candidate rows per round
-// against one query.  q8 rows are read with coalesced 16-byte loads: L lanes
+// One launch per fused score+top-k call.  Each workgroup (256 threads, 4
+// waves) encodes its query into LDS, then scores `rounds` x 256 candidate
+// rows against it.  q8 rows are read with coalesced 16-byte loads: L lanes
 // cover one row (L*16 contiguous bytes per load), C loads per lane per row,
 // so a wave moves 64*16 bytes per load instruction.  The int8 products run
-// on v_dot4_i32_i8 with the query codes held in registers; row sums are
-// reduced across the L lanes with xor shuffles and then transposed so that
-// thread t owns row t of the round.  The epilogue computes the exact f32
-// score of the packed contract and either stores it (score matrix) or feeds
-// the workgroup top-k reservoir (fused top-k; only k keys per workgroup
-// reach HBM).
+// on v_dot4 with the query codes held in registers; row sums are reduced
+// across the L lanes with xor shuffles and then transposed so that thread t
+// owns row t of the round.  The epilogue computes the exact f32 score of the
+// packed contract and either stores it (score matrix) or feeds the LDS top-k
+// reservoir.  In top-k mode each workgroup writes its k best keys; the last
+// workgroup of a query (atomic ticket) merges them into the final ids.
 //
 // Score formulas (the CPU oracle restates them; reference semantics they
 // stand in for: dotRows / cosineRows / l2DistanceRows,
@@ -25,75 +26,108 @@
 
 namespace manta {
 
-
 // ------------------------------------------------------------ query codes
 
-// One workgroup per query.  E8 (q8 dot): qmax = max(1, maxabs), code =
-// clamp(round((q*127)/qmax)).  E16: code = clamp(round(q*(32639/maxabs))),
-// split as code = 256*hi + lo with lo the signed low byte.  Padding columns
-// [d, pitch) get code 0.
-__global__ __launch_bounds__(256) void query_encode_kernel(
-    const uint16_t* __restrict__ q, int d, int pitch, int e16, int8_t* __restrict__ c8,
-    int8_t* __restrict__ hi, int8_t* __restrict__ lo, QConst* __restrict__ qc) {
-    __shared__ float red_f[256];
-    __shared__ long long red_i[256];
-    const int qi = blockIdx.x;
+// E8 (q8 dot): qmax = max(1, maxabs), code = clamp(round((q*127)/qmax)).
+__device__ __forceinline__ int code_e8(float x, float qmax) {
+    float r = round_half_away(fdiv_rn(fmul_rn(x, 127.0f), qmax));
+    return (int)fminf(127.0f, fmaxf(-127.0f, r));
+}
+
+// E16: code = clamp(round(q*(32639/maxabs)), +-32639), split 256*hi + lo
+// with lo the signed low byte.
+__device__ __forceinline__ int code_e16(float x, float inv) {
+    float r = round_half_away(fmul_rn(x, inv));
+    return (int)fminf(32639.0f, fmaxf(-32639.0f, r));
+}
+
+__device__ __forceinline__ QConst e16_consts(float maxabs, long long ss) {
+    QConst k{0.0f, 0.0f, 0.0f, 0.0f};
+    if (maxabs != 0.0f) {
+        const float qs = fdiv_rn(maxabs, 32639.0f);
+        const double dss = (double)ss;
+        k.a = qs;
+        k.b = (float)__dmul_rn(__dsqrt_rn(dss), (double)qs);
+        k.c = (float)__dmul_rn(__dmul_rn(dss, (double)qs), (double)qs);
+    }
+    return k;
+}
+
+// q4 digit planes are permuted per 8 columns to [c0 c2 c4 c6 c1 c3 c5 c7]
+// so that the nibble unpack below feeds v_dot4 without shuffling.
+__device__ __forceinline__ int q4_perm_pos(int c) {
+    const int j = c & 7;
+    return (c & ~7) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
+}
+
+enum { ENC_E8 = 0, ENC_E16 = 1, ENC_E16_Q4 = 2 };
+
+struct QueryLds {
+    int8_t c8[kMaxQueryDim];
+    int8_t hi[kMaxQueryDim];
+    int8_t lo[kMaxQueryDim];
+    QConst qc;
+    float redf[4];
+    long long redi[4];
+};
+
+// Encode one f16 query into LDS (whole workgroup, 256 threads).  `span` is
+// the number of code slots to fill (the row pitch; columns >= d get 0).
+__device__ inline void encode_query_block(const uint16_t* __restrict__ qrow, int d, int span, int enc,
+                                          QueryLds& L) {
     const int tid = threadIdx.x;
-    const uint16_t* qrow = q + (int64_t)qi * d;
+    const int lane = tid & 63, wave = tid >> 6;
     float m = 0.0f;
     for (int c = tid; c < d; c += 256) m = fmaxf(m, __builtin_fabsf(h2f(qrow[c])));
-    red_f[tid] = m;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) L.redf[wave] = m;
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) red_f[tid] = fmaxf(red_f[tid], red_f[tid + s]);
-        __syncthreads();
-    }
-    const float maxabs = red_f[0];
-    if (!e16) {
+    const float maxabs = fmaxf(fmaxf(L.redf[0], L.redf[1]), fmaxf(L.redf[2], L.redf[3]));
+    if (enc == ENC_E8) {
         const float qmax = fmaxf(1.0f, maxabs);
-        for (int c = tid; c < pitch; c += 256) {
-            float r = 0.0f;
-            if (c < d) {
-                r = round_half_away(fdiv_rn(fmul_rn(h2f(qrow[c]), 127.0f), qmax));
-                r = fminf(127.0f, fmaxf(-127.0f, r));
-            }
-            c8[(int64_t)qi * pitch + c] = (int8_t)(int)r;
-        }
-        if (tid == 0) qc[qi] = QConst{qmax, 0.0f, 0.0f, 0.0f};
+        for (int c = tid; c < span; c += 256) L.c8[c] = (int8_t)(c < d ? code_e8(h2f(qrow[c]), qmax) : 0);
+        if (tid == 0) L.qc = QConst{qmax, 0.0f, 0.0f, 0.0f};
+        __syncthreads();
         return;
     }
-    long long ss = 0;
     const float inv = maxabs == 0.0f ? 0.0f : fdiv_rn(32639.0f, maxabs);
-    for (int c = tid; c < pitch; c += 256) {
-        int code = 0;
-        if (c < d && maxabs != 0.0f) {
-            float r = round_half_away(fmul_rn(h2f(qrow[c]), inv));
-            r = fminf(32639.0f, fmaxf(-32639.0f, r));
-            code = (int)r;
-        }
-        int l = (int)(int8_t)(code & 0xFF);
-        int h = (code - l) >> 8;
-        hi[(int64_t)qi * pitch + c] = (int8_t)h;
-        lo[(int64_t)qi * pitch + c] = (int8_t)l;
+    long long ss = 0;
+    for (int c = tid; c < span; c += 256) {
+        const int code = (c < d && maxabs != 0.0f) ? code_e16(h2f(qrow[c]), inv) : 0;
+        const int l = (int)(int8_t)(code & 0xFF);
+        const int h = (code - l) >> 8;
+        const int pos = enc == ENC_E16_Q4 ? q4_perm_pos(c) : c;
+        L.hi[pos] = (int8_t)h;
+        L.lo[pos] = (int8_t)l;
         ss += (long long)code * code;
     }
-    red_i[tid] = ss;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) L.redi[wave] = ss;
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) red_i[tid] += red_i[tid + s];
-        __syncthreads();
-    }
-    if (tid == 0) {
-        QConst k{0.0f, 0.0f, 0.0f, 0.0f};
-        if (maxabs != 0.0f) {
-            float qs = fdiv_rn(maxabs, 32639.0f);
-            double dss = (double)red_i[0];
-            k.a = qs;
-            k.b = (float)__dmul_rn(__dsqrt_rn(dss), (double)qs);
-            k.c = (float)__dmul_rn(__dmul_rn(dss, (double)qs), (double)qs);
+    if (tid == 0) L.qc = e16_consts(maxabs, L.redi[0] + L.redi[1] + L.redi[2] + L.redi[3]);
+    __syncthreads();
+}
+
+// Global-memory variant: one workgroup per query (used by the batched
+// paths, whose many workgroups share each query).
+__global__ __launch_bounds__(256) void query_encode_kernel(const uint16_t* __restrict__ q, int d, int pitch,
+                                                           int e16, int8_t* __restrict__ c8,
+                                                           int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                           QConst* __restrict__ qc) {
+    __shared__ QueryLds L;
+    const int qi = blockIdx.x;
+    encode_query_block(q + (int64_t)qi * d, d, pitch, e16 ? ENC_E16 : ENC_E8, L);
+    for (int c = threadIdx.x; c < pitch; c += 256) {
+        if (e16) {
+            hi[(int64_t)qi * pitch + c] = L.hi[c];
+            lo[(int64_t)qi * pitch + c] = L.lo[c];
+        } else {
+            c8[(int64_t)qi * pitch + c] = L.c8[c];
         }
-        qc[qi] = k;
     }
+    if (threadIdx.x == 0) qc[qi] = L.qc;
 }
 
 // ----------------------------------------------------------- epilogues
@@ -141,7 +175,15 @@ __device__ __forceinline__ int dot16(v4i a, v4i b, int acc) {
     return acc;
 }
 
-// Common tail of a round: store the score, or offer it to the reservoir.
+// ------------------------------------------------------- top-k plumbing
+
+struct ScanLds {
+    QueryLds q;
+    TopKShared st;
+    int last;
+};
+
+// Store the score, or offer it to the reservoir.
 __device__ __forceinline__ void emit_round(float score, bool valid, int64_t row, int64_t n, int qi,
                                            float* __restrict__ out_scores, uint64_t* keys,
                                            TopKShared* st, uint64_t tau, int smallest) {
@@ -153,14 +195,66 @@ __device__ __forceinline__ void emit_round(float score, bool valid, int64_t row,
     topk_offer(key, tau, keys, st);
 }
 
-
+// End of a top-k scan workgroup: publish its k best keys; the last
+// workgroup of the query (ticket == gridDim.x - 1) merges every part into
+// the final sorted ids / scores and resets the ticket for the next call.
+// Publication avoids device-wide fences (each one writes back and
+// invalidates a whole XCD L2): the keys are stored write-through at agent
+// scope (sc1), every thread waits for its stores to complete before the
+// barrier, the ticket is an agent-scope atomic, and the merging workgroup
+// reads the parts with agent-scope (sc1) loads.
+__device__ inline void finish_topk(const ScanArgs& a, uint64_t* keys, ScanLds& S, int qi) {
+    __syncthreads();
+    topk_compact(keys, &S.st, a.k);
+    const int64_t per_q = (int64_t)gridDim.x * a.k;
+    uint64_t* dst = a.partial + (int64_t)qi * per_q + (int64_t)blockIdx.x * a.k;
+    for (int i = threadIdx.x; i < a.k; i += blockDim.x)
+        __hip_atomic_store(dst + i, i < S.st.cnt ? keys[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        S.last = __hip_atomic_fetch_add(&a.tickets[qi], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 gridDim.x - 1;
+    __syncthreads();
+    if (!S.last) return;
+    const uint64_t* src = a.partial + (int64_t)qi * per_q;
+    topk_init(keys, &S.st);
+    if (per_q <= a.lds_keys) {
+        // every part fits in LDS: one batch of loads, empty slots dropped
+        for (int64_t base = 0; base < per_q; base += blockDim.x) {
+            const int64_t i = base + threadIdx.x;
+            const uint64_t key =
+                i < per_q ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+            topk_offer(key, 0ull, keys, &S.st);
+        }
+        __syncthreads();
+    } else {
+        for (int64_t base = 0; base < per_q; base += blockDim.x) {
+            const int64_t i = base + threadIdx.x;
+            const uint64_t key =
+                i < per_q ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+            topk_offer(key, S.st.tau, keys, &S.st);
+            __syncthreads();
+            topk_maybe_compact(keys, &S.st, a.k, a.cap);
+        }
+    }
+    topk_compact(keys, &S.st, a.k);
+    const int kept = S.st.cnt;
+    topk_sort(keys, kept);
+    for (int i = threadIdx.x; i < a.k; i += blockDim.x) {
+        const uint64_t key = i < kept ? keys[i] : 0ull;
+        a.out_ids[(int64_t)qi * a.k + i] = key ? (int32_t)key_index(key) : -1;
+        if (a.out_topk_scores) a.out_topk_scores[(int64_t)qi * a.k + i] = key ? key_score(key, a.smallest) : 0.0f;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[qi], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // -------------------------------------------------- q8, coalesced lanes
 
 template <int OP, int L, int C>
 __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
     extern __shared__ uint64_t topk_keys[];
-    __shared__ TopKShared st;
+    __shared__ ScanLds S;
     constexpr int G = 64 / L;  // rows per wave per load step
     const int qi = blockIdx.y;
     const int lane = threadIdx.x & 63;
@@ -170,21 +264,22 @@ __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
     const int64_t set_row0 = (int64_t)qi * a.set_stride;
     const int8_t* __restrict__ codes = a.codes + set_row0 * a.pitch;
     const float* __restrict__ scales = (const float*)a.scales + set_row0;
-    const QConst kq = a.qconst[qi];
 
+    encode_query_block(a.queries + (int64_t)qi * a.d, a.d, a.pitch, OP == OP_DOT ? ENC_E8 : ENC_E16, S.q);
+    const QConst kq = S.q.qc;
     v4i qa[C], qb[C];
 #pragma unroll
     for (int c = 0; c < C; c++) {
         const int off = c * 16 * L + p * 16;
         if (OP == OP_DOT) {
-            qa[c] = *(const v4i*)(a.qc8 + (int64_t)qi * a.pitch + off);
+            qa[c] = *(const v4i*)(S.q.c8 + off);
             qb[c] = qa[c];
         } else {
-            qa[c] = *(const v4i*)(a.qhi + (int64_t)qi * a.pitch + off);
-            qb[c] = *(const v4i*)(a.qlo + (int64_t)qi * a.pitch + off);
+            qa[c] = *(const v4i*)(S.q.hi + off);
+            qb[c] = *(const v4i*)(S.q.lo + off);
         }
     }
-    if (!a.out_scores) topk_init(topk_keys, &st);
+    if (!a.out_scores) topk_init(topk_keys, &S.st);
 
     const int64_t wg_row0 = (int64_t)blockIdx.x * a.rounds * 256;
     for (int r = 0; r < a.rounds; r++) {
@@ -233,18 +328,14 @@ __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
             if (OP == OP_L2) d2 = a.dd[set_row0 + row];
             score = q8_epilogue<OP>(my_hi, my_lo, scales[row], kq, dn, d2);
         }
-        uint64_t tau = a.out_scores ? 0ull : st.tau;
-        emit_round(score, valid, row, a.n, qi, a.out_scores, topk_keys, &st, tau, a.smallest);
-        if (!a.out_scores) {
+        const uint64_t tau = a.out_scores ? 0ull : S.st.tau;
+        emit_round(score, valid, row, a.n, qi, a.out_scores, topk_keys, &S.st, tau, a.smallest);
+        if (!a.out_scores && a.mid_compact) {
             __syncthreads();
-            topk_maybe_compact(topk_keys, &st, a.k, a.cap);
+            topk_maybe_compact(topk_keys, &S.st, a.k, a.cap);
         }
     }
-    if (!a.out_scores) {
-        topk_compact(topk_keys, &st, a.k);
-        uint64_t* dst = a.partial + ((int64_t)qi * gridDim.x + blockIdx.x) * a.k;
-        for (int i = threadIdx.x; i < a.k; i += blockDim.x) dst[i] = i < st.cnt ? topk_keys[i] : 0ull;
-    }
+    if (!a.out_scores) finish_topk(a, topk_keys, S, qi);
 }
 
 // --------------------------------------------- q8, any pitch (lane = row)
@@ -252,16 +343,17 @@ __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
 template <int OP>
 __global__ __launch_bounds__(256) void q8_scan_generic_kernel(ScanArgs a) {
     extern __shared__ uint64_t topk_keys[];
-    __shared__ TopKShared st;
+    __shared__ ScanLds S;
     const int qi = blockIdx.y;
     const int64_t set_row0 = (int64_t)qi * a.set_stride;
     const int8_t* __restrict__ codes = a.codes + set_row0 * a.pitch;
     const float* __restrict__ scales = (const float*)a.scales + set_row0;
-    const QConst kq = a.qconst[qi];
-    const int8_t* qa = (OP == OP_DOT ? a.qc8 : a.qhi) + (int64_t)qi * a.pitch;
-    const int8_t* qb = a.qlo + (int64_t)qi * a.pitch;
+    encode_query_block(a.queries + (int64_t)qi * a.d, a.d, a.pitch, OP == OP_DOT ? ENC_E8 : ENC_E16, S.q);
+    const QConst kq = S.q.qc;
+    const int8_t* qa = OP == OP_DOT ? S.q.c8 : S.q.hi;
+    const int8_t* qb = S.q.lo;
     const int chunks = a.pitch / 16;
-    if (!a.out_scores) topk_init(topk_keys, &st);
+    if (!a.out_scores) topk_init(topk_keys, &S.st);
     const int64_t wg_row0 = (int64_t)blockIdx.x * a.rounds * 256;
     for (int r = 0; r < a.rounds; r++) {
         const int64_t row = wg_row0 + (int64_t)r * 256 + threadIdx.x;
@@ -282,40 +374,35 @@ __global__ __launch_bounds__(256) void q8_scan_generic_kernel(ScanArgs a) {
             if (OP == OP_L2) d2 = a.dd[set_row0 + row];
             score = q8_epilogue<OP>(s_hi, s_lo, scales[row], kq, dn, d2);
         }
-        uint64_t tau = a.out_scores ? 0ull : st.tau;
-        emit_round(score, valid, row, a.n, qi, a.out_scores, topk_keys, &st, tau, a.smallest);
-        if (!a.out_scores) {
+        const uint64_t tau = a.out_scores ? 0ull : S.st.tau;
+        emit_round(score, valid, row, a.n, qi, a.out_scores, topk_keys, &S.st, tau, a.smallest);
+        if (!a.out_scores && a.mid_compact) {
             __syncthreads();
-            topk_maybe_compact(topk_keys, &st, a.k, a.cap);
+            topk_maybe_compact(topk_keys, &S.st, a.k, a.cap);
         }
     }
-    if (!a.out_scores) {
-        topk_compact(topk_keys, &st, a.k);
-        uint64_t* dst = a.partial + ((int64_t)qi * gridDim.x + blockIdx.x) * a.k;
-        for (int i = threadIdx.x; i < a.k; i += blockDim.x) dst[i] = i < st.cnt ? topk_keys[i] : 0ull;
-    }
+    if (!a.out_scores) finish_topk(a, topk_keys, S, qi);
 }
 
 // ------------------------------------------------------- q4 (lane = row)
 
 // Nibbles to 16x-scaled int8 lanes: (w << 4) & 0xF0F0F0F0 holds the even
-// nibbles of w as 16*code, w & 0xF0F0F0F0 the odd ones.  The query digits
-// for q4 are stored permuted to match: per 8 columns, [c0 c2 c4 c6] then
-// [c1 c3 c5 c7].  Sums are 16x the true block sums and are divided back
-// exactly.
+// nibbles of w as 16*code, w & 0xF0F0F0F0 the odd ones; the query digit
+// planes are permuted to match (q4_perm_pos).  Block sums are 16x the true
+// sums and are divided back exactly.
 template <int OP>
 __global__ __launch_bounds__(256) void q4_scan_kernel(ScanArgs a) {
     extern __shared__ uint64_t topk_keys[];
-    __shared__ TopKShared st;
+    __shared__ ScanLds S;
     const int qi = blockIdx.y;
     const int64_t set_row0 = (int64_t)qi * a.set_stride;
     const uint8_t* __restrict__ packed = (const uint8_t*)a.codes + set_row0 * a.pitch;
     const uint16_t* __restrict__ scales = (const uint16_t*)a.scales + set_row0 * a.nb;
-    const QConst kq = a.qconst[qi];
-    // permuted digits: 2*D bytes per digit plane, see host-side permutation
-    const int* qh = (const int*)(a.qhi + (int64_t)qi * a.pitch * 2);
-    const int* ql = (const int*)(a.qlo + (int64_t)qi * a.pitch * 2);
-    if (!a.out_scores) topk_init(topk_keys, &st);
+    encode_query_block(a.queries + (int64_t)qi * a.d, a.d, a.d, ENC_E16_Q4, S.q);
+    const QConst kq = S.q.qc;
+    const int* qh = (const int*)S.q.hi;
+    const int* ql = (const int*)S.q.lo;
+    if (!a.out_scores) topk_init(topk_keys, &S.st);
     const int64_t wg_row0 = (int64_t)blockIdx.x * a.rounds * 256;
     for (int r = 0; r < a.rounds; r++) {
         const int64_t row = wg_row0 + (int64_t)r * 256 + threadIdx.x;
@@ -350,77 +437,46 @@ __global__ __launch_bounds__(256) void q4_scan_kernel(ScanArgs a) {
             if (OP == OP_L2) d2 = a.dd[set_row0 + row];
             score = q4_finish<OP>(dotf, kq, dn, d2);
         }
-        uint64_t tau = a.out_scores ? 0ull : st.tau;
-        emit_round(score, valid, row, a.n, qi, a.out_scores, topk_keys, &st, tau, a.smallest);
-        if (!a.out_scores) {
+        const uint64_t tau = a.out_scores ? 0ull : S.st.tau;
+        emit_round(score, valid, row, a.n, qi, a.out_scores, topk_keys, &S.st, tau, a.smallest);
+        if (!a.out_scores && a.mid_compact) {
             __syncthreads();
-            topk_maybe_compact(topk_keys, &st, a.k, a.cap);
+            topk_maybe_compact(topk_keys, &S.st, a.k, a.cap);
         }
     }
-    if (!a.out_scores) {
-        topk_compact(topk_keys, &st, a.k);
-        uint64_t* dst = a.partial + ((int64_t)qi * gridDim.x + blockIdx.x) * a.k;
-        for (int i = threadIdx.x; i < a.k; i += blockDim.x) dst[i] = i < st.cnt ? topk_keys[i] : 0ull;
-    }
-}
-
-// Permute E16 digits for the q4 kernel: per group of 8 columns write
-// [c0 c2 c4 c6 c1 c3 c5 c7].  Source and destination planes are [nq][pitch2]
-// where pitch2 = d (one byte per column).
-__global__ void q4_permute_digits_kernel(const int8_t* __restrict__ src, int8_t* __restrict__ dst,
-                                         int d, int64_t total) {
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    int64_t row = i / d;
-    int c = (int)(i % d);
-    int grp = c / 8, w = c % 8;
-    int srcc = grp * 8 + (w < 4 ? 2 * w : 2 * (w - 4) + 1);
-    dst[row * d + c] = src[row * d + srcc];
+    if (!a.out_scores) finish_topk(a, topk_keys, S, qi);
 }
 
 // ------------------------------------------------ exact accumulator rescore
 
-// One thread per selected (query, slot): recompute the q8 integer
-// accumulator of the chosen row (E8 for dot, E16 hi/lo combined for the
-// others) and write it as int64.
-__global__ void q8_rescore_acc_kernel(const int8_t* __restrict__ codes, int pitch, int64_t set_stride,
-                                      int64_t n, const int32_t* __restrict__ ids, int k, int nq, int e16,
-                                      const int8_t* __restrict__ qc8, const int8_t* __restrict__ qhi,
-                                      const int8_t* __restrict__ qlo, int64_t* __restrict__ out) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nq * k) return;
-    int qi = i / k;
-    int64_t row = ids[i];
-    if (row < 0 || row >= n) {
-        out[i] = 0;
-        return;
+// One workgroup per query: re-encode the query and recompute the q8
+// integer accumulator of each selected row (E8 for dot, E16 hi/lo combined
+// for the others), written as int64.
+__global__ __launch_bounds__(256) void q8_rescore_acc_kernel(const int8_t* __restrict__ codes, int pitch,
+                                                             int64_t set_stride, int64_t n, int d,
+                                                             const uint16_t* __restrict__ queries,
+                                                             const int32_t* __restrict__ ids, int k, int e16,
+                                                             int64_t* __restrict__ out) {
+    __shared__ QueryLds L;
+    const int qi = blockIdx.x;
+    encode_query_block(queries + (int64_t)qi * d, d, pitch, e16 ? ENC_E16 : ENC_E8, L);
+    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+        const int64_t row = ids[(int64_t)qi * k + i];
+        int64_t acc = 0;
+        if (row >= 0 && row < n) {
+            const int8_t* rp = codes + ((int64_t)qi * set_stride + row) * pitch;
+            for (int c = 0; c < pitch; c++)
+                acc += (int64_t)rp[c] * (e16 ? 256 * (int64_t)L.hi[c] + L.lo[c] : (int64_t)L.c8[c]);
+        }
+        out[(int64_t)qi * k + i] = acc;
     }
-    const int8_t* rp = codes + ((int64_t)qi * set_stride + row) * pitch;
-    int64_t acc = 0;
-    if (!e16) {
-        const int8_t* qp = qc8 + (int64_t)qi * pitch;
-        for (int c = 0; c < pitch; c++) acc += (int64_t)rp[c] * qp[c];
-    } else {
-        const int8_t* hp = qhi + (int64_t)qi * pitch;
-        const int8_t* lp = qlo + (int64_t)qi * pitch;
-        for (int c = 0; c < pitch; c++) acc += (int64_t)rp[c] * (256 * (int64_t)hp[c] + lp[c]);
-    }
-    out[i] = acc;
 }
 
 // ----------------------------------------------------------------- hosts
 
 hipError_t launch_query_encode(const uint16_t* q, int nq, int d, int pitch, int e16, int8_t* c8,
                                int8_t* hi, int8_t* lo, QConst* qc, hipStream_t s) {
-    hipLaunchKernelGGL(query_encode_kernel, dim3(nq), dim3(256), 0, s, q, d, pitch, e16, c8, hi,
-                       lo, qc);
-    return hipGetLastError();
-}
-
-hipError_t launch_q4_permute(const int8_t* src, int8_t* dst, int d, int nq, hipStream_t s) {
-    int64_t total = (int64_t)nq * d;
-    hipLaunchKernelGGL(q4_permute_digits_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
-                       0, s, src, dst, d, total);
+    hipLaunchKernelGGL(query_encode_kernel, dim3(nq), dim3(256), 0, s, q, d, pitch, e16, c8, hi, lo, qc);
     return hipGetLastError();
 }
 
@@ -462,12 +518,11 @@ hipError_t launch_q4_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipS
     return hipGetLastError();
 }
 
-hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride, int64_t n,
-                             const int32_t* ids, int k, int nq, int e16, const int8_t* qc8,
-                             const int8_t* qhi, const int8_t* qlo, int64_t* out, hipStream_t s) {
-    int total = nq * k;
-    hipLaunchKernelGGL(q8_rescore_acc_kernel, dim3((total + 127) / 128), dim3(128), 0, s, codes,
-                       pitch, set_stride, n, ids, k, nq, e16, qc8, qhi, qlo, out);
+hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride, int64_t n, int d,
+                             const uint16_t* queries, const int32_t* ids, int k, int nq, int e16,
+                             int64_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(q8_rescore_acc_kernel, dim3(nq), dim3(256), 0, s, codes, pitch, set_stride, n, d,
+                       queries, ids, k, e16, out);
     return hipGetLastError();
 }
 

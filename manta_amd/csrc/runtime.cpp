@@ -44,6 +44,8 @@ struct MantaRocm {
     // first out-of-range gather index seen by a device gather (flag | index)
     unsigned long long* err_word = nullptr;
     bool gather_pending = false;
+    // per-query tickets of the last-workgroup merge (zero between calls)
+    uint32_t* tickets = nullptr;
     // per-kernel-family timing (manta_rocm_set_timing)
     bool timing = false;
     std::vector<TimedLaunch> pending;
@@ -282,6 +284,8 @@ int manta_rocm_create(int device, MantaRocm** out, char** err) {
     rt->stream = rt->own_stream;
     e = hipMalloc((void**)&rt->err_word, sizeof(unsigned long long));
     if (e == hipSuccess) e = hipMemset(rt->err_word, 0, sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMalloc((void**)&rt->tickets, 65536 * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(rt->tickets, 0, 65536 * sizeof(uint32_t));
     if (e != hipSuccess) {
         (void)hipStreamDestroy(rt->own_stream);
         delete rt;
@@ -302,6 +306,7 @@ void manta_rocm_destroy(MantaRocm* rt) {
     for (auto e : rt->event_pool) (void)hipEventDestroy(e);
     if (rt->ws) (void)hipFree(rt->ws);
     if (rt->err_word) (void)hipFree(rt->err_word);
+    if (rt->tickets) (void)hipFree(rt->tickets);
     if (rt->own_stream) (void)hipStreamDestroy(rt->own_stream);
     delete rt;
 }
@@ -559,51 +564,7 @@ int manta_rocm_candidates_info(const MantaRocmCandidates* c, int* format, int64_
 
 namespace {
 
-struct QueryPlan {
-    int8_t* c8 = nullptr;
-    int8_t* hi = nullptr;
-    int8_t* lo = nullptr;
-    int8_t* phi = nullptr;  // q4 permuted digits
-    int8_t* plo = nullptr;
-    QConst* qc = nullptr;
-};
-
-// Workspace bytes for the query codes of nq queries.
-size_t query_bytes(const MantaRocmCandidates* c, int64_t nq) {
-    size_t per = (size_t)std::max<int64_t>(c->pitch, c->d);
-    return (size_t)nq * per * 5 + (size_t)nq * sizeof(QConst) + 6 * 256;
-}
-
-void carve_queries(Carver& cv, const MantaRocmCandidates* c, int64_t nq, QueryPlan& qp) {
-    size_t per = (size_t)std::max<int64_t>(c->pitch, c->d);
-    qp.c8 = cv.take<int8_t>((size_t)nq * per);
-    qp.hi = cv.take<int8_t>((size_t)nq * per);
-    qp.lo = cv.take<int8_t>((size_t)nq * per);
-    qp.phi = cv.take<int8_t>((size_t)nq * per);
-    qp.plo = cv.take<int8_t>((size_t)nq * per);
-    qp.qc = cv.take<QConst>((size_t)nq);
-}
-
-int encode_queries(MantaRocm* rt, const MantaRocmCandidates* c, int op, const uint16_t* q, int64_t nq,
-                   QueryPlan& qp, char** err) {
-    const bool e16 = !(c->format == MANTA_ROCM_Q8_ROWS && op == MANTA_ROCM_DOT);
-    if (c->format == MANTA_ROCM_Q8_ROWS) {
-        LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, c->pitch, e16 ? 1 : 0, qp.c8,
-                                              qp.hi, qp.lo, qp.qc, rt->stream),
-                   "query_encode");
-    } else {
-        LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, (int)c->d, 1, qp.c8, qp.hi,
-                                              qp.lo, qp.qc, rt->stream),
-                   "query_encode");
-        LAUNCH_TRY(manta::launch_q4_permute(qp.hi, qp.phi, (int)c->d, (int)nq, rt->stream),
-                   "q4_permute");
-        LAUNCH_TRY(manta::launch_q4_permute(qp.lo, qp.plo, (int)c->d, (int)nq, rt->stream),
-                   "q4_permute");
-    }
-    return MANTA_ROCM_OK;
-}
-
-ScanArgs scan_args(const MantaRocmCandidates* c, const QueryPlan& qp, int64_t nq) {
+ScanArgs scan_args(const MantaRocmCandidates* c, const uint16_t* q) {
     ScanArgs a{};
     a.codes = (const int8_t*)c->codes;
     a.scales = c->scales;
@@ -612,17 +573,9 @@ ScanArgs scan_args(const MantaRocmCandidates* c, const QueryPlan& qp, int64_t nq
     a.n = c->n;
     a.pitch = c->pitch;
     a.nb = c->nb;
+    a.d = (int)c->d;
     a.set_stride = (c->sets == 1) ? 0 : c->n;
-    a.qc8 = qp.c8;
-    if (c->format == MANTA_ROCM_Q8_ROWS) {
-        a.qhi = qp.hi;
-        a.qlo = qp.lo;
-    } else {
-        a.qhi = qp.phi;
-        a.qlo = qp.plo;
-    }
-    a.qconst = qp.qc;
-    (void)nq;
+    a.queries = q;
     return a;
 }
 
@@ -636,9 +589,13 @@ int check_score_args(const MantaRocmCandidates* c, int op, const void* q, int64_
         return fail(err, MANTA_ROCM_ERROR, "score mismatch [%lld,%lld] x [%lld,%lld,%lld]", (long long)nq,
                     (long long)c->d, (long long)c->sets, (long long)c->n, (long long)c->d);
     if (nq > 65535) return fail(err, MANTA_ROCM_UNSUPPORTED, "more than 65535 queries in one call");
+    if (c->d > manta::kMaxQueryDim)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "query length %lld beyond the device path", (long long)c->d);
     return MANTA_ROCM_OK;
 }
 
+// Rounds of 256 rows per workgroup: aim for about 2048 workgroups (8 per
+// CU), with at most 64 rounds.
 int choose_rounds(int64_t tiles, int64_t nq) {
     int64_t r = tiles * nq / 2048;
     return (int)std::max<int64_t>(1, std::min<int64_t>(64, r));
@@ -661,14 +618,7 @@ int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* c, int op, const 
     int rc = check_score_args(c, op, q, nq, err);
     if (rc) return rc;
     if (!out) return fail(err, MANTA_ROCM_ERROR, "nil score output");
-    rc = ensure_workspace(rt, query_bytes(c, nq), err);
-    if (rc) return rc;
-    Carver cv(rt->ws);
-    QueryPlan qp;
-    carve_queries(cv, c, nq, qp);
-    rc = encode_queries(rt, c, op, q, nq, qp, err);
-    if (rc) return rc;
-    ScanArgs a = scan_args(c, qp, nq);
+    ScanArgs a = scan_args(c, q);
     const int64_t tiles = (c->n + 255) / 256;
     a.rounds = choose_rounds(tiles, nq);
     a.out_scores = out;
@@ -696,32 +646,34 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, i
     const int64_t tiles = (c->n + 255) / 256;
     const int rounds = choose_rounds(tiles, nq);
     const int64_t parts = (tiles + rounds - 1) / rounds;
-    const int cap = cap_for_k(k);
-    size_t need = query_bytes(c, nq) + (size_t)nq * parts * k * 8 + 256;
-    rc = ensure_workspace(rt, need, err);
+    // A reservoir that holds every row of the workgroup needs no compaction
+    // (and no barrier) between rounds.
+    int cap = cap_for_k(k);
+    int mid_compact = 1;
+    if (k + (int64_t)rounds * 256 <= manta::kMaxCapKeys) {
+        cap = cap_for_k(k + (int64_t)(rounds - 1) * 256);
+        mid_compact = 0;
+    }
+    rc = ensure_workspace(rt, (size_t)nq * parts * k * 8 + 256, err);
     if (rc) return rc;
-    Carver cv(rt->ws);
-    QueryPlan qp;
-    carve_queries(cv, c, nq, qp);
-    uint64_t* partial = cv.take<uint64_t>((size_t)nq * parts * k);
-    rc = encode_queries(rt, c, op, q, nq, qp, err);
-    if (rc) return rc;
-    ScanArgs a = scan_args(c, qp, nq);
+    ScanArgs a = scan_args(c, q);
+    a.mid_compact = mid_compact;
     a.rounds = rounds;
-    a.partial = partial;
+    a.partial = (uint64_t*)rt->ws;
+    a.tickets = rt->tickets;
+    a.out_ids = out_ids;
+    a.out_topk_scores = out_scores;
     a.k = (int)k;
     a.cap = cap;
+    // the merge loads all parts at once when they fit in LDS (<= 4096 keys)
+    a.lds_keys = (int)std::max<int64_t>(cap, parts * k <= manta::kMaxCapKeys ? parts * k : 0);
     a.smallest = order == MANTA_ROCM_SMALLEST;
-    rc = launch_scan(rt, c, op, a, dim3((unsigned)parts, (unsigned)nq), (size_t)cap * 8, err);
+    rc = launch_scan(rt, c, op, a, dim3((unsigned)parts, (unsigned)nq), (size_t)a.lds_keys * 8, err);
     if (rc) return rc;
-    LAUNCH_TRY(manta::launch_topk_merge(partial, nq, parts * k, (int)k, cap, a.smallest, out_ids,
-                                        out_scores, rt->stream),
-               "topk_merge");
     if (out_acc) {
-        const bool e16 = op != MANTA_ROCM_DOT;
-        LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch,
-                                            c->sets == 1 ? 0 : c->n, c->n, out_ids, (int)k, (int)nq,
-                                            e16 ? 1 : 0, qp.c8, qp.hi, qp.lo, out_acc, rt->stream),
+        LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch, c->sets == 1 ? 0 : c->n,
+                                            c->n, (int)c->d, q, out_ids, (int)k, (int)nq,
+                                            op != MANTA_ROCM_DOT ? 1 : 0, out_acc, rt->stream),
                    "q8_rescore");
     }
     return MANTA_ROCM_OK;
