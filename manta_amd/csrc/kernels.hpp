@@ -47,6 +47,34 @@ hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride,
                              const uint16_t* queries, const int32_t* ids, int k, int nq, int e16,
                              int64_t* out, hipStream_t s);
 
+// Arguments of the multi-query kernels (kernels_mq.hip): nq queries against
+// one shared candidate matrix.
+struct MqArgs {
+    const int8_t* codes;        // q8 [n][pitch]
+    const float* scales;        // [n]
+    const float* dnorm;         // [n]
+    const float* dd;            // [n]
+    int64_t n;
+    int pitch;                  // bytes per row, multiple of 32
+    int nq;
+    const int8_t* qc8;          // E8 codes [nq][pitch]
+    const int8_t* qhi;          // E16 digits [nq][pitch]
+    const int8_t* qlo;
+    const QConst* qconst;       // [nq]
+    int64_t rows_per_wg;        // candidate rows per blockIdx.x (multiple of the tile)
+    uint64_t* partial;          // [nq][gridDim.x][k]
+    unsigned long long* gtau;   // [nq] shared thresholds, zeroed before the call
+    float* out_scores;          // score-matrix mode [nq][n], else nullptr
+    int k;
+    int cap;                    // reservoir keys per query (>= k + tile rows)
+    int smallest;
+};
+
+int mq_tile_rows(int ks);
+bool mq_supported_ks(int ks);
+hipError_t launch_mq_q8(int op, int qg, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
+hipError_t launch_mq_clear(unsigned long long* gtau, int nq, hipStream_t s);
+
 // Arguments of the embed GEMM kernels (kernels_embed.hip).
 struct EmbedArgs {
     const int32_t* tokens;      // [batches*T] (pooled) or [M] (gathered matmul)

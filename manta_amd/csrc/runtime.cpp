@@ -612,12 +612,131 @@ int launch_scan(MantaRocm* rt, const MantaRocmCandidates* c, int op, const ScanA
 
 }  // namespace
 
+}  // extern "C"
+
+namespace {
+
+// Multi-query plan: many queries against one shared q8 matrix go to the
+// matrix-core kernel (kernels_mq.hip); everything else streams one query per
+// workgroup.
+struct MqPlan {
+    bool use = false;
+    int qg = 0;          // queries per group
+    int groups = 0;
+    int tile = 0;        // candidate rows per tile
+    int cap = 0;         // reservoir keys per query
+    int64_t ranges = 0;  // grid.x
+    int64_t rows_per_wg = 0;
+    size_t lds = 0;
+};
+
+constexpr size_t kMqLdsBudget = 150 * 1024;
+
+MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool topk) {
+    MqPlan p;
+    if (c->format != MANTA_ROCM_Q8_ROWS || c->sets != 1 || nq < 8) return p;
+    if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
+    p.tile = manta::mq_tile_rows(c->pitch / 32);
+    const size_t arows = 32 * (size_t)(c->pitch + 16);
+    if (op == MANTA_ROCM_DOT) {
+        p.qg = 32;
+    } else {
+        p.qg = 16;
+    }
+    if (topk) {
+        // reservoir: k + one tile, doubled for slack between compactions
+        int64_t cap = 256;
+        while (cap < 2 * k + p.tile) cap <<= 1;
+        if (cap > manta::kMaxCapKeys) cap = manta::kMaxCapKeys;
+        if (cap < k + p.tile) return p;
+        while (p.qg > 8 && arows + (size_t)p.qg * (16 + cap * 8) > kMqLdsBudget) p.qg >>= 1;
+        if (op == MANTA_ROCM_DOT && p.qg != 32) {
+            // E8 groups are 32 queries; shrink the reservoir instead
+            while (cap > k + p.tile && arows + 32 * (16 + (size_t)cap * 8) > kMqLdsBudget) cap >>= 1;
+            if (cap < k + p.tile) return p;
+            p.qg = 32;
+        }
+        p.cap = (int)cap;
+        p.lds = arows + (size_t)p.qg * (16 + (size_t)cap * 8);
+        if (p.lds > kMqLdsBudget) return p;
+    } else {
+        p.lds = arows + (size_t)p.qg * 16;
+    }
+    p.groups = (int)((nq + p.qg - 1) / p.qg);
+    const int per_cu = p.lds > 75 * 1024 ? 1 : 2;
+    const int64_t tiles = (c->n + p.tile - 1) / p.tile;
+    int64_t ranges = std::max<int64_t>(8, (256 * per_cu / p.groups) / 8 * 8);
+    ranges = std::min<int64_t>(ranges, tiles);
+    p.rows_per_wg = ((tiles + ranges - 1) / ranges) * p.tile;
+    p.ranges = (c->n + p.rows_per_wg - 1) / p.rows_per_wg;
+    if (p.groups > 65535) return p;
+    p.use = true;
+    return p;
+}
+
+// Encode queries to the global digit planes, then run the multi-query kernel.
+int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const uint16_t* q, int64_t nq,
+           int64_t k, const MqPlan& p, float* out_scores, int32_t* out_ids, float* out_topk_scores,
+           char** err) {
+    const size_t plane = (size_t)nq * c->pitch;
+    const size_t parts = out_scores ? 0 : (size_t)nq * p.ranges * k;
+    size_t need = 3 * (plane + 256) + (size_t)nq * sizeof(QConst) + (size_t)nq * 8 + parts * 8 + 2048;
+    int rc = ensure_workspace(rt, need, err);
+    if (rc) return rc;
+    Carver cv(rt->ws);
+    int8_t* c8 = cv.take<int8_t>(plane);
+    int8_t* hi = cv.take<int8_t>(plane);
+    int8_t* lo = cv.take<int8_t>(plane);
+    QConst* qc = cv.take<QConst>((size_t)nq);
+    unsigned long long* gtau = cv.take<unsigned long long>((size_t)nq);
+    uint64_t* partial = cv.take<uint64_t>(parts ? parts : 1);
+    const int e16 = op != MANTA_ROCM_DOT;
+    LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, c->pitch, e16, c8, hi, lo, qc, rt->stream),
+               "query_encode");
+    manta::MqArgs a{};
+    a.codes = (const int8_t*)c->codes;
+    a.scales = (const float*)c->scales;
+    a.dnorm = c->dnorm;
+    a.dd = c->dd;
+    a.n = c->n;
+    a.pitch = c->pitch;
+    a.nq = (int)nq;
+    a.qc8 = c8;
+    a.qhi = hi;
+    a.qlo = lo;
+    a.qconst = qc;
+    a.rows_per_wg = p.rows_per_wg;
+    a.partial = partial;
+    a.gtau = gtau;
+    a.out_scores = out_scores;
+    a.k = (int)k;
+    a.cap = p.cap;
+    a.smallest = order == MANTA_ROCM_SMALLEST;
+    if (!out_scores)
+        LAUNCH_TRY(manta::launch_mq_clear(gtau, (int)nq, rt->stream), "mq_clear");
+    LAUNCH_TRY(manta::launch_mq_q8(op, p.qg, a, dim3((unsigned)p.ranges, (unsigned)p.groups), p.lds, rt->stream),
+               "mq_scan");
+    if (!out_scores) {
+        const int mcap = cap_for_k(k);
+        LAUNCH_TRY(manta::launch_topk_merge(partial, nq, p.ranges * k, (int)k, mcap, a.smallest, out_ids,
+                                            out_topk_scores, rt->stream),
+                   "topk_merge");
+    }
+    return MANTA_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* c, int op, const uint16_t* q,
                      int64_t nq, float* out, char** err) {
     RT_CHECK(rt);
     int rc = check_score_args(c, op, q, nq, err);
     if (rc) return rc;
     if (!out) return fail(err, MANTA_ROCM_ERROR, "nil score output");
+    const MqPlan plan = mq_plan(c, op, nq, 0, false);
+    if (plan.use) return run_mq(rt, c, op, MANTA_ROCM_LARGEST, q, nq, 0, plan, out, nullptr, nullptr, err);
     ScanArgs a = scan_args(c, q);
     const int64_t tiles = (c->n + 255) / 256;
     a.rounds = choose_rounds(tiles, nq);
@@ -643,6 +762,17 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, i
     if (!out_ids) return fail(err, MANTA_ROCM_ERROR, "nil topk output");
     if (out_acc && c->format != MANTA_ROCM_Q8_ROWS)
         return fail(err, MANTA_ROCM_ERROR, "accumulator output needs q8 candidates");
+    const MqPlan plan = mq_plan(c, op, nq, k, true);
+    if (plan.use) {
+        rc = run_mq(rt, c, op, order, q, nq, k, plan, nullptr, out_ids, out_scores, err);
+        if (rc) return rc;
+        if (out_acc)
+            LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch, 0, c->n, (int)c->d, q, out_ids,
+                                                (int)k, (int)nq, op != MANTA_ROCM_DOT ? 1 : 0, out_acc,
+                                                rt->stream),
+                       "q8_rescore");
+        return MANTA_ROCM_OK;
+    }
     const int64_t tiles = (c->n + 255) / 256;
     const int rounds = choose_rounds(tiles, nq);
     const int64_t parts = (tiles + rounds - 1) / rounds;

@@ -156,3 +156,48 @@ def test_config0_full_size_bit_exact(rt):
     np.testing.assert_array_equal(acc.download(), np.take_along_axis(want_acc, want_ids, 1))
     assert np.all(np.abs(acc.download()) < 2 ** 31)
     cands.close()
+
+
+# ---------------------------------------------------------------------------
+# Many queries against one shared candidate matrix (the matrix-core path).
+
+@pytest.mark.parametrize("op,smallest", [("dot", False), ("cosine", False), ("l2_distance", True),
+                                         ("dot", True), ("l2_distance", False)])
+@pytest.mark.parametrize("d", [64, 128, 256, 384, 512])
+def test_multi_query_score_matrix_bit_exact(rt, op, smallest, d):
+    nq, n = 37, 3000
+    q, codes, scales = _q8_case(d + 1, nq, n, d, sets=1, normalize=(op != "l2_distance"))
+    cands = rt.bind_q8(codes[0], scales[0])
+    got = rt.score(cands, op, rt.to_device(q)).download()
+    want = orc.score_q8(op, q, codes[0], scales[0])
+    np.testing.assert_array_equal(got, want)
+    cands.close()
+
+
+@pytest.mark.parametrize("op,smallest", [("dot", False), ("cosine", False), ("l2_distance", True),
+                                         ("dot", True), ("l2_distance", False)])
+@pytest.mark.parametrize("nq,n,d,k", [(8, 5000, 128, 10), (33, 20000, 384, 50), (16, 30000, 128, 1000),
+                                      (40, 4097, 256, 100), (9, 700, 512, 700), (64, 12345, 64, 1)])
+def test_multi_query_topk_bit_exact(rt, op, smallest, nq, n, d, k):
+    q, codes, scales = _q8_case(nq + n + d + k, nq, n, d, sets=1, normalize=(op != "l2_distance"))
+    cands = rt.bind_q8(codes[0], scales[0])
+    ids, sc, acc = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
+    ids, sc, acc = ids.download(), sc.download(), acc.download()
+    want_s, want_acc = orc.score_q8(op, q, codes[0], scales[0], with_acc=True)
+    want_ids = orc.topk(want_s, k, smallest=smallest)
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_array_equal(sc, np.take_along_axis(want_s, want_ids, 1))
+    np.testing.assert_array_equal(acc, np.take_along_axis(want_acc, want_ids, 1))
+    cands.close()
+
+
+def test_multi_query_repeated_calls_are_identical(rt):
+    """Thresholds and tickets are reset between calls: a second call with a
+    smaller input reproduces the oracle too."""
+    for n, nq in ((20000, 32), (5000, 8)):
+        q, codes, scales = _q8_case(n, nq, n, 128, sets=1, normalize=False)
+        cands = rt.bind_q8(codes[0], scales[0])
+        ids, _, _ = rt.score_topk(cands, "l2_distance", rt.to_device(q), 100, smallest=True)
+        want = orc.topk(orc.score_q8("l2_distance", q, codes[0], scales[0]), 100, smallest=True)
+        np.testing.assert_array_equal(ids.download(), want)
+        cands.close()
