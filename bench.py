@@ -27,7 +27,6 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBS = 8000.0
 N, D, K = 65536, 256, 10
 
 
@@ -93,56 +92,175 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--sets", type=int, default=32, help="C0 problems per step")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--copy-calibration-mb", type=int, default=0,
-                    help="only run a plain device copy of this many MiB (PMC scaling run)")
-    args = ap.parse_args()
-    if args.copy_calibration_mb:
-        return copy_calibration(args.copy_calibration_mb)
-    if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (candidate rows "
-              "would shard across GPUs with a KB-scale top-k merge; see DESIGN.md). "
-              "Run with --gpus 1.", file=sys.stderr)
-        return 2
+HBM_PEAK = 8000.0          # GB/s
+F16_PEAK = 2517.0          # dense f16 MFMA TFLOP/s
+I8_PEAK = 5033.0           # dense i8 MFMA TOP/s
 
-    from manta_amd import rocm, synth
+
+def _timed(rt, fn, steps, warmup, families):
+    """Run fn warmup + steps times; host time per step and device time per
+    launch (HIP events on the runtime's stream) of each kernel family."""
+    for _ in range(warmup):
+        fn()
+    rt.synchronize()
+    rt.set_timing(True)
+    rt.timing(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    rt.synchronize()
+    el = time.perf_counter() - t0
+    fam = {}
+    for f in families:
+        n, ms = rt.timing(f)
+        fam[f] = (n, ms / max(n, 1))
+    _, all_ms = rt.timing(None)
+    rt.set_timing(False)
+    rt.timing(reset=True)
+    return el / steps, fam, all_ms / steps
+
+
+def run_c1(rt, steps, warmup) -> dict:
+    """Config 1: embed pipeline, f16, B=64, T=128, V=32000, D=E=384."""
+    from manta_amd import synth
+
+    tokens, mask, table, proj = synth.config1()
+    b, t = tokens.shape
+    d, e = proj.shape
+    td, md, tbd, pd = (rt.to_device(x) for x in (tokens, mask, table, proj))
+    out = rt.empty((b, e), np.uint16)
+    step_s, fam, dev_ms = _timed(rt, lambda: rt.embed_pooled(td, md, tbd, pd, out=out), steps, warmup,
+                                 ["embed", "embed_finalize"])
+    flops = 2.0 * b * t * d * e
+    k_ms = fam["embed"][1]
+    achieved = flops / (k_ms / 1000.0) / 1e12
+    return {
+        "workload": "c1_embed_f16", "shape": {"b": b, "t": t, "vocab": table.shape[0], "d": d, "e": e},
+        "value": b * t / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0,
+        "device_ms_per_step": dev_ms,
+        "roofline": {"bound": "mfma", "kernel": "embed_gemm_kernel<gather,f16,pool> (f16 MFMA 32x32x16)",
+                     "achieved": achieved, "peak": F16_PEAK, "unit": "TFLOP/s", "frac": achieved / F16_PEAK,
+                     "avg_launch_us": k_ms * 1000.0, "flops_per_launch": flops,
+                     "note": "flops counted over all B*T positions (masked ones included), as the reference computes them"},
+        "finalize_us": fam["embed_finalize"][1] * 1000.0,
+    }
+
+
+def run_c2(rt, steps, warmup) -> dict:
+    """Config 2: batched q4 cosine + top-100, Q=256, N=1,048,576, D=384."""
+    from manta_amd import synth
+
+    queries, packed, scales = synth.config2()
+    nq, d = queries.shape
+    n = packed.shape[0]
+    k = 100
+    cands = rt.bind_q4(packed, scales, d)
+    qd = rt.to_device(queries)
+    ids = rt.empty((nq, k), np.int32)
+    sc = rt.empty((nq, k), np.float32)
+    fams = ["q4_scan", "mq4_scan", "topk_merge", "query_encode"]
+    step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "cosine", qd, k, out=(ids, sc, None)),
+                                 steps, warmup, fams)
+    dom = max(fams, key=lambda f: fam[f][0] * fam[f][1])
+    ops = 2.0 * nq * n * d
+    achieved = ops / (fam[dom][1] / 1000.0) / 1e12
+    cands.close()
+    return {
+        "workload": "c2_q4_cosine_top100", "shape": {"q": nq, "n": n, "d": d, "k": k},
+        "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0,
+        "device_ms_per_step": dev_ms,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": F16_PEAK,
+                     "unit": "TFLOP/s (algorithmic 2*Q*N*D over the f16 peak)", "frac": achieved / F16_PEAK,
+                     "avg_launch_us": fam[dom][1] * 1000.0},
+    }
+
+
+def run_c3(rt, steps, warmup) -> dict:
+    """Config 3: q8 l2_distance rerank, smallest-1000, Q=32, N=8,388,608, D=128."""
+    from manta_amd import synth
+
+    queries, codes, scales = synth.config3()
+    nq, d = queries.shape
+    n = codes.shape[0]
+    k = 1000
+    cands = rt.bind_q8(codes, scales)
+    del codes
+    qd = rt.to_device(queries)
+    ids = rt.empty((nq, k), np.int32)
+    sc = rt.empty((nq, k), np.float32)
+    fams = ["mq_scan", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
+    step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "l2_distance", qd, k, smallest=True,
+                                                           out=(ids, sc, None)), steps, warmup, fams)
+    dom = max(fams, key=lambda f: fam[f][0] * fam[f][1])
+    nbytes = n * (d + 4) + nq * d * 2 + nq * k * 8
+    achieved = nbytes / (fam[dom][1] / 1000.0) / 1e9
+    cands.close()
+    return {
+        "workload": "c3_q8_l2_smallest1000", "shape": {"q": nq, "n": n, "d": d, "k": k},
+        "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0,
+        "device_ms_per_step": dev_ms,
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK, "avg_launch_us": fam[dom][1] * 1000.0,
+                     "bytes_per_launch": nbytes},
+        "merge_us": fam["topk_merge"][1] * 1000.0,
+    }
+
+
+def run_c4(rt, steps, warmup) -> dict:
+    """Config 4: embed 1024x64 tokens with a q8 projection, then q8 dot
+    top-50 of the 1024 embedded queries over 4,194,304 x 384 candidates."""
+    from manta_amd import synth
+
+    tokens, mask, table, pcodes, cs, codes, scales = synth.config4()
+    b, t = tokens.shape
+    d = table.shape[1]
+    e = pcodes.shape[1]
+    n = codes.shape[0]
+    k = 50
+    cands = rt.bind_q8(codes, scales)
+    del codes
+    td, md, tbd, pd, csd = (rt.to_device(x) for x in (tokens, mask, table, pcodes, cs))
+    emb = rt.empty((b, e), np.uint16)
+    ids = rt.empty((b, k), np.int32)
+    sc = rt.empty((b, k), np.float32)
+
+    def step():
+        rt.embed_pooled(td, md, tbd, pd, csd, out=emb)
+        rt.score_topk(cands, "dot", emb, k, out=(ids, sc, None))
+
+    fams = ["embed", "embed_finalize", "mq_scan", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
+    step_s, fam, dev_ms = _timed(rt, step, steps, warmup, fams)
+    flops_a = 2.0 * b * t * d * e
+    ops_b = 2.0 * b * n * d
+    emb_t = flops_a / (fam["embed"][1] / 1000.0) / 1e12
+    dom = "mq_scan" if fam["mq_scan"][0] else "q8_scan"
+    sc_t = ops_b / (fam[dom][1] / 1000.0) / 1e12
+    cands.close()
+    return {
+        "workload": "c4_embed_q8proj_then_q8dot_top50", "shape": {"q": b, "t": t, "d": d, "n": n, "k": k},
+        "value": b * n / step_s, "unit": "candidates/s (end to end, embed included)",
+        "ms_per_step": step_s * 1000.0, "device_ms_per_step": dev_ms,
+        "embed": {"tokens_per_s_kernel": b * t / (fam["embed"][1] / 1000.0),
+                  "roofline": {"bound": "mfma", "achieved": emb_t, "peak": F16_PEAK, "unit": "TFLOP/s",
+                               "frac": emb_t / F16_PEAK, "avg_launch_us": fam["embed"][1] * 1000.0}},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": sc_t, "peak": I8_PEAK, "unit": "TOP/s",
+                     "frac": sc_t / I8_PEAK, "avg_launch_us": fam[dom][1] * 1000.0, "ops_per_launch": ops_b},
+    }
+
+
+def run_c0(rt, args) -> dict:
+    from manta_amd import synth
 
     t_gen = time.perf_counter()
     queries, codes, scales = synth.config0(sets=args.sets)
     t_gen = time.perf_counter() - t_gen
-
-    rt = rocm.Runtime(0)
     cands = rt.bind_q8(codes, scales)
     q_dev = rt.to_device(queries)
     ids = rt.empty((args.sets, K), np.int32)
     sc = rt.empty((args.sets, K), np.float32)
-    out = (ids, sc, None)
-
-    for _ in range(args.warmup):
-        rt.score_topk(cands, "dot", q_dev, K, out=out)
-    rt.synchronize()
-
-    rt.set_timing(True)
-    rt.timing(reset=True)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        rt.score_topk(cands, "dot", q_dev, K, out=out)
-    rt.synchronize()
-    elapsed = time.perf_counter() - t0
-    scan_n, scan_ms = rt.timing("q8_scan")
-    all_n, all_ms = rt.timing(None)
-    rt.set_timing(False)
-
-    ms_per_step = elapsed * 1000.0 / args.steps
-    value = args.sets * N / (elapsed / args.steps)
-    scan_avg_s = scan_ms / 1000.0 / max(scan_n, 1)
+    step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "dot", q_dev, K, out=(ids, sc, None)),
+                                 args.steps, args.warmup, ["q8_scan"])
+    scan_avg_s = fam["q8_scan"][1] / 1000.0
     bytes_per_launch = args.sets * c0_bytes_per_problem()
     achieved = bytes_per_launch / scan_avg_s / 1e9
 
@@ -150,24 +268,15 @@ def main() -> int:
     q1 = rt.to_device(queries[:1])
     one = rt.bind_q8(codes[0], scales[0])
     ids1 = rt.empty((1, K), np.int32)
-    for _ in range(5):
-        rt.score_topk(one, "dot", q1, K, out=(ids1, None, None))
-    rt.synchronize()
-    reps = 200
-    t1 = time.perf_counter()
-    for _ in range(reps):
-        rt.score_topk(one, "dot", q1, K, out=(ids1, None, None))
-    rt.synchronize()
-    single_us = (time.perf_counter() - t1) * 1e6 / reps
-
+    single_s, _, _ = _timed(rt, lambda: rt.score_topk(one, "dot", q1, K, out=(ids1, None, None)), 200, 5, [])
     line = {
         "metric": "candidates scored/sec (q8 dot + top-k, BASELINE config 0 shape)",
-        "value": value,
+        "value": args.sets * N / step_s,
         "unit": "candidates/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": step_s * 1000.0,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -181,19 +290,19 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "q8_scan (manta::q8_scan_kernel<0,16,1>)",
+            "kernel": "q8_scan (manta::q8_scan_kernel<0,16,1>, fused top-k incl. merge)",
             "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
+            "peak": HBM_PEAK,
             "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
+            "frac": achieved / HBM_PEAK,
             "traffic": profiled_traffic("q8_scan_c0_batched.md") if args.sets == 32 else None,
             "traffic_source": "profiles/q8_scan_c0_batched.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
             "avg_launch_us": scan_avg_s * 1e6,
             "bytes_per_launch": bytes_per_launch,
         },
-        "device_ms_per_step_all_kernels": all_ms / args.steps,
-        "single_query_call_us": single_us,
-        "hbm_fraction_of_step": bytes_per_launch / (ms_per_step / 1000.0) / 1e9 / HBM_PEAK_GBS,
+        "device_ms_per_step_all_kernels": dev_ms,
+        "single_query_call_us": single_s * 1e6,
+        "hbm_fraction_of_step": bytes_per_launch / step_s / 1e9 / HBM_PEAK,
         "gen_seconds": t_gen,
     }
     if not args.no_cpu:
@@ -202,6 +311,45 @@ def main() -> int:
         line["cpu_baseline"] = None
     cands.close()
     one.close()
+    return line
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--sets", type=int, default=32, help="C0 problems per step")
+    ap.add_argument("--workload", default="c0", choices=["c0", "c1", "c2", "c3", "c4", "all"],
+                    help="c0 is the headline line; the others (or all) are added under 'configs'")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (PMC scaling run)")
+    args = ap.parse_args()
+    if args.copy_calibration_mb:
+        return copy_calibration(args.copy_calibration_mb)
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (candidate rows "
+              "would shard across GPUs with a KB-scale top-k merge; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from manta_amd import rocm
+
+    rt = rocm.Runtime(0)
+    extra = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4}
+    todo = list(extra) if args.workload == "all" else ([args.workload] if args.workload in extra else [])
+    heavy_steps = max(3, min(args.steps, 10))
+    configs = {}
+    for w in todo:
+        print("bench: %s" % w, file=sys.stderr, flush=True)
+        steps = args.steps if w == "c1" else heavy_steps
+        configs[w] = extra[w](rt, steps, min(args.warmup, 2) if w != "c1" else args.warmup)
+    print("bench: c0", file=sys.stderr, flush=True)
+    line = run_c0(rt, args)
+    if configs:
+        line["configs"] = configs
     rt.close()
     print(json.dumps(line), flush=True)
     return 0

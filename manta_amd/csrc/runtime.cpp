@@ -644,21 +644,18 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
         p.qg = 16;
     }
     if (topk) {
-        // reservoir: k + one tile, doubled for slack between compactions
-        int64_t cap = 256;
-        while (cap < 2 * k + p.tile) cap <<= 1;
-        if (cap > manta::kMaxCapKeys) cap = manta::kMaxCapKeys;
-        if (cap < k + p.tile) return p;
-        while (p.qg > 8 && arows + (size_t)p.qg * (16 + cap * 8) > kMqLdsBudget) p.qg >>= 1;
-        if (op == MANTA_ROCM_DOT && p.qg != 32) {
-            // E8 groups are 32 queries; shrink the reservoir instead
-            while (cap > k + p.tile && arows + 32 * (16 + (size_t)cap * 8) > kMqLdsBudget) cap >>= 1;
-            if (cap < k + p.tile) return p;
-            p.qg = 32;
-        }
+        // Reservoir keys per query: room for k plus one tile of offers, with
+        // slack so compactions stay rare; largest that fits the LDS budget.
+        auto lds_for = [&](int qg, int64_t cap) { return arows + (size_t)qg * (16 + (size_t)cap * 8); };
+        const int64_t need = k + p.tile;
+        if (need > manta::kMaxCapKeys) return p;
+        const int qg_min = op == MANTA_ROCM_DOT ? 32 : 8;
+        int64_t cap = std::min<int64_t>(manta::kMaxCapKeys, std::max<int64_t>(256, 2 * k + 2 * p.tile));
+        while (p.qg > qg_min && lds_for(p.qg, cap) > kMqLdsBudget) p.qg >>= 1;
+        while (cap > need && lds_for(p.qg, cap) > kMqLdsBudget) cap = std::max(need, cap - 256);
+        if (lds_for(p.qg, cap) > kMqLdsBudget) return p;
         p.cap = (int)cap;
-        p.lds = arows + (size_t)p.qg * (16 + (size_t)cap * 8);
-        if (p.lds > kMqLdsBudget) return p;
+        p.lds = lds_for(p.qg, cap);
     } else {
         p.lds = arows + (size_t)p.qg * 16;
     }
