@@ -42,8 +42,27 @@ __device__ __forceinline__ float loosen_up(float x) {
     return x + __builtin_fabsf(x) * 9.5367431640625e-7f + 1e-30f;
 }
 
-template <int OP, int ENC, int QG, int KS, int TJ>
-__global__ __launch_bounds__(256) void mq_q8_kernel(MqArgs a) {
+// Pre-score bound of one query from its threshold key: dot compares s*acc
+// against (tau*127)/qmax, l2 compares dist^2 against tau^2; no threshold (or
+// cosine) lets everything through.
+template <int OP>
+__device__ __forceinline__ float mq_bound(uint64_t tk, const QConst& qc, int smallest) {
+    const float open = smallest ? __builtin_inff() : -__builtin_inff();
+    if (!tk) return open;
+    const float ts = key_score(tk, smallest);
+    if (OP == OP_DOT) {
+        const float tt = fdiv_rn(fmul_rn(ts, 127.0f), qc.a);
+        return smallest ? loosen_up(tt) : loosen_down(tt);
+    }
+    if (OP == OP_L2) {
+        const float t2 = fmul_rn(ts, ts);
+        return smallest ? loosen_up(t2) : loosen_down(t2);
+    }
+    return open;
+}
+
+template <int OP, int ENC, int QG, int KS, int TJ, bool SMALL, bool TOPK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mq_q8_kernel(MqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int APITCH = KS * 32 + 16;  // bytes per A row in LDS (padded)
     constexpr int QPL = ENC == MQ_E8 ? 16 : (QG == 16 ? 8 : 4);  // queries per lane
@@ -52,6 +71,7 @@ __global__ __launch_bounds__(256) void mq_q8_kernel(MqArgs a) {
     uint64_t* keys = (uint64_t*)(smem + 32 * APITCH + QG * sizeof(TopKShared));  // [QG][cap]
     __shared__ QConst qcs[32];
     __shared__ uint64_t tau_s[QG];  // max(local reservoir tau, global tau) per query
+    __shared__ float bound_s[QG];   // pre-score bound derived from tau_s
     __shared__ uint32_t cmask;
 
     const int tid = threadIdx.x;
@@ -59,7 +79,7 @@ __global__ __launch_bounds__(256) void mq_q8_kernel(MqArgs a) {
     const int wave = tid >> 6;
     const int half = lane >> 5;
     const int q0 = blockIdx.y * QG;
-    const bool topk = a.out_scores == nullptr;
+    constexpr bool topk = TOPK;
 
     // ---- A rows: query codes (E8) or digit planes (E16)
     for (int idx = tid; idx < 32 * (KS * 2); idx += 256) {
@@ -88,26 +108,26 @@ __global__ __launch_bounds__(256) void mq_q8_kernel(MqArgs a) {
             st[q].cnt = 0;
             st[q].tau = 0;
             tau_s[q] = 0;
+            bound_s[q] = SMALL ? __builtin_inff() : -__builtin_inff();
         }
     }
     __syncthreads();
 
     // ---- per-lane query slots
-    // E8:  slot r (0..15) -> A row 8*(r/4) + 4*half + r%4 = query.
-    // E16: slot u -> hi acc index r_hi, lo index r_hi + 4, query index.
-    int slot_q[QPL];
-    int slot_r[QPL];
+    // E8:  slot u (0..15) = accumulator u = A row 8*(u/4) + 4*half + u%4 = query.
+    // E16: slot u -> hi accumulator r = (u < 4 ? u : u + 4), lo accumulator
+    //      r + 4, hi A row i = 8*(r/4) + 4*half + r%4, query (i/16)*8 + i%8.
+    auto slot_r = [](int u) { return ENC == MQ_E8 ? u : (u < 4 ? u : u + 4); };
+    auto slot_q = [&](int u) {
+        const int r = slot_r(u);
+        const int i = 8 * (r / 4) + 4 * half + (r % 4);
+        return ENC == MQ_E8 ? i : (i >> 4) * 8 + (i & 7);
+    };
+    uint32_t live_mask = 0;
 #pragma unroll
     for (int u = 0; u < QPL; u++) {
-        if (ENC == MQ_E8) {
-            slot_r[u] = u;
-            slot_q[u] = 8 * (u / 4) + 4 * half + (u % 4);
-        } else {
-            const int r = (u < 4) ? u : 8 + (u - 4);  // hi accumulators 0-3, 8-11
-            slot_r[u] = r;
-            const int i = 8 * (r / 4) + 4 * half + (r % 4);  // hi A row
-            slot_q[u] = (i >> 4) * 8 + (i & 7);
-        }
+        const int qq = slot_q(u);
+        if (qq < QG && q0 + qq < a.nq) live_mask |= 1u << u;
     }
 
     const int64_t range0 = (int64_t)blockIdx.x * a.rows_per_wg;
@@ -115,91 +135,118 @@ __global__ __launch_bounds__(256) void mq_q8_kernel(MqArgs a) {
     if (range1 > a.n) range1 = a.n;
     constexpr int TILE = 4 * TJ * 32;
 
-    for (int64_t t0 = range0; t0 < range1; t0 += TILE) {
-        // thresholds for this tile (local reservoir or any workgroup's)
-        float bound[QPL];
-        uint64_t tau[QPL];
+    // B fragments (16 bytes of a candidate row per K step) of the next tile
+    // are loaded while the current one is multiplied.
+    v4i bn[TJ][KS];
+    float sn[TJ], cn[TJ];  // scale and |d| or |d|^2 of the prefetched rows
+    auto load_tile = [&](int64_t t0) {
 #pragma unroll
-        for (int u = 0; u < QPL; u++) {
-            const int qq = slot_q[u];
-            const uint64_t tk = (topk && qq < QG) ? tau_s[qq] : 0ull;
-            tau[u] = tk;
-            if (!tk) {
-                bound[u] = a.smallest ? __builtin_inff() : -__builtin_inff();
-            } else {
-                const float ts = key_score(tk, a.smallest);
-                if (OP == OP_DOT) {
-                    const float tt = fmul_rn(ts, 127.0f);
-                    bound[u] = a.smallest ? loosen_up(tt) : loosen_down(tt);
-                } else if (OP == OP_L2) {
-                    const float t2 = fmul_rn(ts, ts);
-                    bound[u] = a.smallest ? loosen_up(t2) : loosen_down(t2);
-                } else {
-                    bound[u] = a.smallest ? __builtin_inff() : -__builtin_inff();
-                }
-            }
+        for (int tj = 0; tj < TJ; tj++) {
+            const int64_t row = t0 + (int64_t)(wave * TJ + tj) * 32 + (lane & 31);
+            const bool ok = row < range1;
+            const int64_t rr = ok ? row : 0;
+            const int8_t* rp = a.codes + rr * a.pitch + half * 16;
+#pragma unroll
+            for (int s = 0; s < KS; s++)
+                bn[tj][s] = ok ? *(const v4i*)(rp + s * 32) : v4i{0, 0, 0, 0};
+            sn[tj] = a.scales[rr];
+            cn[tj] = OP == OP_COSINE ? a.dnorm[rr] : (OP == OP_L2 ? a.dd[rr] : 0.0f);
         }
+    };
+    if (range0 < range1) load_tile(range0);
+    // shared thresholds are read one tile ahead of their use
+    uint64_t gnext = 0;
+    if (topk && tid < QG && q0 + tid < a.nq)
+        gnext = __hip_atomic_load(&a.gtau[q0 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    for (int64_t t0 = range0; t0 < range1; t0 += TILE) {
+        float sc[TJ], cc[TJ];
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) {
+            sc[tj] = sn[tj];
+            cc[tj] = cn[tj];
+        }
+
+        // per-slot filter bounds (computed once per query per tile, in LDS)
+        float bound[QPL];
+#pragma unroll
+        for (int u = 0; u < QPL; u++) bound[u] = bound_s[slot_q(u) < QG ? slot_q(u) : 0];
+
+        // MFMA phase: independent accumulator chains (TJ row blocks, and the
+        // K steps split in two for long rows) so the matrix pipe never waits
+        // on its own previous result.
+        constexpr int NC = (KS >= 8) ? 2 : 1;
+        v16i acc[TJ][NC];
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++)
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[tj][c][r] = 0;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const v4i av = *(const v4i*)(arows + (lane & 31) * APITCH + s * 32 + half * 16);
+#pragma unroll
+            for (int tj = 0; tj < TJ; tj++)
+                acc[tj][s % NC] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bn[tj][s], acc[tj][s % NC], 0, 0, 0);
+        }
+        // the fragments are consumed: start the next tile's loads now so they
+        // overlap this tile's epilogue and reservoir upkeep
+        if (t0 + TILE < range1) load_tile(t0 + TILE);
 
 #pragma unroll
         for (int tj = 0; tj < TJ; tj++) {
-            const int64_t rowblk = t0 + (int64_t)(wave * TJ + tj) * 32;
-            const int64_t row = rowblk + (lane & 31);
-            const bool rvalid = row < range1;
-            // B fragments: 16 bytes of the candidate row per K step
-            v4i b[KS];
-            const int8_t* rp = a.codes + row * a.pitch + half * 16;
-#pragma unroll
-            for (int s = 0; s < KS; s++)
-                b[s] = rvalid ? __builtin_nontemporal_load((const v4i*)(rp + s * 32)) : v4i{0, 0, 0, 0};
-            v16i acc;
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[r] = 0;
-#pragma unroll
-            for (int s = 0; s < KS; s++) {
-                const v4i av = *(const v4i*)(arows + (lane & 31) * APITCH + s * 32 + half * 16);
-                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b[s], acc, 0, 0, 0);
-            }
-            if (!rvalid) continue;
-            const float scale = a.scales[row];
-            float rowc = 0.0f;
-            if (OP == OP_COSINE) rowc = a.dnorm[row];
-            if (OP == OP_L2) rowc = a.dd[row];
+            const int64_t row = t0 + (int64_t)(wave * TJ + tj) * 32 + (lane & 31);
+            if (row >= range1) continue;
+            v16i accs = acc[tj][0];
+            if (NC > 1) accs += acc[tj][NC - 1];
+            const float scale = sc[tj];
+            const float rowc = cc[tj];
+            // pre-scores: dot s*acc, l2 dist^2, cosine q.d (exact f32 steps)
+            auto pre_of = [&](int hi, int lo, int qq) {
+                if (OP == OP_DOT) return fmul_rn(scale, (float)hi);
+                const float dotf = __fmaf_rn(256.0f, (float)hi, (float)lo);
+                const float qd = fmul_rn(fmul_rn(scale, qcs[qq].a), dotf);
+                return OP == OP_L2 ? fsub_rn(fadd_rn(qcs[qq].c, rowc), fmul_rn(2.0f, qd)) : qd;
+            };
+            uint32_t pmask = 0;
 #pragma unroll
             for (int u = 0; u < QPL; u++) {
-                const int qq = slot_q[u];
-                const int q = q0 + qq;
-                if ((ENC == MQ_E16 && qq >= QG) || q >= a.nq) continue;
-                const QConst kq = qcs[qq];
+                const int r = slot_r(u);
+                const float p = pre_of(accs[r], ENC == MQ_E8 ? 0 : accs[r + 4], slot_q(u) < QG ? slot_q(u) : 0);
+                const bool keep = !topk || (SMALL ? !(p > bound[u]) : !(p < bound[u]));
+                if (keep) pmask |= 1u << u;
+            }
+            pmask &= live_mask;
+            // exact scores for the survivors only (rare once thresholds settle)
+            while (pmask) {
+                const int u = __builtin_ctz(pmask);
+                pmask &= pmask - 1;
+                int hi = accs[slot_r(0)], lo = ENC == MQ_E8 ? 0 : accs[slot_r(0) + 4];
+#pragma unroll
+                for (int w = 1; w < QPL; w++) {
+                    hi = (u == w) ? accs[slot_r(w)] : hi;
+                    if (ENC != MQ_E8) lo = (u == w) ? accs[slot_r(w) + 4] : lo;
+                }
+                const int r0 = slot_r(u);
+                const int i0 = 8 * (r0 / 4) + 4 * half + (r0 % 4);
+                const int qq = ENC == MQ_E8 ? i0 : (i0 >> 4) * 8 + (i0 & 7);
+                const float v = pre_of(hi, lo, qq);
                 float score;
-                bool pass;
                 if (OP == OP_DOT) {
-                    float t = fmul_rn(fmul_rn(scale, (float)acc[slot_r[u]]), kq.a);
-                    pass = a.smallest ? (t <= bound[u]) : (t >= bound[u]);
-                    if (!topk) pass = true;
-                    if (!pass) continue;
-                    score = fdiv_rn(t, 127.0f);
+                    score = fdiv_rn(fmul_rn(v, qcs[qq].a), 127.0f);
+                } else if (OP == OP_COSINE) {
+                    const float den = fmul_rn(qcs[qq].b, rowc);
+                    score = den == 0.0f ? 0.0f : fdiv_rn(v, den);
                 } else {
-                    const float dotf = __fmaf_rn(256.0f, (float)acc[slot_r[u]], (float)acc[slot_r[u] + 4]);
-                    const float qd = fmul_rn(fmul_rn(scale, kq.a), dotf);
-                    if (OP == OP_COSINE) {
-                        const float den = fmul_rn(kq.b, rowc);
-                        score = den == 0.0f ? 0.0f : fdiv_rn(qd, den);
-                    } else {
-                        const float t = fadd_rn(kq.c, rowc);
-                        float dist2 = fsub_rn(t, fmul_rn(2.0f, qd));
-                        pass = a.smallest ? (dist2 <= bound[u]) : (dist2 >= bound[u]);
-                        if (!topk) pass = true;
-                        if (!pass) continue;
-                        dist2 = dist2 < 0.0f ? 0.0f : dist2;
-                        score = fsqrt_rn(dist2);
-                    }
+                    score = fsqrt_rn(v < 0.0f ? 0.0f : v);
                 }
                 if (!topk) {
-                    a.out_scores[(int64_t)q * a.n + row] = score;
+                    a.out_scores[(int64_t)(q0 + qq) * a.n + row] = score;
                     continue;
                 }
-                const uint64_t key = make_key(score, (uint32_t)row, a.smallest);
-                if (key > tau[u]) {
+                const uint64_t key = make_key(score, (uint32_t)row, SMALL);
+                if (key > tau_s[qq]) {
                     const int pos = atomicAdd(&st[qq].cnt, 1);
                     keys[(int64_t)qq * a.cap + pos] = key;
                 }
@@ -208,11 +255,10 @@ __global__ __launch_bounds__(256) void mq_q8_kernel(MqArgs a) {
         if (!topk) continue;
         // ---- keep every reservoir able to take the next tile
         __syncthreads();
-        if (tid == 0) {
-            uint32_t m = 0;
-            for (int qq = 0; qq < QG; qq++)
-                if (st[qq].cnt + TILE > a.cap) m |= 1u << qq;
-            cmask = m;
+        if (tid < 64) {
+            const bool need = tid < QG && st[tid].cnt + TILE > a.cap;
+            const uint64_t m = __ballot(need);
+            if (tid == 0) cmask = (uint32_t)m;
         }
         __syncthreads();
         const uint32_t m = cmask;
@@ -222,8 +268,10 @@ __global__ __launch_bounds__(256) void mq_q8_kernel(MqArgs a) {
             if (tid == 0 && st[qq].tau && q0 + qq < a.nq) atomicMax(&a.gtau[q0 + qq], st[qq].tau);
         }
         if (tid < QG && q0 + tid < a.nq) {
-            const uint64_t g = __hip_atomic_load(&a.gtau[q0 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            tau_s[tid] = st[tid].tau > g ? st[tid].tau : g;
+            const uint64_t tk = st[tid].tau > gnext ? st[tid].tau : gnext;
+            tau_s[tid] = tk;
+            bound_s[tid] = mq_bound<OP>(tk, qcs[tid], SMALL);
+            gnext = __hip_atomic_load(&a.gtau[q0 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
     }
@@ -249,12 +297,12 @@ __global__ void mq_clear_kernel(unsigned long long* gtau, int nq) {
 
 // ----------------------------------------------------------------- hosts
 
-template <int OP, int ENC, int QG>
+template <int OP, int ENC, int QG, bool SMALL, bool TOPK>
 static hipError_t launch_mq_ks(const MqArgs& a, dim3 grid, size_t lds, hipStream_t s, int ks) {
-#define MANTA_MQ(KSV, TJV)                                                                     \
-    if (ks == (KSV)) {                                                                         \
-        hipLaunchKernelGGL((mq_q8_kernel<OP, ENC, QG, KSV, TJV>), grid, dim3(256), lds, s, a); \
-        return hipGetLastError();                                                              \
+#define MANTA_MQ(KSV, TJV)                                                                                   \
+    if (ks == (KSV)) {                                                                                       \
+        hipLaunchKernelGGL((mq_q8_kernel<OP, ENC, QG, KSV, TJV, SMALL, TOPK>), grid, dim3(256), lds, s, a); \
+        return hipGetLastError();                                                                            \
     }
     MANTA_MQ(2, 4)
     MANTA_MQ(4, 4)
@@ -263,6 +311,13 @@ static hipError_t launch_mq_ks(const MqArgs& a, dim3 grid, size_t lds, hipStream
     MANTA_MQ(16, 1)
 #undef MANTA_MQ
     return hipErrorInvalidValue;
+}
+
+template <int OP, int ENC, int QG>
+static hipError_t launch_mq_mode(const MqArgs& a, dim3 grid, size_t lds, hipStream_t s, int ks) {
+    if (a.out_scores) return launch_mq_ks<OP, ENC, QG, false, false>(a, grid, lds, s, ks);
+    if (a.smallest) return launch_mq_ks<OP, ENC, QG, true, true>(a, grid, lds, s, ks);
+    return launch_mq_ks<OP, ENC, QG, false, true>(a, grid, lds, s, ks);
 }
 
 int mq_tile_rows(int ks) {
@@ -274,13 +329,13 @@ bool mq_supported_ks(int ks) { return ks == 2 || ks == 4 || ks == 8 || ks == 12 
 
 hipError_t launch_mq_q8(int op, int qg, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     const int ks = a.pitch / 32;
-    if (op == OP_DOT) return launch_mq_ks<OP_DOT, MQ_E8, 32>(a, grid, lds, s, ks);
+    if (op == OP_DOT) return launch_mq_mode<OP_DOT, MQ_E8, 32>(a, grid, lds, s, ks);
     if (op == OP_COSINE) {
-        if (qg == 16) return launch_mq_ks<OP_COSINE, MQ_E16, 16>(a, grid, lds, s, ks);
-        return launch_mq_ks<OP_COSINE, MQ_E16, 8>(a, grid, lds, s, ks);
+        if (qg == 16) return launch_mq_mode<OP_COSINE, MQ_E16, 16>(a, grid, lds, s, ks);
+        return launch_mq_mode<OP_COSINE, MQ_E16, 8>(a, grid, lds, s, ks);
     }
-    if (qg == 16) return launch_mq_ks<OP_L2, MQ_E16, 16>(a, grid, lds, s, ks);
-    return launch_mq_ks<OP_L2, MQ_E16, 8>(a, grid, lds, s, ks);
+    if (qg == 16) return launch_mq_mode<OP_L2, MQ_E16, 16>(a, grid, lds, s, ks);
+    return launch_mq_mode<OP_L2, MQ_E16, 8>(a, grid, lds, s, ks);
 }
 
 hipError_t launch_mq_clear(unsigned long long* gtau, int nq, hipStream_t s) {

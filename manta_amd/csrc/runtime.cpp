@@ -631,6 +631,7 @@ struct MqPlan {
 };
 
 constexpr size_t kMqLdsBudget = 150 * 1024;
+constexpr size_t kMqLdsTwoPerCu = 78 * 1024;
 
 MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool topk) {
     MqPlan p;
@@ -653,6 +654,9 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
         int64_t cap = std::min<int64_t>(manta::kMaxCapKeys, std::max<int64_t>(256, 2 * k + 2 * p.tile));
         while (p.qg > qg_min && lds_for(p.qg, cap) > kMqLdsBudget) p.qg >>= 1;
         while (cap > need && lds_for(p.qg, cap) > kMqLdsBudget) cap = std::max(need, cap - 256);
+        // prefer two workgroups per CU when the smaller reservoir still fits
+        const int64_t cap2 = std::max<int64_t>(need, 256);
+        if (lds_for(p.qg, cap) > kMqLdsTwoPerCu && lds_for(p.qg, cap2) <= kMqLdsTwoPerCu) cap = cap2;
         if (lds_for(p.qg, cap) > kMqLdsBudget) return p;
         p.cap = (int)cap;
         p.lds = lds_for(p.qg, cap);
@@ -660,7 +664,7 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
         p.lds = arows + (size_t)p.qg * 16;
     }
     p.groups = (int)((nq + p.qg - 1) / p.qg);
-    const int per_cu = p.lds > 75 * 1024 ? 1 : 2;
+    const int per_cu = p.lds > kMqLdsTwoPerCu ? 1 : 2;
     const int64_t tiles = (c->n + p.tile - 1) / p.tile;
     int64_t ranges = std::max<int64_t>(8, (256 * per_cu / p.groups) / 8 * 8);
     ranges = std::min<int64_t>(ranges, tiles);
