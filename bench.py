@@ -331,7 +331,7 @@ def main() -> int:
         return copy_calibration(args.copy_calibration_mb)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (candidate rows "
-              "would shard across GPUs with a KB-scale top-k merge; see DESIGN.md). "
+              "would shard across GPUs, each returning its own top-k for a KB-scale merge). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
 

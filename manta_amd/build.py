@@ -28,7 +28,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
-    # packed f32 VALU forms stay off ("Build flags")
+    # packed f32 VALU forms stay off: some of their forms have given wrong
+    # results on this hardware without any error
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-I" + os.path.join(ROOT, "include"),

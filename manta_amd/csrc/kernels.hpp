@@ -47,8 +47,8 @@ hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride,
                              const uint16_t* queries, const int32_t* ids, int k, int nq, int e16,
                              int64_t* out, hipStream_t s);
 
-// Arguments of the multi-query kernels (kernels_mq.hip): nq queries against
-// one shared candidate matrix.
+// Arguments of the multi-query scan kernel (kernels_mq.hip): nq queries
+// against one shared candidate matrix, over rows [row_begin, row_end).
 struct MqArgs {
     const int8_t* codes;        // q8 [n][pitch]
     const float* scales;        // [n]
@@ -56,24 +56,58 @@ struct MqArgs {
     const float* dd;            // [n]
     int64_t n;
     int pitch;                  // bytes per row, multiple of 32
+    int64_t row_begin;          // rows of this pass
+    int64_t row_end;
+    int64_t rows_per_wg;        // rows per blockIdx.x (multiple of the chunk)
     int nq;
     const int8_t* qc8;          // E8 codes [nq][pitch]
     const int8_t* qhi;          // E16 digits [nq][pitch]
     const int8_t* qlo;
     const QConst* qconst;       // [nq]
-    int64_t rows_per_wg;        // candidate rows per blockIdx.x (multiple of the tile)
-    uint64_t* partial;          // [nq][gridDim.x][k]
-    unsigned long long* gtau;   // [nq] shared thresholds, zeroed before the call
-    float* out_scores;          // score-matrix mode [nq][n], else nullptr
+    const uint64_t* tau;        // [nq] threshold keys of this pass (0: none)
+    uint64_t* regions;          // [R][nq][rc] appended keys (nq*R*rc < 2^31)
+    int* counts;                // [R][nq] keys per region
+    int R;                      // gridDim.x
+    int rc;                     // region capacity (>= k + 2 * chunk rows + 1)
     int k;
-    int cap;                    // reservoir keys per query (>= k + tile rows)
+    float* out_scores;          // score-matrix mode [nq][n], else nullptr
     int smallest;
 };
 
-int mq_tile_rows(int ks);
+// Arguments of the per-query merge after a pass.
+struct MqSelectArgs {
+    const uint64_t* regions;    // [R][nq][rc]
+    const int* counts;          // [R][nq]
+    int R;
+    int rc;
+    uint64_t* best;             // [nq][k] best keys so far (sorted), updated
+    int* bcnt;                  // [nq] valid keys in best
+    uint64_t* tau;              // [nq] next pass's threshold key (0: none)
+    int k;
+    int nq;
+    int32_t* out_ids;           // final pass: [nq][k] ids (else nullptr)
+    float* out_scores;          // final pass: [nq][k] scores or nullptr
+    int smallest;
+};
+
+// Launch shape of the scan kernel for an op, K steps (pitch / 32) and query count.
+struct MqShape {
+    int ks = 0;
+    int na = 0;          // A blocks per wave
+    int wq = 0;          // waves splitting the queries (1 or 4)
+    int qg = 0;          // queries per workgroup
+    int chunk = 0;       // candidate rows per LDS chunk
+    int tile = 0;        // LDS bytes of one chunk tile
+    int tile_bytes = 0;  // LDS bytes of all chunk tiles and their row constants
+};
+
+MqShape mq_shape(int op, int ks, int64_t nq);
 bool mq_supported_ks(int ks);
-hipError_t launch_mq_q8(int op, int qg, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
-hipError_t launch_mq_clear(unsigned long long* gtau, int nq, hipStream_t s);
+hipError_t launch_mq_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
+int mq_select_threads(int64_t expect_keys);
+size_t mq_select_lds(int threads, int R);
+hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s);
+hipError_t launch_mq_clear(uint64_t* tau, int* bcnt, int nq, hipStream_t s);
 
 // Arguments of the embed GEMM kernels (kernels_embed.hip).
 struct EmbedArgs {

@@ -1,27 +1,32 @@
 // kernels_mq.hip -- many queries against one shared q8 candidate matrix
 // ([Q,D] x [N,D]) on the i8 matrix cores of gfx950.
 //
-// Workgroup = 4 waves; grid = (row ranges, query groups).  The group's query
-// codes sit in LDS as the A operand of v_mfma_i32_32x32x32_i8 (32 "rows" =
-// queries or query digits); each wave streams TJ blocks of 32 candidate rows
-// per tile straight from HBM as the B operand (16 bytes per lane per
-// 32-wide K step), so every candidate byte is loaded once per query group.
-// With the candidate on the output column, a lane ends a tile holding one
-// candidate row against 16 A rows:
-//   E8 (dot, 32 queries per group)      : 16 queries per lane;
-//   E16 (cosine / l2, 8 or 16 queries)  : A rows [hi q0-7 | lo q0-7 | hi
-//        q8-15 | lo q8-15], so a query's hi and lo sums land in the same lane
-//        (acc[r] and acc[r+4]) and combine exactly as fma(256, hi, lo).
-// The epilogue evaluates a cheap monotone pre-score (t = (s*acc)*qmax for
-// dot, dist^2 for l2) against a conservative per-query bound derived from
-// the current threshold key, and only survivors get the exact score and key
-// (the same f32 formulas as the streaming kernels and the CPU oracle).
-// Keys go to per-query LDS reservoirs (radix-select compaction); each
-// compaction raises a per-query global threshold (agent-scope atomic max)
-// that every workgroup filters with.  Each workgroup finally writes k keys
-// per query; topk_merge_kernel reduces them.  Row ranges are a multiple of 8
-// long in blocks, so the workgroups of different query groups that share a
-// range share an XCD (and its L2).
+// mq_scan_kernel: workgroup = 4 waves, grid = (row ranges, query groups).
+// Each wave keeps NA blocks of query codes resident in VGPRs as the A
+// operand of v_mfma_i32_32x32x32_i8 (32 A rows = 32 queries for E8 codes,
+// or 16 queries x {hi, lo} digit for E16 codes).  Candidate rows stream
+// through LDS in chunks: the workgroup loads a chunk with coalesced 16-byte
+// loads (rows are contiguous, so a chunk is one contiguous span of HBM),
+// stores it into a padded LDS tile, and every wave reads its B fragments
+// from there -- each candidate byte is fetched from HBM/L2 once per
+// workgroup and feeds 4*NA (WQ = 4) or NA (WQ = 1) MFMAs.  The next chunk's
+// loads are in flight while the current one is multiplied.
+//
+// With the candidate on the MFMA output column, lane l ends a 32-row block
+// holding candidate l%32 against 16 A rows: 16 queries (E8), or 8 queries as
+// (hi, lo) pairs in acc[r] / acc[r+4] (E16; A rows [hi q0-7 | lo q0-7 |
+// hi q8-15 | lo q8-15]), combined exactly as fma(256, hi, lo).
+//
+// Top-k runs in passes over growing row prefixes.  A pass gets a threshold
+// key per query -- the k-th best key of all rows of the earlier passes, a
+// valid lower bound of the final k-th key -- and appends every key above it
+// to a per-(query, workgroup) region in HBM.  A cheap monotone pre-score
+// (dot: s*acc, l2: dist^2, cosine: q.d against tau*|q|*|d|) tested against
+// a loosened bound decides which scores are computed exactly.  If a region
+// still fills up (adversarially ordered rows) the workgroup compacts it to
+// its best k keys and raises its own threshold, so no key is ever lost.
+// mq_select_kernel then merges the previous best k with the pass's regions
+// into the new best k and the next pass's threshold.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -30,11 +35,12 @@ namespace manta {
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 enum { MQ_E8 = 0, MQ_E16 = 1 };
+enum { MQ_SCORES = 0, MQ_APPEND = 1 };
 
 // Conservative pre-score bounds from a threshold key.  Survivors of the
 // bound are re-checked with the exact key, so the bound only has to be
-// loose on the safe side (relative 2^-20 covers every rounding in t and
-// dist^2).
+// loose on the safe side (relative 2^-20 covers every rounding in the
+// pre-scores and in the exact score formulas).
 __device__ __forceinline__ float loosen_down(float x) {
     return x - __builtin_fabsf(x) * 9.5367431640625e-7f - 1e-30f;
 }
@@ -42,11 +48,12 @@ __device__ __forceinline__ float loosen_up(float x) {
     return x + __builtin_fabsf(x) * 9.5367431640625e-7f + 1e-30f;
 }
 
-// Pre-score bound of one query from its threshold key: dot compares s*acc
-// against (tau*127)/qmax, l2 compares dist^2 against tau^2; no threshold (or
-// cosine) lets everything through.
+// Pre-score bound of one query from its threshold key.  dot compares s*acc
+// against (tau*127)/qmax; l2 compares dist^2 against tau^2; cosine compares
+// q.d against (tau*|q|) * |d| (the |d| factor is applied per row).  No
+// threshold lets everything through.
 template <int OP>
-__device__ __forceinline__ float mq_bound(uint64_t tk, const QConst& qc, int smallest) {
+__device__ __forceinline__ float mq_bound(uint64_t tk, const QConst& qc, bool smallest) {
     const float open = smallest ? __builtin_inff() : -__builtin_inff();
     if (!tk) return open;
     const float ts = key_score(tk, smallest);
@@ -58,288 +65,662 @@ __device__ __forceinline__ float mq_bound(uint64_t tk, const QConst& qc, int sma
         const float t2 = fmul_rn(ts, ts);
         return smallest ? loosen_up(t2) : loosen_down(t2);
     }
-    return open;
+    return fmul_rn(smallest ? loosen_up(ts) : loosen_down(ts), qc.b);
 }
 
-template <int OP, int ENC, int QG, int KS, int TJ, bool SMALL, bool TOPK>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mq_q8_kernel(MqArgs a) {
+// Direct global->LDS loads (gfx950): each lane's 16 (or 4) bytes land at
+// M0 + 16*lane (4*lane) of the wave's LDS segment.  Issued from inline asm so
+// the compiler does not wait for them around LDS reads of other tiles; the
+// scan waits for them itself (s_waitcnt vmcnt, loads complete in order).
+// The compiler's own waits stay correct: they only ever count too few
+// outstanding loads and so wait longer, never shorter.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+__device__ __forceinline__ void lds_load16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_load4(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+// Radix select over keys[0..c) (c > k, keys distinct), whole workgroup:
+// finds (prefix, pmask) such that exactly k keys satisfy
+// (key & pmask) >= prefix.  8-bit digits, most significant first; a wave
+// whose matching lanes share one digit adds them with a single LDS atomic,
+// so the (typically uniform) leading digits of the keys cost no contention.
+__device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, SelectShared& ss,
+                                          uint64_t& prefix_out, uint64_t& pmask_out) {
+    const int tid = threadIdx.x;
+    const int nt = blockDim.x;
+    const int lane = tid & 63;
+    uint64_t prefix = 0, pmask = 0;
+    int remaining = k;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        for (int i = tid; i < 256; i += nt) ss.hist[i] = 0;
+        __syncthreads();
+        for (int i = tid; i < c; i += nt) {
+            const uint64_t key = keys[i];
+            const bool m = (key & pmask) == prefix;
+            const int dg = (int)((key >> shift) & 0xFF);
+            const uint64_t mm = __ballot(m);
+            if (mm) {
+                const int lead = __ffsll((unsigned long long)mm) - 1;
+                const int d0 = __shfl(dg, lead);
+                const uint64_t same = __ballot(m && dg == d0);
+                if (same == mm) {
+                    if (lane == lead) atomicAdd(&ss.hist[d0], __popcll(mm));
+                } else if (m) {
+                    atomicAdd(&ss.hist[dg], 1);
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < 64) {
+            // lane l owns digits 255-4l .. 252-4l (descending)
+            int h[4];
+            int sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                h[j] = ss.hist[255 - 4 * tid - j];
+                sum += h[j];
+            }
+            int incl = sum;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int t = __shfl_up(incl, off);
+                if (tid >= off) incl += t;
+            }
+            int cum = incl - sum;  // keys with a larger digit
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (cum < remaining && cum + h[j] >= remaining) {
+                    ss.digit = 255 - 4 * tid - j;
+                    ss.above = cum;
+                }
+                cum += h[j];
+            }
+        }
+        __syncthreads();
+        const int d = ss.digit;
+        remaining -= ss.above;
+        prefix |= (uint64_t)d << shift;
+        pmask |= 0xFFull << shift;
+        const bool all_in = ss.hist[d] == remaining;
+        __syncthreads();
+        if (all_in) break;  // every key with this prefix is kept
+    }
+    prefix_out = prefix;
+    pmask_out = pmask;
+}
+
+template <int OP, int ENC, int KS, int NA, int WQ, int MODE, bool SMALL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mq_scan_kernel(MqArgs a) {
+    constexpr int PITCH = KS * 32;           // bytes per candidate row
+    constexpr int P = PITCH + 16;            // LDS row pitch (padding spreads banks)
+    constexpr int WR = 4 / WQ;               // waves splitting the rows of a chunk (WQ: 1, 2 or 4)
+    // 4 waves sharing rows (WQ = 4): 64-row chunks, two tiles (chunk c+1 in
+    // flight), two workgroups per CU.  Waves splitting rows: 32 rows per wave,
+    // three tiles (chunks c+1 and c+2 in flight) to cover HBM latency.
+    constexpr int NBW = WQ == 4 ? 2 : 1;     // 32-row blocks per wave per chunk
+    constexpr int NBUF = WQ == 4 ? 2 : 3;    // LDS chunk tiles
+    constexpr int CHUNK = WR * NBW * 32;     // rows per chunk
+    constexpr int SEGS = (CHUNK * P + 1023) / 1024;  // 1 KB LDS segments per chunk tile
+    constexpr int DPW = (SEGS + 3) / 4;              // 16-byte direct-to-LDS loads per wave per chunk
+    constexpr int TILE = DPW * 4 * 1024;             // LDS bytes per tile
+    constexpr int NARR = OP == OP_DOT ? 1 : 2;       // per-row arrays: scale (+ |d| or |d|^2)
+    constexpr int CSA = (CHUNK + 63) / 64;           // 256-byte segments per array per chunk
+    constexpr int CPW = (NARR * CSA + 3) / 4;        // 4-byte direct-to-LDS loads per wave per chunk
+    constexpr int CTILE = CPW * 4 * 256;             // LDS bytes of a chunk's per-row constants
+    constexpr int VPW = DPW + CPW;                   // direct-to-LDS loads per wave per chunk
+    constexpr int QPB = ENC == MQ_E8 ? 32 : 16;  // queries per A block
+    constexpr int QPW = NA * QPB;                // queries per wave
+    constexpr int QG = WQ * QPW;                 // queries per workgroup
+    constexpr int QPL = ENC == MQ_E8 ? 16 : 8;   // queries per lane per A block
+    constexpr int NC = (NA == 1 && KS >= 4) ? 2 : 1;  // accumulator chains per A block
+    constexpr int NFW = (QG + 63) / 64;               // flag words
+    constexpr bool APPEND = MODE == MQ_APPEND;
+
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    constexpr int APITCH = KS * 32 + 16;  // bytes per A row in LDS (padded)
-    constexpr int QPL = ENC == MQ_E8 ? 16 : (QG == 16 ? 8 : 4);  // queries per lane
-    int8_t* arows = (int8_t*)smem;                          // [32][APITCH]
-    TopKShared* st = (TopKShared*)(smem + 32 * APITCH);      // [QG]
-    uint64_t* keys = (uint64_t*)(smem + 32 * APITCH + QG * sizeof(TopKShared));  // [QG][cap]
-    __shared__ QConst qcs[32];
-    __shared__ uint64_t tau_s[QG];  // max(local reservoir tau, global tau) per query
-    __shared__ float bound_s[QG];   // pre-score bound derived from tau_s
-    __shared__ uint32_t cmask;
+    uint8_t* tiles = smem;                                   // [NBUF][TILE]
+    float* consts = (float*)(smem + NBUF * TILE);            // [NBUF][CTILE / 4]
+    // compaction scratch: the tile that is about to be refilled, or an extra
+    // LDS area when rc keys do not fit in a tile
+    uint64_t* scratch_extra = (uint64_t*)(smem + NBUF * (TILE + CTILE));
+    __shared__ QConst qcs[QG];
+    __shared__ uint64_t tau_s[QG];
+    // per-query values the epilogue reads four at a time (float4)
+    __shared__ __attribute__((aligned(16))) float bnd_s[QG];  // pre-score bound
+    __shared__ __attribute__((aligned(16))) float qa_s[QG];   // QConst.a
+    __shared__ __attribute__((aligned(16))) float qc_s[QG];   // QConst.c
+    __shared__ int cnt_s[QG];
+    __shared__ uint64_t flags[2][NFW];  // double-buffered by chunk parity
+    __shared__ SelectShared ss;
+    __shared__ int wpos;
+    __shared__ unsigned long long minkey;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int half = lane >> 5;
+    const int wq = wave % WQ;
+    const int wr = wave / WQ;
     const int q0 = blockIdx.y * QG;
-    constexpr bool topk = TOPK;
 
-    // ---- A rows: query codes (E8) or digit planes (E16)
-    for (int idx = tid; idx < 32 * (KS * 2); idx += 256) {
-        const int i = idx / (KS * 2);
-        const int seg = idx % (KS * 2);  // 16-byte segment of the row
-        int q = -1;
-        const int8_t* src = nullptr;
+    // ---- query constants, thresholds, region counters
+    for (int i = tid; i < QG; i += 256) {
+        const int q = q0 + i;
+        const bool ok = q < a.nq;
+        const QConst qc = ok ? a.qconst[q] : QConst{1.0f, 0.0f, 0.0f, 0.0f};
+        qcs[i] = qc;
+        qa_s[i] = qc.a;
+        qc_s[i] = qc.c;
+        const uint64_t tk = (APPEND && ok) ? a.tau[q] : 0ull;
+        // a query past nq gets a bound nothing passes and the largest key
+        tau_s[i] = ok ? tk : ~0ull;
+        bnd_s[i] = ok ? mq_bound<OP>(tk, qc, SMALL) : (SMALL ? -__builtin_inff() : __builtin_inff());
+        cnt_s[i] = 0;
+    }
+
+    // ---- A operand: this wave's query codes, resident for the whole scan
+    v4i av[NA][KS];
+#pragma unroll
+    for (int na = 0; na < NA; na++) {
+        const int i = lane & 31;
+        int q;
+        const int8_t* plane;
         if (ENC == MQ_E8) {
-            q = q0 + i;
-            src = a.qc8;
+            q = q0 + wq * QPW + na * 32 + i;
+            plane = a.qc8;
         } else {
-            const int blk = i >> 3;  // 0: hi 0-7, 1: lo 0-7, 2: hi 8-15, 3: lo 8-15
-            const int qq = (blk >> 1) * 8 + (i & 7);
-            if (qq < QG) {
-                q = q0 + qq;
-                src = (blk & 1) ? a.qlo : a.qhi;
-            }
+            const int blk = i >> 3;  // 0: hi q0-7, 1: lo q0-7, 2: hi q8-15, 3: lo q8-15
+            q = q0 + wq * QPW + na * 16 + (blk >> 1) * 8 + (i & 7);
+            plane = (blk & 1) ? a.qlo : a.qhi;
         }
-        v4i v = v4i{0, 0, 0, 0};
-        if (src && q < a.nq && seg * 16 < a.pitch) v = *(const v4i*)(src + (int64_t)q * a.pitch + seg * 16);
-        *(v4i*)(arows + i * APITCH + seg * 16) = v;
+        const bool ok = q < a.nq;
+        const int8_t* src = plane + (int64_t)(ok ? q : 0) * PITCH + half * 16;
+#pragma unroll
+        for (int s = 0; s < KS; s++) av[na][s] = ok ? *(const v4i*)(src + s * 32) : v4i{0, 0, 0, 0};
     }
-    if (tid < 32) qcs[tid] = (q0 + tid < a.nq && tid < QG) ? a.qconst[q0 + tid] : QConst{0, 0, 0, 0};
-    if (topk) {
-        for (int q = tid; q < QG; q += 256) {
-            st[q].cnt = 0;
-            st[q].tau = 0;
-            tau_s[q] = 0;
-            bound_s[q] = SMALL ? __builtin_inff() : -__builtin_inff();
-        }
-    }
-    __syncthreads();
 
-    // ---- per-lane query slots
-    // E8:  slot u (0..15) = accumulator u = A row 8*(u/4) + 4*half + u%4 = query.
-    // E16: slot u -> hi accumulator r = (u < 4 ? u : u + 4), lo accumulator
-    //      r + 4, hi A row i = 8*(r/4) + 4*half + r%4, query (i/16)*8 + i%8.
+    // slot u of A block na -> accumulator index and workgroup-local query
     auto slot_r = [](int u) { return ENC == MQ_E8 ? u : (u < 4 ? u : u + 4); };
-    auto slot_q = [&](int u) {
+    auto slot_lq = [&](int na, int u) {
         const int r = slot_r(u);
         const int i = 8 * (r / 4) + 4 * half + (r % 4);
-        return ENC == MQ_E8 ? i : (i >> 4) * 8 + (i & 7);
+        return wq * QPW + na * QPB + (ENC == MQ_E8 ? i : (i >> 4) * 8 + (i & 7));
     };
-    uint32_t live_mask = 0;
+    uint32_t live[NA];  // slots whose query exists (score-matrix mode)
 #pragma unroll
-    for (int u = 0; u < QPL; u++) {
-        const int qq = slot_q(u);
-        if (qq < QG && q0 + qq < a.nq) live_mask |= 1u << u;
+    for (int na = 0; na < NA; na++) {
+        live[na] = 0;
+#pragma unroll
+        for (int u = 0; u < QPL; u++)
+            if (q0 + slot_lq(na, u) < a.nq) live[na] |= 1u << u;
     }
 
-    const int64_t range0 = (int64_t)blockIdx.x * a.rows_per_wg;
-    int64_t range1 = range0 + a.rows_per_wg;
-    if (range1 > a.n) range1 = a.n;
-    constexpr int TILE = 4 * TJ * 32;
+    // this workgroup's key regions: [query][rc] (32-bit indices, checked on the host)
+    uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.nq * a.rc;
+    const int64_t r0 = a.row_begin + (int64_t)blockIdx.x * a.rows_per_wg;
+    int64_t r1 = r0 + a.rows_per_wg;
+    if (r1 > a.row_end) r1 = a.row_end;
 
-    // B fragments (16 bytes of a candidate row per K step) of the next tile
-    // are loaded while the current one is multiplied.
-    v4i bn[TJ][KS];
-    float sn[TJ], cn[TJ];  // scale and |d| or |d|^2 of the prefetched rows
-    auto load_tile = [&](int64_t t0) {
+    // Candidate chunks go straight from HBM into LDS tiles (16-byte direct-
+    // to-LDS loads, no VGPR staging) NBUF-1 chunks ahead of their use.  Lane
+    // i of a wave's load fills bytes [16i, 16i+16) of a 1 KB tile segment;
+    // the source is the row byte that belongs there in the padded layout,
+    // clamped into the range (padding and rows past the range receive
+    // arbitrary in-range bytes and are never used).  The chunk's per-row
+    // constants follow the same way (4-byte loads, 64 rows per load), so the
+    // loop issues no other global loads that would have to be waited for.
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    auto issue_chunk = [&](int64_t c0, int buf) {
+        const int8_t* base = a.codes + c0 * PITCH;
+        const int left = (int)(r1 - c0 < CHUNK ? r1 - c0 : CHUNK);
+        const int lim = left * PITCH - 16;  // last 16 bytes inside the range
+        const uint32_t t = lds_addr(tiles) + buf * TILE;
 #pragma unroll
-        for (int tj = 0; tj < TJ; tj++) {
-            const int64_t row = t0 + (int64_t)(wave * TJ + tj) * 32 + (lane & 31);
-            const bool ok = row < range1;
-            const int64_t rr = ok ? row : 0;
-            const int8_t* rp = a.codes + rr * a.pitch + half * 16;
+        for (int i = 0; i < DPW; i++) {
+            const int seg = wave_s * DPW + i;
+            const int x = seg * 1024 + lane * 16;
+            const int row = x / P;
+            const int off = row * PITCH + (x - row * P);
+            lds_load16(base + (off < lim ? off : lim), t + seg * 1024);
+        }
+        const uint32_t ct = lds_addr(consts) + buf * CTILE;
 #pragma unroll
-            for (int s = 0; s < KS; s++)
-                bn[tj][s] = ok ? *(const v4i*)(rp + s * 32) : v4i{0, 0, 0, 0};
-            sn[tj] = a.scales[rr];
-            cn[tj] = OP == OP_COSINE ? a.dnorm[rr] : (OP == OP_L2 ? a.dd[rr] : 0.0f);
+        for (int i = 0; i < CPW; i++) {
+            const int cs = wave_s * CPW + i;  // segments past NARR*CSA are filler
+            const int arr = cs / CSA < NARR ? cs / CSA : 0;
+            const int row = (cs % CSA) * 64 + lane;
+            const float* src = arr == 0 ? a.scales : (OP == OP_COSINE ? a.dnorm : a.dd);
+            lds_load4(src + c0 + (row < left ? row : left - 1), ct + cs * 256);
         }
     };
-    if (range0 < range1) load_tile(range0);
-    // shared thresholds are read one tile ahead of their use
-    uint64_t gnext = 0;
-    if (topk && tid < QG && q0 + tid < a.nq)
-        gnext = __hip_atomic_load(&a.gtau[q0 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();  // LDS query state above is complete
+    // Retire the A-fragment loads here, where the compiler sees it: otherwise
+    // it would wait for them (and with them every chunk load in flight) at
+    // their first use inside the loop, in every iteration.
+    __builtin_amdgcn_s_waitcnt(0);
+    if (r0 < r1) {
+        issue_chunk(r0, 0);
+        if (NBUF == 3 && r0 + CHUNK < r1) issue_chunk(r0 + CHUNK, 1);
+    }
 
-    for (int64_t t0 = range0; t0 < range1; t0 += TILE) {
-        float sc[TJ], cc[TJ];
-#pragma unroll
-        for (int tj = 0; tj < TJ; tj++) {
-            sc[tj] = sn[tj];
-            cc[tj] = cn[tj];
-        }
-
-        // per-slot filter bounds (computed once per query per tile, in LDS)
-        float bound[QPL];
-#pragma unroll
-        for (int u = 0; u < QPL; u++) bound[u] = bound_s[slot_q(u) < QG ? slot_q(u) : 0];
-
-        // MFMA phase: independent accumulator chains (TJ row blocks, and the
-        // K steps split in two for long rows) so the matrix pipe never waits
-        // on its own previous result.
-        constexpr int NC = (KS >= 8) ? 2 : 1;
-        v16i acc[TJ][NC];
-#pragma unroll
-        for (int tj = 0; tj < TJ; tj++)
-#pragma unroll
-            for (int c = 0; c < NC; c++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[tj][c][r] = 0;
-#pragma unroll
-        for (int s = 0; s < KS; s++) {
-            const v4i av = *(const v4i*)(arows + (lane & 31) * APITCH + s * 32 + half * 16);
-#pragma unroll
-            for (int tj = 0; tj < TJ; tj++)
-                acc[tj][s % NC] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bn[tj][s], acc[tj][s % NC], 0, 0, 0);
-        }
-        // the fragments are consumed: start the next tile's loads now so they
-        // overlap this tile's epilogue and reservoir upkeep
-        if (t0 + TILE < range1) load_tile(t0 + TILE);
-
-#pragma unroll
-        for (int tj = 0; tj < TJ; tj++) {
-            const int64_t row = t0 + (int64_t)(wave * TJ + tj) * 32 + (lane & 31);
-            if (row >= range1) continue;
-            v16i accs = acc[tj][0];
-            if (NC > 1) accs += acc[tj][NC - 1];
-            const float scale = sc[tj];
-            const float rowc = cc[tj];
-            // pre-scores: dot s*acc, l2 dist^2, cosine q.d (exact f32 steps)
-            auto pre_of = [&](int hi, int lo, int qq) {
-                if (OP == OP_DOT) return fmul_rn(scale, (float)hi);
-                const float dotf = __fmaf_rn(256.0f, (float)hi, (float)lo);
-                const float qd = fmul_rn(fmul_rn(scale, qcs[qq].a), dotf);
-                return OP == OP_L2 ? fsub_rn(fadd_rn(qcs[qq].c, rowc), fmul_rn(2.0f, qd)) : qd;
-            };
-            uint32_t pmask = 0;
-#pragma unroll
-            for (int u = 0; u < QPL; u++) {
-                const int r = slot_r(u);
-                const float p = pre_of(accs[r], ENC == MQ_E8 ? 0 : accs[r + 4], slot_q(u) < QG ? slot_q(u) : 0);
-                const bool keep = !topk || (SMALL ? !(p > bound[u]) : !(p < bound[u]));
-                if (keep) pmask |= 1u << u;
+    int buf = 0, par = 0;
+    for (int64_t c0 = r0; c0 < r1; c0 += CHUNK, buf = buf == NBUF - 1 ? 0 : buf + 1, par ^= 1) {
+        if (APPEND) {
+            // Flag regions that might not take one more chunk of keys.  Read
+            // before the barrier, a count may still miss up to CHUNK keys of
+            // the previous chunk from other waves, hence the margin of two
+            // chunks (rc >= k + 2*CHUNK + 1).  Parity buffers: the flags
+            // written here are read after this barrier, while the next
+            // chunk's flags go to the other buffer.
+            for (int w = wave; w < NFW; w += 4) {
+                const int i = w * 64 + lane;
+                const uint64_t m = __ballot(i < QG && cnt_s[i < QG ? i : 0] > a.rc - 2 * CHUNK);
+                if (lane == 0) flags[par][w] = m;
             }
-            pmask &= live_mask;
-            // exact scores for the survivors only (rare once thresholds settle)
-            while (pmask) {
-                const int u = __builtin_ctz(pmask);
-                pmask &= pmask - 1;
-                int hi = accs[slot_r(0)], lo = ENC == MQ_E8 ? 0 : accs[slot_r(0) + 4];
+        }
+        // This wave's loads of chunk c are done once at most the VPW loads of
+        // chunk c+1 are outstanding (NBUF == 3; loads complete in order); the
+        // barrier extends that to every wave's loads, retires the previous
+        // chunk's tile reads before that tile is refilled, and publishes the
+        // flags.  (A plain __syncthreads would also wait for chunk c+1.)
+        if (NBUF == 3 && c0 + CHUNK < r1)
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(VPW) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int nbuf = buf == 0 ? NBUF - 1 : buf - 1;  // tile of chunk c+NBUF-1 (free now)
+        if (APPEND) {
+            // rare: compact full regions to their best k keys
+            bool any = false;
 #pragma unroll
-                for (int w = 1; w < QPL; w++) {
-                    hi = (u == w) ? accs[slot_r(w)] : hi;
-                    if (ENC != MQ_E8) lo = (u == w) ? accs[slot_r(w) + 4] : lo;
+            for (int w = 0; w < NFW; w++) any |= flags[par][w] != 0;
+            if (any) {
+                uint64_t* scratch = a.rc * 8 <= TILE ? (uint64_t*)(tiles + nbuf * TILE) : scratch_extra;
+                for (int lq = 0; lq < QG; lq++) {
+                    if (!((flags[par][lq >> 6] >> (lq & 63)) & 1)) continue;
+                    uint64_t* reg = wreg + (uint32_t)((q0 + lq) * a.rc);
+                    const int c = cnt_s[lq];
+                    for (int i = tid; i < c; i += 256) scratch[i] = reg[i];
+                    if (tid == 0) {
+                        wpos = 0;
+                        minkey = ~0ull;
+                    }
+                    __syncthreads();
+                    uint64_t prefix, pmask;
+                    block_radix_prefix(scratch, c, a.k, ss, prefix, pmask);
+                    uint64_t lo = ~0ull;
+                    for (int i = tid; i < c; i += 256) {
+                        const uint64_t key = scratch[i];
+                        if ((key & pmask) >= prefix) {
+                            reg[atomicAdd(&wpos, 1)] = key;
+                            lo = key < lo ? key : lo;
+                        }
+                    }
+                    if (lo != ~0ull) atomicMin(&minkey, (unsigned long long)lo);
+                    __syncthreads();
+                    if (tid == 0) {
+                        cnt_s[lq] = a.k;
+                        if (minkey > tau_s[lq]) {
+                            tau_s[lq] = minkey;
+                            bnd_s[lq] = mq_bound<OP>(minkey, qcs[lq], SMALL);
+                        }
+                    }
+                    __syncthreads();
                 }
-                const int r0 = slot_r(u);
-                const int i0 = 8 * (r0 / 4) + 4 * half + (r0 % 4);
-                const int qq = ENC == MQ_E8 ? i0 : (i0 >> 4) * 8 + (i0 & 7);
-                const float v = pre_of(hi, lo, qq);
-                float score;
-                if (OP == OP_DOT) {
-                    score = fdiv_rn(fmul_rn(v, qcs[qq].a), 127.0f);
-                } else if (OP == OP_COSINE) {
-                    const float den = fmul_rn(qcs[qq].b, rowc);
-                    score = den == 0.0f ? 0.0f : fdiv_rn(v, den);
-                } else {
-                    score = fsqrt_rn(v < 0.0f ? 0.0f : v);
+            }
+        }
+
+        // Refill the free tile with chunk c+NBUF-1 now -- except that with
+        // three tiles the score matrix does it after this chunk's stores,
+        // which also count in vmcnt and would otherwise be waited for with it.
+        constexpr bool LATE = !APPEND && NBUF == 3;
+        if (!LATE && c0 + (NBUF - 1) * CHUNK < r1) issue_chunk(c0 + (NBUF - 1) * CHUNK, nbuf);
+        const uint8_t* tile = tiles + buf * TILE;
+        const float* ctile = consts + buf * (CTILE / 4);
+
+#pragma unroll
+        for (int b = 0; b < NBW; b++) {
+            const int blk = wr * NBW + b;
+            const int64_t row = c0 + blk * 32 + (lane & 31);
+            v16i acc[NA][NC];
+#pragma unroll
+            for (int na = 0; na < NA; na++)
+#pragma unroll
+                for (int ch = 0; ch < NC; ch++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[na][ch][r] = 0;
+            // B fragments are read from LDS two K steps ahead of their MFMAs
+            const uint8_t* bp = tile + (blk * 32 + (lane & 31)) * P + half * 16;
+            v4i b0 = *(const v4i*)bp;
+            v4i b1 = KS > 1 ? *(const v4i*)(bp + 32) : b0;
+#pragma unroll
+            for (int s = 0; s < KS; s++) {
+                const v4i b2 = s + 2 < KS ? *(const v4i*)(bp + (s + 2) * 32) : b1;
+#pragma unroll
+                for (int na = 0; na < NA; na++)
+                    acc[na][s % NC] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[na][s], b0, acc[na][s % NC], 0, 0, 0);
+                b0 = b1;
+                b1 = b2;
+            }
+            if (row >= r1) continue;
+            const float scale = ctile[blk * 32 + (lane & 31)];
+            const float rowc = OP == OP_DOT ? 0.0f : ctile[CSA * 64 + blk * 32 + (lane & 31)];
+#pragma unroll
+            for (int na = 0; na < NA; na++) {
+                v16i accs = acc[na][0];
+                if (NC > 1) accs += acc[na][NC - 1];
+                // slot u's query is lq = lq0 + 8*(u/4) + u%4: the per-query
+                // values of four slots are one float4 in LDS
+                const int lq0 = wq * QPW + na * QPB + 4 * half;
+                float bq[QPL], qa[QPL], qcv[QPL];
+#pragma unroll
+                for (int m = 0; m < QPL / 4; m++) {
+                    const float4 b4 = *(const float4*)&bnd_s[lq0 + 8 * m];
+                    bq[4 * m] = b4.x, bq[4 * m + 1] = b4.y, bq[4 * m + 2] = b4.z, bq[4 * m + 3] = b4.w;
+                    if (OP != OP_DOT) {
+                        const float4 a4 = *(const float4*)&qa_s[lq0 + 8 * m];
+                        qa[4 * m] = a4.x, qa[4 * m + 1] = a4.y, qa[4 * m + 2] = a4.z, qa[4 * m + 3] = a4.w;
+                    }
+                    if (OP == OP_L2) {
+                        const float4 c4 = *(const float4*)&qc_s[lq0 + 8 * m];
+                        qcv[4 * m] = c4.x, qcv[4 * m + 1] = c4.y, qcv[4 * m + 2] = c4.z, qcv[4 * m + 3] = c4.w;
+                    }
                 }
-                if (!topk) {
-                    a.out_scores[(int64_t)(q0 + qq) * a.n + row] = score;
+                // pre-scores: dot s*acc, l2 dist^2, cosine q.d (exact f32 steps)
+                auto pre_of = [&](int hi, int lo, int u) {
+                    if (OP == OP_DOT) return fmul_rn(scale, (float)hi);
+                    const float dotf = __fmaf_rn(256.0f, (float)hi, (float)lo);
+                    const float qd = fmul_rn(fmul_rn(scale, qa[u]), dotf);
+                    return OP == OP_L2 ? fsub_rn(fadd_rn(qcv[u], rowc), fmul_rn(2.0f, qd)) : qd;
+                };
+                auto score_of = [&](float v, int lq) {
+                    if (OP == OP_DOT) return fdiv_rn(fmul_rn(v, qcs[lq].a), 127.0f);
+                    if (OP == OP_COSINE) {
+                        const float den = fmul_rn(qcs[lq].b, rowc);
+                        return den == 0.0f ? 0.0f : fdiv_rn(v, den);
+                    }
+                    return fsqrt_rn(v < 0.0f ? 0.0f : v);
+                };
+                if (!APPEND) {
+                    // score matrix: every live slot
+#pragma unroll
+                    for (int u = 0; u < QPL; u++) {
+                        if (!((live[na] >> u) & 1)) continue;
+                        const int r = slot_r(u);
+                        const int lq = slot_lq(na, u);
+                        const float v = pre_of(accs[r], ENC == MQ_E8 ? 0 : accs[r + 4], u);
+                        a.out_scores[(int64_t)(q0 + lq) * a.n + row] = score_of(v, lq);
+                    }
                     continue;
                 }
-                const uint64_t key = make_key(score, (uint32_t)row, SMALL);
-                if (key > tau_s[qq]) {
-                    const int pos = atomicAdd(&st[qq].cnt, 1);
-                    keys[(int64_t)qq * a.cap + pos] = key;
+                // filter: one compare per slot; the exact score and key are
+                // computed only where some lane of the wave survives (an
+                // exec-masked branch that the wave skips when none does)
+#pragma unroll
+                for (int u = 0; u < QPL; u++) {
+                    const int r = slot_r(u);
+                    const float p = pre_of(accs[r], ENC == MQ_E8 ? 0 : accs[r + 4], u);
+                    const float bv = OP == OP_COSINE ? fmul_rn(bq[u], rowc) : bq[u];
+                    const bool keep = SMALL ? !(p > bv) : !(p < bv);
+                    if (keep) {
+                        const int lq = slot_lq(na, u);
+                        const uint64_t key = make_key(score_of(p, lq), (uint32_t)row, SMALL);
+                        if (key > tau_s[lq]) {
+                            const int pos = atomicAdd(&cnt_s[lq], 1);
+                            wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = key;
+                        }
+                    }
                 }
             }
         }
-        if (!topk) continue;
-        // ---- keep every reservoir able to take the next tile
+        if (LATE && c0 + 2 * CHUNK < r1) issue_chunk(c0 + 2 * CHUNK, nbuf);
+    }
+    if (!APPEND) return;
+    __syncthreads();
+    for (int i = tid; i < QG; i += 256)
+        if (q0 + i < a.nq) a.counts[(int64_t)blockIdx.x * a.nq + q0 + i] = cnt_s[i];
+}
+
+// ------------------------------------------------------------- select
+
+// Merge a query's previous best keys with the keys its pass appended: the
+// new best k (sorted descending), their count, and the next pass's
+// threshold (the k-th key once k keys exist).  One workgroup per query.
+// Keys stream through an LDS buffer of NT*16 keys; whenever it fills, a
+// radix select keeps the best k.  The final pass writes ids and scores.
+template <int NT>
+__global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
+    constexpr int KPT = 16;
+    constexpr int LCAP = NT * KPT;
+    constexpr int NW = NT / 64;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint64_t* buf = (uint64_t*)smem;           // [LCAP]
+    int* pre = (int*)(smem + LCAP * 8);        // [R + 1]
+    __shared__ SelectShared ss;
+    __shared__ int wsum[NW];
+    __shared__ int wpos;
+    __shared__ unsigned long long minkey;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int q = blockIdx.x;
+    const int k = a.k;
+
+    // exclusive prefix of the pass's region counts
+    int carry = 0;
+    for (int base = 0; base < a.R; base += NT) {
+        const int w = base + tid;
+        int c = w < a.R ? a.counts[(int64_t)w * a.nq + q] : 0;
+        c = c < a.rc ? c : a.rc;
+        int incl = c;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(incl, off);
+            if (lane >= off) incl += t;
+        }
+        if (lane == 63) wsum[wave] = incl;
         __syncthreads();
-        if (tid < 64) {
-            const bool need = tid < QG && st[tid].cnt + TILE > a.cap;
-            const uint64_t m = __ballot(need);
-            if (tid == 0) cmask = (uint32_t)m;
-        }
-        __syncthreads();
-        const uint32_t m = cmask;
-        for (int qq = 0; qq < QG; qq++) {
-            if (!(m & (1u << qq))) continue;
-            topk_compact(keys + (int64_t)qq * a.cap, &st[qq], a.k);
-            if (tid == 0 && st[qq].tau && q0 + qq < a.nq) atomicMax(&a.gtau[q0 + qq], st[qq].tau);
-        }
-        if (tid < QG && q0 + tid < a.nq) {
-            const uint64_t tk = st[tid].tau > gnext ? st[tid].tau : gnext;
-            tau_s[tid] = tk;
-            bound_s[tid] = mq_bound<OP>(tk, qcs[tid], SMALL);
-            gnext = __hip_atomic_load(&a.gtau[q0 + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        int before = carry;
+        for (int j = 0; j < wave; j++) before += wsum[j];
+        if (w < a.R) pre[w] = before + incl - c;
+        int total = 0;
+        for (int j = 0; j < NW; j++) total += wsum[j];
+        carry += total;
         __syncthreads();
     }
-    if (!topk) return;
-    // ---- publish k keys per query
-    for (int qq = 0; qq < QG; qq++) {
-        if (q0 + qq >= a.nq) break;
-        topk_compact(keys + (int64_t)qq * a.cap, &st[qq], a.k);
-        uint64_t* dst = a.partial + ((int64_t)(q0 + qq) * gridDim.x + blockIdx.x) * a.k;
-        const int c = st[qq].cnt;
-        for (int i = tid; i < a.k; i += 256) dst[i] = i < c ? keys[(int64_t)qq * a.cap + i] : 0ull;
-        if (tid == 0 && st[qq].tau) atomicMax(&a.gtau[q0 + qq], st[qq].tau);
+    const int M = carry;
+
+    int fill = a.bcnt[q];
+    for (int i = tid; i < fill; i += NT) buf[i] = a.best[(int64_t)q * k + i];
+    __syncthreads();
+
+    auto compact = [&]() {
+        uint64_t prefix, pmask;
+        block_radix_prefix(buf, fill, k, ss, prefix, pmask);
+        uint64_t v[KPT];
+        uint32_t keep = 0;
+#pragma unroll
+        for (int j = 0; j < KPT; j++) {
+            const int i = tid + NT * j;
+            v[j] = i < fill ? buf[i] : 0ull;
+            if (i < fill && (v[j] & pmask) >= prefix) keep |= 1u << j;
+        }
+        if (tid == 0) wpos = 0;
         __syncthreads();
+#pragma unroll
+        for (int j = 0; j < KPT; j++)
+            if (keep & (1u << j)) buf[atomicAdd(&wpos, 1)] = v[j];
+        __syncthreads();
+        fill = k;
+    };
+
+    const uint64_t* regq = a.regions + (int64_t)q * a.rc;  // region w at regq + w*nq*rc
+    for (int base = 0; base < M;) {
+        const int take = (M - base) < (LCAP - fill) ? (M - base) : (LCAP - fill);
+        // batches of 8 independent loads per thread keep many in flight
+        for (int j0 = 0; j0 < take; j0 += 8 * NT) {
+            uint64_t v[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int j = j0 + t * NT + tid;
+                v[t] = 0;
+                if (j < take) {
+                    const int g = base + j;
+                    int lo = 0, hi = a.R;  // last region w with pre[w] <= g
+                    while (hi - lo > 1) {
+                        const int mid = (lo + hi) >> 1;
+                        if (pre[mid] <= g) lo = mid;
+                        else hi = mid;
+                    }
+                    v[t] = regq[(int64_t)lo * a.nq * a.rc + (g - pre[lo])];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int j = j0 + t * NT + tid;
+                if (j < take) buf[fill + j] = v[t];
+            }
+        }
+        __syncthreads();
+        fill += take;
+        base += take;
+        if (fill > k && (fill == LCAP || base == M)) compact();
+    }
+    if (fill > k) compact();
+
+    // threshold for the next pass: the k-th key once k keys exist
+    if (tid == 0) minkey = ~0ull;
+    __syncthreads();
+    if (fill == k) {
+        uint64_t lo = ~0ull;
+        for (int i = tid; i < fill; i += NT) lo = buf[i] < lo ? buf[i] : lo;
+        if (lo != ~0ull) atomicMin(&minkey, (unsigned long long)lo);
+    }
+    topk_sort(buf, fill);  // its barriers also order the minimum before its use
+    if (tid == 0) {
+        a.bcnt[q] = fill;
+        a.tau[q] = fill == k ? (uint64_t)minkey : 0ull;
+    }
+    if (a.out_ids) {
+        for (int i = tid; i < k; i += NT) {
+            const uint64_t key = i < fill ? buf[i] : 0ull;
+            a.out_ids[(int64_t)q * k + i] = key ? (int32_t)key_index(key) : -1;
+            if (a.out_scores) a.out_scores[(int64_t)q * k + i] = key ? key_score(key, a.smallest) : 0.0f;
+        }
+    } else {
+        for (int i = tid; i < fill; i += NT) a.best[(int64_t)q * k + i] = buf[i];
     }
 }
 
-// Zero the per-query global thresholds before a call (a fill kernel, not a
-// memset node, so a captured graph replays it reliably).
-__global__ void mq_clear_kernel(unsigned long long* gtau, int nq) {
+// Reset the per-query pass state before a call (a fill kernel, not a memset
+// node, so a captured graph replays it reliably).
+__global__ void mq_clear_kernel(uint64_t* tau, int* bcnt, int nq) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < nq) gtau[i] = 0ull;
+    if (i < nq) {
+        tau[i] = 0ull;
+        bcnt[i] = 0;
+    }
 }
 
 // ----------------------------------------------------------------- hosts
 
-template <int OP, int ENC, int QG, bool SMALL, bool TOPK>
-static hipError_t launch_mq_ks(const MqArgs& a, dim3 grid, size_t lds, hipStream_t s, int ks) {
-#define MANTA_MQ(KSV, TJV)                                                                                   \
-    if (ks == (KSV)) {                                                                                       \
-        hipLaunchKernelGGL((mq_q8_kernel<OP, ENC, QG, KSV, TJV, SMALL, TOPK>), grid, dim3(256), lds, s, a); \
-        return hipGetLastError();                                                                            \
+// Register budget: NA*KS*4 VGPRs of resident A fragments plus the staged
+// chunk (4 VGPRs per 16-byte load per thread) must leave room for the
+// accumulators and the epilogue at two waves per SIMD.
+static constexpr bool mq_valid(int na, int wq, int ks) {
+    return (na == 2 && wq == 4 && ks <= 12) || (na == 1 && wq == 4) || (na == 2 && wq == 1 && ks <= 4) ||
+           (na == 1 && wq == 2 && ks >= 8);
+}
+
+MqShape mq_shape(int op, int ks, int64_t nq) {
+    MqShape s;
+    s.ks = ks;
+    const int qpb = op == OP_DOT ? 32 : 16;
+    if (nq >= 8 * qpb && ks <= 12) {
+        s.na = 2, s.wq = 4;
+    } else if (nq >= 4 * qpb) {
+        s.na = 1, s.wq = 4;
+    } else if (ks <= 4) {
+        s.na = 2, s.wq = 1;
+    } else {
+        s.na = 1, s.wq = 2;
     }
-    MANTA_MQ(2, 4)
-    MANTA_MQ(4, 4)
-    MANTA_MQ(8, 2)
-    MANTA_MQ(12, 1)
-    MANTA_MQ(16, 1)
-#undef MANTA_MQ
-    return hipErrorInvalidValue;
-}
-
-template <int OP, int ENC, int QG>
-static hipError_t launch_mq_mode(const MqArgs& a, dim3 grid, size_t lds, hipStream_t s, int ks) {
-    if (a.out_scores) return launch_mq_ks<OP, ENC, QG, false, false>(a, grid, lds, s, ks);
-    if (a.smallest) return launch_mq_ks<OP, ENC, QG, true, true>(a, grid, lds, s, ks);
-    return launch_mq_ks<OP, ENC, QG, false, true>(a, grid, lds, s, ks);
-}
-
-int mq_tile_rows(int ks) {
-    const int tj = ks <= 4 ? 4 : (ks <= 8 ? 2 : 1);
-    return 4 * tj * 32;
+    s.qg = s.wq * s.na * qpb;
+    const int nbw = s.wq == 4 ? 2 : 1;
+    const int nbuf = s.wq == 4 ? 2 : 3;
+    s.chunk = (4 / s.wq) * nbw * 32;
+    const int segs = (s.chunk * (ks * 32 + 16) + 1023) / 1024;
+    s.tile = ((segs + 3) / 4) * 4 * 1024;
+    const int narr = op == OP_DOT ? 1 : 2;
+    const int cpw = (narr * ((s.chunk + 63) / 64) + 3) / 4;
+    s.tile_bytes = nbuf * (s.tile + cpw * 4 * 256);  // chunk tiles + row constants
+    return s;
 }
 
 bool mq_supported_ks(int ks) { return ks == 2 || ks == 4 || ks == 8 || ks == 12 || ks == 16; }
 
-hipError_t launch_mq_q8(int op, int qg, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
-    const int ks = a.pitch / 32;
-    if (op == OP_DOT) return launch_mq_mode<OP_DOT, MQ_E8, 32>(a, grid, lds, s, ks);
-    if (op == OP_COSINE) {
-        if (qg == 16) return launch_mq_mode<OP_COSINE, MQ_E16, 16>(a, grid, lds, s, ks);
-        return launch_mq_mode<OP_COSINE, MQ_E16, 8>(a, grid, lds, s, ks);
+template <int OP, int ENC, int NA, int WQ, int MODE, bool SMALL, int KS>
+static hipError_t launch_mq_one(const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+    if constexpr (mq_valid(NA, WQ, KS)) {
+        hipLaunchKernelGGL((mq_scan_kernel<OP, ENC, KS, NA, WQ, MODE, SMALL>), grid, dim3(256), lds, s, a);
+        return hipGetLastError();
     }
-    if (qg == 16) return launch_mq_mode<OP_L2, MQ_E16, 16>(a, grid, lds, s, ks);
-    return launch_mq_mode<OP_L2, MQ_E16, 8>(a, grid, lds, s, ks);
+    return hipErrorInvalidValue;
 }
 
-hipError_t launch_mq_clear(unsigned long long* gtau, int nq, hipStream_t s) {
-    hipLaunchKernelGGL(mq_clear_kernel, dim3((nq + 255) / 256), dim3(256), 0, s, gtau, nq);
+template <int OP, int ENC, int NA, int WQ, int MODE, bool SMALL>
+static hipError_t launch_mq_ks(const MqArgs& a, int ks, dim3 grid, size_t lds, hipStream_t s) {
+    switch (ks) {
+        case 2: return launch_mq_one<OP, ENC, NA, WQ, MODE, SMALL, 2>(a, grid, lds, s);
+        case 4: return launch_mq_one<OP, ENC, NA, WQ, MODE, SMALL, 4>(a, grid, lds, s);
+        case 8: return launch_mq_one<OP, ENC, NA, WQ, MODE, SMALL, 8>(a, grid, lds, s);
+        case 12: return launch_mq_one<OP, ENC, NA, WQ, MODE, SMALL, 12>(a, grid, lds, s);
+        case 16: return launch_mq_one<OP, ENC, NA, WQ, MODE, SMALL, 16>(a, grid, lds, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int OP, int ENC, int NA, int WQ>
+static hipError_t launch_mq_mode(const MqArgs& a, int ks, dim3 grid, size_t lds, hipStream_t s) {
+    if (a.out_scores) return launch_mq_ks<OP, ENC, NA, WQ, MQ_SCORES, false>(a, ks, grid, lds, s);
+    if (a.smallest) return launch_mq_ks<OP, ENC, NA, WQ, MQ_APPEND, true>(a, ks, grid, lds, s);
+    return launch_mq_ks<OP, ENC, NA, WQ, MQ_APPEND, false>(a, ks, grid, lds, s);
+}
+
+template <int OP, int ENC>
+static hipError_t launch_mq_op(const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+    if (sh.na == 2 && sh.wq == 4) return launch_mq_mode<OP, ENC, 2, 4>(a, sh.ks, grid, lds, s);
+    if (sh.na == 1 && sh.wq == 4) return launch_mq_mode<OP, ENC, 1, 4>(a, sh.ks, grid, lds, s);
+    if (sh.na == 2 && sh.wq == 1) return launch_mq_mode<OP, ENC, 2, 1>(a, sh.ks, grid, lds, s);
+    if (sh.na == 1 && sh.wq == 2) return launch_mq_mode<OP, ENC, 1, 2>(a, sh.ks, grid, lds, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_mq_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+    if (op == OP_DOT) return launch_mq_op<OP_DOT, MQ_E8>(sh, a, grid, lds, s);
+    if (op == OP_COSINE) return launch_mq_op<OP_COSINE, MQ_E16>(sh, a, grid, lds, s);
+    return launch_mq_op<OP_L2, MQ_E16>(sh, a, grid, lds, s);
+}
+
+// Threads of the select kernel: 1024 (16K-key buffer) when a pass is
+// expected to leave more keys than the 256-thread, 4K-key buffer holds.
+int mq_select_threads(int64_t expect_keys) { return expect_keys > 3072 ? 1024 : 256; }
+
+size_t mq_select_lds(int threads, int R) { return (size_t)threads * 16 * 8 + (size_t)(R + 1) * 4; }
+
+hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s) {
+    const size_t lds = mq_select_lds(threads, a.R);
+    if (threads == 1024)
+        hipLaunchKernelGGL(mq_select_kernel<1024>, dim3((unsigned)a.nq), dim3(1024), lds, s, a);
+    else
+        hipLaunchKernelGGL(mq_select_kernel<256>, dim3((unsigned)a.nq), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_mq_clear(uint64_t* tau, int* bcnt, int nq, hipStream_t s) {
+    hipLaunchKernelGGL(mq_clear_kernel, dim3((nq + 255) / 256), dim3(256), 0, s, tau, bcnt, nq);
     return hipGetLastError();
 }
 

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -617,71 +618,102 @@ int launch_scan(MantaRocm* rt, const MantaRocmCandidates* c, int op, const ScanA
 namespace {
 
 // Multi-query plan: many queries against one shared q8 matrix go to the
-// matrix-core kernel (kernels_mq.hip); everything else streams one query per
-// workgroup.
-struct MqPlan {
-    bool use = false;
-    int qg = 0;          // queries per group
-    int groups = 0;
-    int tile = 0;        // candidate rows per tile
-    int cap = 0;         // reservoir keys per query
-    int64_t ranges = 0;  // grid.x
+// matrix-core kernels (kernels_mq.hip); everything else streams one query per
+// workgroup.  Top-k runs in passes over growing row prefixes: pass 0 keeps
+// every key of its rows, and each later pass starts from the k-th best key
+// of all earlier rows, so only a few times k keys per query survive a pass.
+struct MqPass {
+    int64_t begin = 0;
+    int64_t end = 0;
     int64_t rows_per_wg = 0;
-    size_t lds = 0;
+    int R = 0;
+    int select_threads = 256;
 };
 
-constexpr size_t kMqLdsBudget = 150 * 1024;
-constexpr size_t kMqLdsTwoPerCu = 78 * 1024;
+struct MqPlan {
+    bool use = false;
+    manta::MqShape sh;
+    int groups = 0;
+    int rc = 0;          // region capacity (keys per query and workgroup)
+    int rmax = 0;        // largest grid.x over the passes
+    size_t lds = 0;
+    std::vector<MqPass> passes;
+};
+
+constexpr int kMqWorkgroups = 512;     // two workgroups per CU of a 256-CU MI355X
+constexpr int64_t kMqSelectKeys = 16384;  // LDS keys of the select kernel
+
+MqPass mq_pass(int64_t begin, int64_t end, int chunk, int groups, int64_t max_rows_per_wg) {
+    MqPass p;
+    p.begin = begin;
+    p.end = end;
+    const int64_t chunks = (end - begin + chunk - 1) / chunk;
+    int64_t R = std::max<int64_t>(1, std::min<int64_t>(chunks, kMqWorkgroups / groups));
+    int64_t cpw = (chunks + R - 1) / R;
+    if (max_rows_per_wg > 0) cpw = std::max<int64_t>(1, std::min<int64_t>(cpw, max_rows_per_wg / chunk));
+    p.rows_per_wg = cpw * chunk;
+    p.R = (int)((chunks + cpw - 1) / cpw);
+    return p;
+}
 
 MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool topk) {
     MqPlan p;
     if (c->format != MANTA_ROCM_Q8_ROWS || c->sets != 1 || nq < 8) return p;
     if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
-    p.tile = manta::mq_tile_rows(c->pitch / 32);
-    const size_t arows = 32 * (size_t)(c->pitch + 16);
-    if (op == MANTA_ROCM_DOT) {
-        p.qg = 32;
-    } else {
-        p.qg = 16;
-    }
-    if (topk) {
-        // Reservoir keys per query: room for k plus one tile of offers, with
-        // slack so compactions stay rare; largest that fits the LDS budget.
-        auto lds_for = [&](int qg, int64_t cap) { return arows + (size_t)qg * (16 + (size_t)cap * 8); };
-        const int64_t need = k + p.tile;
-        if (need > manta::kMaxCapKeys) return p;
-        const int qg_min = op == MANTA_ROCM_DOT ? 32 : 8;
-        int64_t cap = std::min<int64_t>(manta::kMaxCapKeys, std::max<int64_t>(256, 2 * k + 2 * p.tile));
-        while (p.qg > qg_min && lds_for(p.qg, cap) > kMqLdsBudget) p.qg >>= 1;
-        while (cap > need && lds_for(p.qg, cap) > kMqLdsBudget) cap = std::max(need, cap - 256);
-        // prefer two workgroups per CU when the smaller reservoir still fits
-        const int64_t cap2 = std::max<int64_t>(need, 256);
-        if (lds_for(p.qg, cap) > kMqLdsTwoPerCu && lds_for(p.qg, cap2) <= kMqLdsTwoPerCu) cap = cap2;
-        if (lds_for(p.qg, cap) > kMqLdsBudget) return p;
-        p.cap = (int)cap;
-        p.lds = lds_for(p.qg, cap);
-    } else {
-        p.lds = arows + (size_t)p.qg * 16;
-    }
-    p.groups = (int)((nq + p.qg - 1) / p.qg);
-    const int per_cu = p.lds > kMqLdsTwoPerCu ? 1 : 2;
-    const int64_t tiles = (c->n + p.tile - 1) / p.tile;
-    int64_t ranges = std::max<int64_t>(8, (256 * per_cu / p.groups) / 8 * 8);
-    ranges = std::min<int64_t>(ranges, tiles);
-    p.rows_per_wg = ((tiles + ranges - 1) / ranges) * p.tile;
-    p.ranges = (c->n + p.rows_per_wg - 1) / p.rows_per_wg;
+    p.sh = manta::mq_shape(op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE
+                                                                                             : manta::OP_L2),
+                           c->pitch / 32, nq);
+    p.groups = (int)((nq + p.sh.qg - 1) / p.sh.qg);
     if (p.groups > 65535) return p;
+    const int chunk = p.sh.chunk;
+    if (!topk) {
+        p.passes.push_back(mq_pass(0, c->n, chunk, p.groups, 0));
+        p.rmax = p.passes[0].R;
+        p.lds = (size_t)p.sh.tile_bytes;
+        p.use = true;
+        return p;
+    }
+    // region: the best k after a compaction plus one chunk of appends, with
+    // slack so a compaction frees at least k slots
+    p.rc = (int)(((2 * k + 2 * chunk + 64) + 63) / 64 * 64);
+    p.lds = (size_t)p.sh.tile_bytes + ((size_t)p.rc * 8 > (size_t)p.sh.tile ? (size_t)p.rc * 8 : 0);
+    // pass 0: everything is kept, so a workgroup takes at most rc - 2*chunk rows
+    int64_t s = std::min<int64_t>(c->n, std::max<int64_t>(8 * k, 4096));
+    p.passes.push_back(mq_pass(0, s, chunk, p.groups, p.rc - 2 * chunk));
+    p.passes.back().select_threads = manta::mq_select_threads(s);
+    if (s < c->n) {
+        // later passes grow the prefix by g: about k*g keys per query reach
+        // the select.  Fewest passes the select's buffer allows, then the
+        // smallest g that still needs no more of them.
+        const double span = (double)c->n / (double)s;
+        const double gmax = std::max(4.0, (double)kMqSelectKeys / (double)k);
+        const int npass = std::max(1, (int)std::ceil(std::log(span) / std::log(gmax) - 1e-9));
+        const double g = std::pow(span, 1.0 / npass);
+        for (int i = 0; i < npass; i++) {
+            const int64_t e = i + 1 == npass ? c->n : std::min<int64_t>(c->n, (int64_t)std::ceil(s * g));
+            if (e <= s) continue;
+            p.passes.push_back(mq_pass(s, e, chunk, p.groups, 0));
+            p.passes.back().select_threads = manta::mq_select_threads(k + (int64_t)(k * (g - 1.0) * 1.5));
+            s = e;
+        }
+    }
+    for (const MqPass& ps : p.passes) p.rmax = std::max(p.rmax, ps.R);
+    // the kernels index regions with 32-bit offsets
+    if ((int64_t)nq * p.rmax * p.rc >= ((int64_t)1 << 31)) return p;
     p.use = true;
     return p;
 }
 
-// Encode queries to the global digit planes, then run the multi-query kernel.
+// Encode queries to the global digit planes, then run the multi-query passes.
 int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const uint16_t* q, int64_t nq,
            int64_t k, const MqPlan& p, float* out_scores, int32_t* out_ids, float* out_topk_scores,
            char** err) {
     const size_t plane = (size_t)nq * c->pitch;
-    const size_t parts = out_scores ? 0 : (size_t)nq * p.ranges * k;
-    size_t need = 3 * (plane + 256) + (size_t)nq * sizeof(QConst) + (size_t)nq * 8 + parts * 8 + 2048;
+    const bool topk = out_scores == nullptr;
+    const size_t regions = topk ? (size_t)nq * p.rmax * p.rc : 0;
+    const size_t counts = topk ? (size_t)nq * p.rmax : 0;
+    size_t need = 3 * (plane + 256) + (size_t)nq * sizeof(QConst) + 256 + (size_t)nq * 12 + 512 +
+                  (size_t)nq * (size_t)k * 8 + 256 + regions * 8 + 256 + counts * 4 + 256;
     int rc = ensure_workspace(rt, need, err);
     if (rc) return rc;
     Carver cv(rt->ws);
@@ -689,8 +721,11 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
     int8_t* hi = cv.take<int8_t>(plane);
     int8_t* lo = cv.take<int8_t>(plane);
     QConst* qc = cv.take<QConst>((size_t)nq);
-    unsigned long long* gtau = cv.take<unsigned long long>((size_t)nq);
-    uint64_t* partial = cv.take<uint64_t>(parts ? parts : 1);
+    uint64_t* tau = cv.take<uint64_t>((size_t)nq);
+    int* bcnt = cv.take<int>((size_t)nq);
+    uint64_t* best = cv.take<uint64_t>(topk ? (size_t)nq * k : 1);
+    uint64_t* reg = cv.take<uint64_t>(regions ? regions : 1);
+    int* cnt = cv.take<int>(counts ? counts : 1);
     const int e16 = op != MANTA_ROCM_DOT;
     LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, c->pitch, e16, c8, hi, lo, qc, rt->stream),
                "query_encode");
@@ -706,22 +741,48 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
     a.qhi = hi;
     a.qlo = lo;
     a.qconst = qc;
-    a.rows_per_wg = p.rows_per_wg;
-    a.partial = partial;
-    a.gtau = gtau;
-    a.out_scores = out_scores;
+    a.tau = tau;
+    a.regions = reg;
+    a.counts = cnt;
+    a.rc = p.rc;
     a.k = (int)k;
-    a.cap = p.cap;
+    a.out_scores = out_scores;
     a.smallest = order == MANTA_ROCM_SMALLEST;
-    if (!out_scores)
-        LAUNCH_TRY(manta::launch_mq_clear(gtau, (int)nq, rt->stream), "mq_clear");
-    LAUNCH_TRY(manta::launch_mq_q8(op, p.qg, a, dim3((unsigned)p.ranges, (unsigned)p.groups), p.lds, rt->stream),
-               "mq_scan");
-    if (!out_scores) {
-        const int mcap = cap_for_k(k);
-        LAUNCH_TRY(manta::launch_topk_merge(partial, nq, p.ranges * k, (int)k, mcap, a.smallest, out_ids,
-                                            out_topk_scores, rt->stream),
-                   "topk_merge");
+    const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
+    if (!topk) {
+        const MqPass& ps = p.passes[0];
+        a.row_begin = ps.begin;
+        a.row_end = ps.end;
+        a.rows_per_wg = ps.rows_per_wg;
+        a.R = ps.R;
+        LAUNCH_TRY(manta::launch_mq_scan(dop, p.sh, a, dim3((unsigned)ps.R, (unsigned)p.groups), p.lds, rt->stream),
+                   "mq_scan");
+        return MANTA_ROCM_OK;
+    }
+    LAUNCH_TRY(manta::launch_mq_clear(tau, bcnt, (int)nq, rt->stream), "mq_clear");
+    manta::MqSelectArgs sa{};
+    sa.regions = reg;
+    sa.counts = cnt;
+    sa.rc = p.rc;
+    sa.best = best;
+    sa.bcnt = bcnt;
+    sa.tau = tau;
+    sa.k = (int)k;
+    sa.nq = (int)nq;
+    sa.smallest = a.smallest;
+    for (size_t i = 0; i < p.passes.size(); i++) {
+        const MqPass& ps = p.passes[i];
+        a.row_begin = ps.begin;
+        a.row_end = ps.end;
+        a.rows_per_wg = ps.rows_per_wg;
+        a.R = ps.R;
+        LAUNCH_TRY(manta::launch_mq_scan(dop, p.sh, a, dim3((unsigned)ps.R, (unsigned)p.groups), p.lds, rt->stream),
+                   "mq_scan");
+        sa.R = ps.R;
+        const bool last = i + 1 == p.passes.size();
+        sa.out_ids = last ? out_ids : nullptr;
+        sa.out_scores = last ? out_topk_scores : nullptr;
+        LAUNCH_TRY(manta::launch_mq_select(sa, ps.select_threads, rt->stream), "mq_select");
     }
     return MANTA_ROCM_OK;
 }

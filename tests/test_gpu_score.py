@@ -201,3 +201,54 @@ def test_multi_query_repeated_calls_are_identical(rt):
         want = orc.topk(orc.score_q8("l2_distance", q, codes[0], scales[0]), 100, smallest=True)
         np.testing.assert_array_equal(ids.download(), want)
         cands.close()
+
+
+def _ordered_case(op, nq, n, d, seed):
+    """Every row holds the same codes; only the scale changes, so each query
+    ranks the rows by index -- worst first.  Each pass's threshold then lets
+    every later row through: regions fill up and are compacted inside the
+    scan kernel, and the select streams more keys than its LDS buffer."""
+    rng = np.random.default_rng(seed)
+    base = rng.standard_normal(d)
+    q = orc.f32_to_f16((base + 0.05 * rng.standard_normal((nq, d))).astype(np.float32))
+    codes1, scale1 = orc.pack_q8_rows((base / np.linalg.norm(base)).astype(np.float32).reshape(1, -1))
+    codes = np.repeat(codes1, n, axis=0)
+    if op == "l2_distance":
+        # scales below the distance minimum: distance falls with the index
+        # the row is scale * codes ~ scale/scale1 * unit(base); its distance
+        # to a query near base falls while scale/scale1 stays below |base|
+        smax = 0.9 * scale1[0] * np.linalg.norm(base)
+        scales = (smax * (np.arange(n) + 1) / n).astype(np.float32)
+    else:
+        scales = (scale1[0] * (1.0 + np.arange(n) / n)).astype(np.float32)
+    return q, codes, scales
+
+
+@pytest.mark.parametrize("op,smallest", [("dot", False), ("l2_distance", True)])
+@pytest.mark.parametrize("k", [7, 100, 1000])
+def test_multi_query_adversarial_row_order(rt, op, smallest, k):
+    nq, n, d = 24, 300000, 128
+    q, codes, scales = _ordered_case(op, nq, n, d, k)
+    cands = rt.bind_q8(codes, scales)
+    ids, sc, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    want_s = orc.score_q8(op, q, codes, scales)
+    want_ids = orc.topk(want_s, k, smallest=smallest)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    cands.close()
+
+
+@pytest.mark.parametrize("op", ["dot", "cosine", "l2_distance"])
+def test_multi_query_all_ties(rt, op):
+    """Identical rows: every score ties, so the lowest indices win."""
+    nq, n, d, k = 16, 50000, 256, 300
+    q = synth.normal_f16(5, 0, nq, d, 1.0, normalize=True)
+    codes1, scale1 = synth.q8_rows(5, 1, 1, d, normalize=True)
+    codes = np.repeat(codes1, n, axis=0)
+    scales = np.repeat(scale1, n)
+    cands = rt.bind_q8(codes, scales)
+    ids, _, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=(op == "l2_distance"))
+    want = orc.topk(orc.score_q8(op, q, codes, scales), k, smallest=(op == "l2_distance"))
+    np.testing.assert_array_equal(ids.download(), want)
+    np.testing.assert_array_equal(want, np.tile(np.arange(k), (nq, 1)))
+    cands.close()
