@@ -154,17 +154,38 @@ __device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, Se
     pmask_out = pmask;
 }
 
+// Chunk tiles per workgroup: as many (2..4) as fit in about 72 KB of LDS
+// (two workgroups per CU), and at most as many as s_waitcnt can count.
+static constexpr int mq_nbuf(int tile_and_consts, int loads_per_chunk) {
+    int n = 73728 / tile_and_consts;
+    n = n > 4 ? 4 : n;
+    while (n > 2 && (n - 2) * loads_per_chunk > 63) n--;
+    return n < 2 ? 2 : n;
+}
+
+// s_waitcnt vmcnt(J*VPW) + s_barrier when at least J chunks were issued after
+// the current one, else the next smaller J (a smaller count waits longer,
+// never shorter).
+template <int VPW, int J>
+__device__ __forceinline__ void mq_wait_barrier(int64_t after) {
+    if constexpr (J <= 0) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+        if (after >= J)
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(J * VPW) : "memory");
+        else
+            mq_wait_barrier<VPW, J - 1>(after);
+    }
+}
+
 template <int OP, int ENC, int KS, int NA, int WQ, int MODE, bool SMALL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mq_scan_kernel(MqArgs a) {
     constexpr int PITCH = KS * 32;           // bytes per candidate row
     constexpr int P = PITCH + 16;            // LDS row pitch (padding spreads banks)
     constexpr int WR = 4 / WQ;               // waves splitting the rows of a chunk (WQ: 1, 2 or 4)
-    // 4 waves sharing rows (WQ = 4): 64-row chunks, two tiles (chunk c+1 in
-    // flight), two workgroups per CU.  Waves splitting rows: 32 rows per wave,
-    // three tiles (chunks c+1 and c+2 in flight) to cover HBM latency.
-    constexpr int NBW = WQ == 4 ? 2 : 1;     // 32-row blocks per wave per chunk
-    constexpr int NBUF = WQ == 4 ? 2 : 3;    // LDS chunk tiles
-    constexpr int CHUNK = WR * NBW * 32;     // rows per chunk
+    // One 32-row block per wave per chunk (WR*32 rows), two workgroups per
+    // CU: chunks c+1 .. c+NBUF-1 are in flight while chunk c is multiplied.
+    constexpr int CHUNK = WR * 32;                   // rows per chunk
     constexpr int SEGS = (CHUNK * P + 1023) / 1024;  // 1 KB LDS segments per chunk tile
     constexpr int DPW = (SEGS + 3) / 4;              // 16-byte direct-to-LDS loads per wave per chunk
     constexpr int TILE = DPW * 4 * 1024;             // LDS bytes per tile
@@ -173,6 +194,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     constexpr int CPW = (NARR * CSA + 3) / 4;        // 4-byte direct-to-LDS loads per wave per chunk
     constexpr int CTILE = CPW * 4 * 256;             // LDS bytes of a chunk's per-row constants
     constexpr int VPW = DPW + CPW;                   // direct-to-LDS loads per wave per chunk
+    constexpr int NBUF = mq_nbuf(TILE + CTILE, VPW); // LDS chunk tiles
     constexpr int QPB = ENC == MQ_E8 ? 32 : 16;  // queries per A block
     constexpr int QPW = NA * QPB;                // queries per wave
     constexpr int QG = WQ * QPW;                 // queries per workgroup
@@ -302,17 +324,129 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     // it would wait for them (and with them every chunk load in flight) at
     // their first use inside the loop, in every iteration.
     __builtin_amdgcn_s_waitcnt(0);
-    if (r0 < r1) {
-        issue_chunk(r0, 0);
-        if (NBUF == 3 && r0 + CHUNK < r1) issue_chunk(r0 + CHUNK, 1);
-    }
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; j++)
+        if (r0 + j * CHUNK < r1) issue_chunk(r0 + j * CHUNK, j);
 
+    // MFMAs of one 32-row block: B fragments from the LDS tile, A resident.
+    auto multiply = [&](const uint8_t* tile, v16i (&acc)[NA]) {
+        v16i ch[NA][NC];
+#pragma unroll
+        for (int na = 0; na < NA; na++)
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) ch[na][c][r] = 0;
+        const uint8_t* bp = tile + (wr * 32 + (lane & 31)) * P + half * 16;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const v4i bf = *(const v4i*)(bp + s * 32);
+#pragma unroll
+            for (int na = 0; na < NA; na++)
+                ch[na][s % NC] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[na][s], bf, ch[na][s % NC], 0, 0, 0);
+        }
+#pragma unroll
+        for (int na = 0; na < NA; na++) {
+            acc[na] = ch[na][0];
+            if (NC > 1) acc[na] += ch[na][NC - 1];
+        }
+    };
+
+    // Per-query values of one A block's slots: slot u's query is
+    // lq = lq0 + 8*(u/4) + u%4, so four slots read one float4 from LDS.
+    struct SlotVals {
+        float bq[QPL], qa[QPL], qcv[QPL];
+    };
+    auto slot_vals = [&](int na, SlotVals& v) {
+        const int lq0 = wq * QPW + na * QPB + 4 * half;
+#pragma unroll
+        for (int m = 0; m < QPL / 4; m++) {
+            const float4 b4 = *(const float4*)&bnd_s[lq0 + 8 * m];
+            v.bq[4 * m] = b4.x, v.bq[4 * m + 1] = b4.y, v.bq[4 * m + 2] = b4.z, v.bq[4 * m + 3] = b4.w;
+            if (OP != OP_DOT) {
+                const float4 a4 = *(const float4*)&qa_s[lq0 + 8 * m];
+                v.qa[4 * m] = a4.x, v.qa[4 * m + 1] = a4.y, v.qa[4 * m + 2] = a4.z, v.qa[4 * m + 3] = a4.w;
+            }
+            if (OP == OP_L2) {
+                const float4 c4 = *(const float4*)&qc_s[lq0 + 8 * m];
+                v.qcv[4 * m] = c4.x, v.qcv[4 * m + 1] = c4.y, v.qcv[4 * m + 2] = c4.z, v.qcv[4 * m + 3] = c4.w;
+            }
+        }
+    };
+    // pre-scores: dot s*acc, l2 dist^2, cosine q.d (exact f32 steps)
+    auto pre_of = [&](const v16i& accs, const SlotVals& v, int u, float scale, float rowc) {
+        const int r = slot_r(u);
+        if (OP == OP_DOT) return fmul_rn(scale, (float)accs[r]);
+        const float dotf = __fmaf_rn(256.0f, (float)accs[r], (float)accs[r + 4]);
+        const float qd = fmul_rn(fmul_rn(scale, v.qa[u]), dotf);
+        return OP == OP_L2 ? fsub_rn(fadd_rn(v.qcv[u], rowc), fmul_rn(2.0f, qd)) : qd;
+    };
+    auto keep_of = [&](const SlotVals& v, int u, float p, float rowc) {
+        const float bv = OP == OP_COSINE ? fmul_rn(v.bq[u], rowc) : v.bq[u];
+        return SMALL ? !(p > bv) : !(p < bv);
+    };
+    auto score_of = [&](float p, int lq, float rowc) {
+        if (OP == OP_DOT) return fdiv_rn(fmul_rn(p, qcs[lq].a), 127.0f);
+        if (OP == OP_COSINE) {
+            const float den = fmul_rn(qcs[lq].b, rowc);
+            return den == 0.0f ? 0.0f : fdiv_rn(p, den);
+        }
+        return fsqrt_rn(p < 0.0f ? 0.0f : p);
+    };
+    // Branch-free filter of one block: does any slot of this lane pass?
+    auto filter_any = [&](const v16i (&acc)[NA], int64_t row, float scale, float rowc) {
+        bool any = false;
+#pragma unroll
+        for (int na = 0; na < NA; na++) {
+            SlotVals v;
+            slot_vals(na, v);
+#pragma unroll
+            for (int u = 0; u < QPL; u++) any |= keep_of(v, u, pre_of(acc[na], v, u, scale, rowc), rowc);
+        }
+        return any && row < r1;
+    };
+    // Exact scores and keys of the survivors (a wave with at least one).
+    auto survivors = [&](const v16i (&acc)[NA], int64_t row, float scale, float rowc) {
+        if (row >= r1) return;
+#pragma unroll
+        for (int na = 0; na < NA; na++) {
+            SlotVals v;
+            slot_vals(na, v);
+#pragma unroll
+            for (int u = 0; u < QPL; u++) {
+                const float p = pre_of(acc[na], v, u, scale, rowc);
+                if (keep_of(v, u, p, rowc)) {
+                    const int lq = slot_lq(na, u);
+                    const uint64_t key = make_key(score_of(p, lq, rowc), (uint32_t)row, SMALL);
+                    if (key > tau_s[lq]) {
+                        const int pos = atomicAdd(&cnt_s[lq], 1);
+                        wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = key;
+                    }
+                }
+            }
+        }
+    };
+    // Score-matrix stores of one block.
+    auto store_scores = [&](const v16i (&acc)[NA], int64_t row, float scale, float rowc) {
+        if (row >= r1) return;
+#pragma unroll
+        for (int na = 0; na < NA; na++) {
+            SlotVals v;
+            slot_vals(na, v);
+#pragma unroll
+            for (int u = 0; u < QPL; u++) {
+                if (!((live[na] >> u) & 1)) continue;
+                const int lq = slot_lq(na, u);
+                a.out_scores[(int64_t)(q0 + lq) * a.n + row] = score_of(pre_of(acc[na], v, u, scale, rowc), lq, rowc);
+            }
+        }
+    };
     int buf = 0, par = 0;
     for (int64_t c0 = r0; c0 < r1; c0 += CHUNK, buf = buf == NBUF - 1 ? 0 : buf + 1, par ^= 1) {
         if (APPEND) {
             // Flag regions that might not take one more chunk of keys.  Read
             // before the barrier, a count may still miss up to CHUNK keys of
-            // the previous chunk from other waves, hence the margin of two
+            // the chunk other waves are filtering, hence the margin of two
             // chunks (rc >= k + 2*CHUNK + 1).  Parity buffers: the flags
             // written here are read after this barrier, while the next
             // chunk's flags go to the other buffer.
@@ -322,15 +456,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                 if (lane == 0) flags[par][w] = m;
             }
         }
-        // This wave's loads of chunk c are done once at most the VPW loads of
-        // chunk c+1 are outstanding (NBUF == 3; loads complete in order); the
-        // barrier extends that to every wave's loads, retires the previous
-        // chunk's tile reads before that tile is refilled, and publishes the
-        // flags.  (A plain __syncthreads would also wait for chunk c+1.)
-        if (NBUF == 3 && c0 + CHUNK < r1)
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(VPW) : "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // This wave's loads of chunk c are done once at most the loads of the
+        // chunks issued after it are outstanding (loads complete in order);
+        // the barrier extends that to every wave's loads, retires the
+        // previous chunk's tile reads before that tile is refilled, and
+        // publishes the flags.  (A plain __syncthreads would wait for every
+        // chunk in flight.)
+        mq_wait_barrier<VPW, NBUF - 2>((r1 - c0 - 1) / CHUNK);
         const int nbuf = buf == 0 ? NBUF - 1 : buf - 1;  // tile of chunk c+NBUF-1 (free now)
         if (APPEND) {
             // rare: compact full regions to their best k keys
@@ -373,110 +505,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
             }
         }
 
-        // Refill the free tile with chunk c+NBUF-1 now -- except that with
-        // three tiles the score matrix does it after this chunk's stores,
-        // which also count in vmcnt and would otherwise be waited for with it.
-        constexpr bool LATE = !APPEND && NBUF == 3;
-        if (!LATE && c0 + (NBUF - 1) * CHUNK < r1) issue_chunk(c0 + (NBUF - 1) * CHUNK, nbuf);
+        // Refill the free tile with chunk c+NBUF-1 now -- except that the
+        // score matrix does it after this chunk's stores, which also count
+        // in vmcnt and would otherwise be waited for with it.
+        if (APPEND && c0 + (NBUF - 1) * CHUNK < r1) issue_chunk(c0 + (NBUF - 1) * CHUNK, nbuf);
         const uint8_t* tile = tiles + buf * TILE;
         const float* ctile = consts + buf * (CTILE / 4);
-
-#pragma unroll
-        for (int b = 0; b < NBW; b++) {
-            const int blk = wr * NBW + b;
-            const int64_t row = c0 + blk * 32 + (lane & 31);
-            v16i acc[NA][NC];
-#pragma unroll
-            for (int na = 0; na < NA; na++)
-#pragma unroll
-                for (int ch = 0; ch < NC; ch++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) acc[na][ch][r] = 0;
-            // B fragments are read from LDS two K steps ahead of their MFMAs
-            const uint8_t* bp = tile + (blk * 32 + (lane & 31)) * P + half * 16;
-            v4i b0 = *(const v4i*)bp;
-            v4i b1 = KS > 1 ? *(const v4i*)(bp + 32) : b0;
-#pragma unroll
-            for (int s = 0; s < KS; s++) {
-                const v4i b2 = s + 2 < KS ? *(const v4i*)(bp + (s + 2) * 32) : b1;
-#pragma unroll
-                for (int na = 0; na < NA; na++)
-                    acc[na][s % NC] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[na][s], b0, acc[na][s % NC], 0, 0, 0);
-                b0 = b1;
-                b1 = b2;
-            }
-            if (row >= r1) continue;
-            const float scale = ctile[blk * 32 + (lane & 31)];
-            const float rowc = OP == OP_DOT ? 0.0f : ctile[CSA * 64 + blk * 32 + (lane & 31)];
-#pragma unroll
-            for (int na = 0; na < NA; na++) {
-                v16i accs = acc[na][0];
-                if (NC > 1) accs += acc[na][NC - 1];
-                // slot u's query is lq = lq0 + 8*(u/4) + u%4: the per-query
-                // values of four slots are one float4 in LDS
-                const int lq0 = wq * QPW + na * QPB + 4 * half;
-                float bq[QPL], qa[QPL], qcv[QPL];
-#pragma unroll
-                for (int m = 0; m < QPL / 4; m++) {
-                    const float4 b4 = *(const float4*)&bnd_s[lq0 + 8 * m];
-                    bq[4 * m] = b4.x, bq[4 * m + 1] = b4.y, bq[4 * m + 2] = b4.z, bq[4 * m + 3] = b4.w;
-                    if (OP != OP_DOT) {
-                        const float4 a4 = *(const float4*)&qa_s[lq0 + 8 * m];
-                        qa[4 * m] = a4.x, qa[4 * m + 1] = a4.y, qa[4 * m + 2] = a4.z, qa[4 * m + 3] = a4.w;
-                    }
-                    if (OP == OP_L2) {
-                        const float4 c4 = *(const float4*)&qc_s[lq0 + 8 * m];
-                        qcv[4 * m] = c4.x, qcv[4 * m + 1] = c4.y, qcv[4 * m + 2] = c4.z, qcv[4 * m + 3] = c4.w;
-                    }
-                }
-                // pre-scores: dot s*acc, l2 dist^2, cosine q.d (exact f32 steps)
-                auto pre_of = [&](int hi, int lo, int u) {
-                    if (OP == OP_DOT) return fmul_rn(scale, (float)hi);
-                    const float dotf = __fmaf_rn(256.0f, (float)hi, (float)lo);
-                    const float qd = fmul_rn(fmul_rn(scale, qa[u]), dotf);
-                    return OP == OP_L2 ? fsub_rn(fadd_rn(qcv[u], rowc), fmul_rn(2.0f, qd)) : qd;
-                };
-                auto score_of = [&](float v, int lq) {
-                    if (OP == OP_DOT) return fdiv_rn(fmul_rn(v, qcs[lq].a), 127.0f);
-                    if (OP == OP_COSINE) {
-                        const float den = fmul_rn(qcs[lq].b, rowc);
-                        return den == 0.0f ? 0.0f : fdiv_rn(v, den);
-                    }
-                    return fsqrt_rn(v < 0.0f ? 0.0f : v);
-                };
-                if (!APPEND) {
-                    // score matrix: every live slot
-#pragma unroll
-                    for (int u = 0; u < QPL; u++) {
-                        if (!((live[na] >> u) & 1)) continue;
-                        const int r = slot_r(u);
-                        const int lq = slot_lq(na, u);
-                        const float v = pre_of(accs[r], ENC == MQ_E8 ? 0 : accs[r + 4], u);
-                        a.out_scores[(int64_t)(q0 + lq) * a.n + row] = score_of(v, lq);
-                    }
-                    continue;
-                }
-                // filter: one compare per slot; the exact score and key are
-                // computed only where some lane of the wave survives (an
-                // exec-masked branch that the wave skips when none does)
-#pragma unroll
-                for (int u = 0; u < QPL; u++) {
-                    const int r = slot_r(u);
-                    const float p = pre_of(accs[r], ENC == MQ_E8 ? 0 : accs[r + 4], u);
-                    const float bv = OP == OP_COSINE ? fmul_rn(bq[u], rowc) : bq[u];
-                    const bool keep = SMALL ? !(p > bv) : !(p < bv);
-                    if (keep) {
-                        const int lq = slot_lq(na, u);
-                        const uint64_t key = make_key(score_of(p, lq), (uint32_t)row, SMALL);
-                        if (key > tau_s[lq]) {
-                            const int pos = atomicAdd(&cnt_s[lq], 1);
-                            wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = key;
-                        }
-                    }
-                }
-            }
+        const int64_t row = c0 + wr * 32 + (lane & 31);
+        const float scale = ctile[wr * 32 + (lane & 31)];
+        const float rowc = OP == OP_DOT ? 0.0f : ctile[CSA * 64 + wr * 32 + (lane & 31)];
+        // MFMAs of this wave's 32-row block, then its filter: one compare per
+        // slot without branches, and the exact scores and keys only in a wave
+        // that has a survivor
+        v16i acc[NA];
+        multiply(tile, acc);
+        if (APPEND) {
+            if (__ballot(filter_any(acc, row, scale, rowc))) survivors(acc, row, scale, rowc);
+        } else {
+            store_scores(acc, row, scale, rowc);
         }
-        if (LATE && c0 + 2 * CHUNK < r1) issue_chunk(c0 + 2 * CHUNK, nbuf);
+        if (!APPEND && c0 + (NBUF - 1) * CHUNK < r1) issue_chunk(c0 + (NBUF - 1) * CHUNK, nbuf);
     }
     if (!APPEND) return;
     __syncthreads();
@@ -648,14 +696,13 @@ MqShape mq_shape(int op, int ks, int64_t nq) {
         s.na = 1, s.wq = 2;
     }
     s.qg = s.wq * s.na * qpb;
-    const int nbw = s.wq == 4 ? 2 : 1;
-    const int nbuf = s.wq == 4 ? 2 : 3;
-    s.chunk = (4 / s.wq) * nbw * 32;
+    s.chunk = (4 / s.wq) * 32;
     const int segs = (s.chunk * (ks * 32 + 16) + 1023) / 1024;
     s.tile = ((segs + 3) / 4) * 4 * 1024;
     const int narr = op == OP_DOT ? 1 : 2;
-    const int cpw = (narr * ((s.chunk + 63) / 64) + 3) / 4;
-    s.tile_bytes = nbuf * (s.tile + cpw * 4 * 256);  // chunk tiles + row constants
+    const int ctile = ((narr * ((s.chunk + 63) / 64) + 3) / 4) * 4 * 256;
+    const int vpw = s.tile / 4096 + ctile / 1024;
+    s.tile_bytes = mq_nbuf(s.tile + ctile, vpw) * (s.tile + ctile);  // chunk tiles + row constants
     return s;
 }
 
@@ -706,7 +753,7 @@ hipError_t launch_mq_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid,
 
 // Threads of the select kernel: 1024 (16K-key buffer) when a pass is
 // expected to leave more keys than the 256-thread, 4K-key buffer holds.
-int mq_select_threads(int64_t expect_keys) { return expect_keys > 3072 ? 1024 : 256; }
+int mq_select_threads(int64_t expect_keys) { return expect_keys > 4096 ? 1024 : 256; }
 
 size_t mq_select_lds(int threads, int R) { return (size_t)threads * 16 * 8 + (size_t)(R + 1) * 4; }
 
