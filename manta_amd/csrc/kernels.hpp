@@ -104,6 +104,12 @@ struct MqShape {
 MqShape mq_shape(int op, int ks, int64_t nq);
 bool mq_supported_ks(int ks);
 hipError_t launch_mq_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
+// q4 blocks (kernels_mq4.hip): codes = packed nibbles [n][nb*16], scales =
+// f16 [n][nb] (passed through MqArgs.scales), qhi/qlo = E16 planes in the q4
+// nibble order [nq][nb*32]; MqShape.ks holds nb.
+MqShape mq4_shape(int op, int nb, int64_t nq);
+bool mq4_supported_nb(int nb);
+hipError_t launch_mq4_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
 int mq_select_threads(int64_t expect_keys);
 size_t mq_select_lds(int threads, int R);
 hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s);

@@ -118,7 +118,8 @@ __global__ __launch_bounds__(256) void query_encode_kernel(const uint16_t* __res
                                                            QConst* __restrict__ qc) {
     __shared__ QueryLds L;
     const int qi = blockIdx.x;
-    encode_query_block(q + (int64_t)qi * d, d, pitch, e16 ? ENC_E16 : ENC_E8, L);
+    // e16: 0 = E8 codes, 1 = E16 digit planes, 2 = E16 planes in the q4 nibble order
+    encode_query_block(q + (int64_t)qi * d, d, pitch, e16 == 2 ? ENC_E16_Q4 : (e16 ? ENC_E16 : ENC_E8), L);
     for (int c = threadIdx.x; c < pitch; c += 256) {
         if (e16) {
             hi[(int64_t)qi * pitch + c] = L.hi[c];

@@ -632,6 +632,7 @@ struct MqPass {
 
 struct MqPlan {
     bool use = false;
+    bool q4 = false;     // q4 blocks (kernels_mq4.hip), else q8 rows
     manta::MqShape sh;
     int groups = 0;
     int rc = 0;          // region capacity (keys per query and workgroup)
@@ -658,11 +659,16 @@ MqPass mq_pass(int64_t begin, int64_t end, int chunk, int groups, int64_t max_ro
 
 MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool topk) {
     MqPlan p;
-    if (c->format != MANTA_ROCM_Q8_ROWS || c->sets != 1 || nq < 8) return p;
-    if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
-    p.sh = manta::mq_shape(op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE
-                                                                                             : manta::OP_L2),
-                           c->pitch / 32, nq);
+    if (c->sets != 1 || nq < 8) return p;
+    const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
+    if (c->format == MANTA_ROCM_Q8_ROWS) {
+        if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
+        p.sh = manta::mq_shape(dop, c->pitch / 32, nq);
+    } else {
+        if (!manta::mq4_supported_nb(c->nb)) return p;
+        p.q4 = true;
+        p.sh = manta::mq4_shape(dop, c->nb, nq);
+    }
     p.groups = (int)((nq + p.sh.qg - 1) / p.sh.qg);
     if (p.groups > 65535) return p;
     const int chunk = p.sh.chunk;
@@ -704,11 +710,19 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
     return p;
 }
 
+hipError_t launch_mq_pass(const MqPlan& p, int dop, const manta::MqArgs& a, int R, hipStream_t s) {
+    const dim3 grid((unsigned)R, (unsigned)p.groups);
+    return p.q4 ? manta::launch_mq4_scan(dop, p.sh, a, grid, p.lds, s) : manta::launch_mq_scan(dop, p.sh, a, grid, p.lds, s);
+}
+
 // Encode queries to the global digit planes, then run the multi-query passes.
 int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const uint16_t* q, int64_t nq,
            int64_t k, const MqPlan& p, float* out_scores, int32_t* out_ids, float* out_topk_scores,
            char** err) {
-    const size_t plane = (size_t)nq * c->pitch;
+    // query planes: E8 codes or E16 digits, one row per query, as wide as a
+    // q8 row (pitch) or a q4 row in elements (d)
+    const int width = p.q4 ? (int)c->d : c->pitch;
+    const size_t plane = (size_t)nq * width;
     const bool topk = out_scores == nullptr;
     const size_t regions = topk ? (size_t)nq * p.rmax * p.rc : 0;
     const size_t counts = topk ? (size_t)nq * p.rmax : 0;
@@ -726,8 +740,8 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
     uint64_t* best = cv.take<uint64_t>(topk ? (size_t)nq * k : 1);
     uint64_t* reg = cv.take<uint64_t>(regions ? regions : 1);
     int* cnt = cv.take<int>(counts ? counts : 1);
-    const int e16 = op != MANTA_ROCM_DOT;
-    LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, c->pitch, e16, c8, hi, lo, qc, rt->stream),
+    const int e16 = p.q4 ? 2 : (op != MANTA_ROCM_DOT ? 1 : 0);
+    LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, width, e16, c8, hi, lo, qc, rt->stream),
                "query_encode");
     manta::MqArgs a{};
     a.codes = (const int8_t*)c->codes;
@@ -755,8 +769,7 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
         a.row_end = ps.end;
         a.rows_per_wg = ps.rows_per_wg;
         a.R = ps.R;
-        LAUNCH_TRY(manta::launch_mq_scan(dop, p.sh, a, dim3((unsigned)ps.R, (unsigned)p.groups), p.lds, rt->stream),
-                   "mq_scan");
+        LAUNCH_TRY(launch_mq_pass(p, dop, a, ps.R, rt->stream), "mq_scan");
         return MANTA_ROCM_OK;
     }
     LAUNCH_TRY(manta::launch_mq_clear(tau, bcnt, (int)nq, rt->stream), "mq_clear");
@@ -776,8 +789,7 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
         a.row_end = ps.end;
         a.rows_per_wg = ps.rows_per_wg;
         a.R = ps.R;
-        LAUNCH_TRY(manta::launch_mq_scan(dop, p.sh, a, dim3((unsigned)ps.R, (unsigned)p.groups), p.lds, rt->stream),
-                   "mq_scan");
+        LAUNCH_TRY(launch_mq_pass(p, dop, a, ps.R, rt->stream), "mq_scan");
         sa.R = ps.R;
         const bool last = i + 1 == p.passes.size();
         sa.out_ids = last ? out_ids : nullptr;

@@ -252,3 +252,59 @@ def test_multi_query_all_ties(rt, op):
     np.testing.assert_array_equal(ids.download(), want)
     np.testing.assert_array_equal(want, np.tile(np.arange(k), (nq, 1)))
     cands.close()
+
+
+# ---------------------------------------------------------------------------
+# Many queries against one shared q4 matrix (the q4 matrix-core path).
+
+def _q4_case(seed, nq, n, d, normalize=True):
+    q = synth.normal_f16(200 + seed, 0, nq, d, 1.0, normalize=normalize)
+    packed, s4 = synth.q4_rows(200 + seed, 1, n, d, normalize=normalize)
+    return q, packed, s4
+
+
+@pytest.mark.parametrize("op", ["cosine", "l2_distance", "dot"])
+@pytest.mark.parametrize("d", [32, 64, 384, 512])
+def test_q4_multi_query_score_matrix_bit_exact(rt, op, d):
+    nq, n = 40, 3000
+    q, packed, s4 = _q4_case(d, nq, n, d, normalize=(op != "l2_distance"))
+    cands = rt.bind_q4(packed, s4, d)
+    got = rt.score(cands, op, rt.to_device(q)).download()
+    np.testing.assert_array_equal(got, orc.score_q4(op, q, packed, s4, d))
+    cands.close()
+
+
+@pytest.mark.parametrize("op,smallest", [("cosine", False), ("l2_distance", True), ("dot", False), ("dot", True)])
+@pytest.mark.parametrize("nq,n,d,k", [(8, 3000, 32, 10), (37, 5000, 128, 50), (129, 4097, 384, 100),
+                                      (64, 20000, 256, 7), (16, 700, 512, 700), (9, 2000, 64, 1)])
+def test_q4_multi_query_topk_bit_exact(rt, op, smallest, nq, n, d, k):
+    q, packed, s4 = _q4_case(nq + n + d + k, nq, n, d, normalize=(op != "l2_distance"))
+    cands = rt.bind_q4(packed, s4, d)
+    ids, sc, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    want_s = orc.score_q4(op, q, packed, s4, d)
+    want_ids = orc.topk(want_s, k, smallest=smallest)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    cands.close()
+
+
+@pytest.mark.parametrize("k", [5, 100])
+def test_q4_multi_query_adversarial_row_order(rt, k):
+    """One row's nibbles repeated with block scales growing with the index
+    (rounded to f16, so runs of equal scores too): every pass lets the later
+    rows through, forcing region compaction and multi-round selects."""
+    nq, n, d = 20, 200000, 128
+    rng = np.random.default_rng(k)
+    base = rng.standard_normal(d).astype(np.float32)
+    q = orc.f32_to_f16((base + 0.05 * rng.standard_normal((nq, d))).reshape(nq, d).astype(np.float32))
+    packed1, s1 = orc.pack_q4_blocks(base.reshape(1, -1))
+    packed = np.repeat(packed1, n, axis=0)
+    grow = (1.0 + np.arange(n, dtype=np.float64) / n)[:, None]
+    s4 = orc.f32_to_f16((orc.f16_to_f32(s1) * grow).astype(np.float32))
+    cands = rt.bind_q4(packed, s4, d)
+    ids, sc, _ = rt.score_topk(cands, "dot", rt.to_device(q), k)
+    want_s = orc.score_q4("dot", q, packed, s4, d)
+    want_ids = orc.topk(want_s, k)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    cands.close()
