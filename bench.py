@@ -113,11 +113,17 @@ def _timed(rt, fn, steps, warmup, families):
     fam = {}
     for f in families:
         n, ms = rt.timing(f)
-        fam[f] = (n, ms / max(n, 1))
+        # (launches per step, average ms per launch, total ms per step)
+        fam[f] = (n / steps, ms / max(n, 1), ms / steps)
     _, all_ms = rt.timing(None)
     rt.set_timing(False)
     rt.timing(reset=True)
     return el / steps, fam, all_ms / steps
+
+
+def _kernels(fam) -> dict:
+    """Device time per step of each kernel family that ran."""
+    return {f: {"launches_per_step": v[0], "us_per_step": v[2] * 1000.0} for f, v in fam.items() if v[0]}
 
 
 def run_c1(rt, steps, warmup) -> dict:
@@ -158,20 +164,21 @@ def run_c2(rt, steps, warmup) -> dict:
     qd = rt.to_device(queries)
     ids = rt.empty((nq, k), np.int32)
     sc = rt.empty((nq, k), np.float32)
-    fams = ["q4_scan", "mq4_scan", "topk_merge", "query_encode"]
+    fams = ["mq_scan", "mq_select", "q4_scan", "topk_merge", "query_encode", "mq_clear"]
     step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "cosine", qd, k, out=(ids, sc, None)),
                                  steps, warmup, fams)
-    dom = max(fams, key=lambda f: fam[f][0] * fam[f][1])
+    dom = "mq_scan" if fam["mq_scan"][0] else "q4_scan"
     ops = 2.0 * nq * n * d
-    achieved = ops / (fam[dom][1] / 1000.0) / 1e12
+    achieved = ops / (fam[dom][2] / 1000.0) / 1e12
     cands.close()
     return {
         "workload": "c2_q4_cosine_top100", "shape": {"q": nq, "n": n, "d": d, "k": k},
         "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0,
-        "device_ms_per_step": dev_ms,
+        "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": F16_PEAK,
                      "unit": "TFLOP/s (algorithmic 2*Q*N*D over the f16 peak)", "frac": achieved / F16_PEAK,
-                     "avg_launch_us": fam[dom][1] * 1000.0},
+                     "scan_us_per_step": fam[dom][2] * 1000.0,
+                     "note": "all threshold passes of the scan together cover the N rows once"},
     }
 
 
@@ -188,21 +195,21 @@ def run_c3(rt, steps, warmup) -> dict:
     qd = rt.to_device(queries)
     ids = rt.empty((nq, k), np.int32)
     sc = rt.empty((nq, k), np.float32)
-    fams = ["mq_scan", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
+    fams = ["mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
     step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "l2_distance", qd, k, smallest=True,
                                                            out=(ids, sc, None)), steps, warmup, fams)
-    dom = max(fams, key=lambda f: fam[f][0] * fam[f][1])
+    dom = "mq_scan" if fam["mq_scan"][0] else "q8_scan"
     nbytes = n * (d + 4) + nq * d * 2 + nq * k * 8
-    achieved = nbytes / (fam[dom][1] / 1000.0) / 1e9
+    achieved = nbytes / (fam[dom][2] / 1000.0) / 1e9
     cands.close()
     return {
         "workload": "c3_q8_l2_smallest1000", "shape": {"q": nq, "n": n, "d": d, "k": k},
         "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0,
-        "device_ms_per_step": dev_ms,
+        "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK, "avg_launch_us": fam[dom][1] * 1000.0,
-                     "bytes_per_launch": nbytes},
-        "merge_us": fam["topk_merge"][1] * 1000.0,
+                     "frac": achieved / HBM_PEAK, "scan_us_per_step": fam[dom][2] * 1000.0,
+                     "bytes_per_step": nbytes,
+                     "note": "all threshold passes of the scan together cover the N rows once"},
     }
 
 
@@ -228,23 +235,24 @@ def run_c4(rt, steps, warmup) -> dict:
         rt.embed_pooled(td, md, tbd, pd, csd, out=emb)
         rt.score_topk(cands, "dot", emb, k, out=(ids, sc, None))
 
-    fams = ["embed", "embed_finalize", "mq_scan", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
+    fams = ["embed", "embed_finalize", "mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
     step_s, fam, dev_ms = _timed(rt, step, steps, warmup, fams)
     flops_a = 2.0 * b * t * d * e
     ops_b = 2.0 * b * n * d
     emb_t = flops_a / (fam["embed"][1] / 1000.0) / 1e12
     dom = "mq_scan" if fam["mq_scan"][0] else "q8_scan"
-    sc_t = ops_b / (fam[dom][1] / 1000.0) / 1e12
+    sc_t = ops_b / (fam[dom][2] / 1000.0) / 1e12
     cands.close()
     return {
         "workload": "c4_embed_q8proj_then_q8dot_top50", "shape": {"q": b, "t": t, "d": d, "n": n, "k": k},
         "value": b * n / step_s, "unit": "candidates/s (end to end, embed included)",
-        "ms_per_step": step_s * 1000.0, "device_ms_per_step": dev_ms,
+        "ms_per_step": step_s * 1000.0, "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         "embed": {"tokens_per_s_kernel": b * t / (fam["embed"][1] / 1000.0),
                   "roofline": {"bound": "mfma", "achieved": emb_t, "peak": F16_PEAK, "unit": "TFLOP/s",
                                "frac": emb_t / F16_PEAK, "avg_launch_us": fam["embed"][1] * 1000.0}},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": sc_t, "peak": I8_PEAK, "unit": "TOP/s",
-                     "frac": sc_t / I8_PEAK, "avg_launch_us": fam[dom][1] * 1000.0, "ops_per_launch": ops_b},
+                     "frac": sc_t / I8_PEAK, "scan_us_per_step": fam[dom][2] * 1000.0, "ops_per_step": ops_b,
+                     "note": "all threshold passes of the scan together cover the N rows once"},
     }
 
 
