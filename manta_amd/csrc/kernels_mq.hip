@@ -62,7 +62,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     // compaction scratch: the tile that is about to be refilled, or an extra
     // LDS area when rc keys do not fit in a tile
     uint64_t* scratch_extra = (uint64_t*)(smem + NBUF * (TILE + CTILE));
-    __shared__ QConst qcs[QG];
     __shared__ uint64_t tau_s[QG];
     // per-query values the epilogue reads four at a time (float4)
     __shared__ __attribute__((aligned(16))) float bnd_s[QG];  // pre-score bound
@@ -70,7 +69,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     __shared__ __attribute__((aligned(16))) float qc_s[QG];   // QConst.c
     __shared__ int cnt_s[QG];
     __shared__ uint64_t flags[2][NFW];  // double-buffered by chunk parity
-    __shared__ SelectShared ss;
+    __shared__ RadixShared ss;
     __shared__ int wpos;
     __shared__ unsigned long long minkey;
 
@@ -87,7 +86,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         const int q = q0 + i;
         const bool ok = q < a.nq;
         const QConst qc = ok ? a.qconst[q] : QConst{1.0f, 0.0f, 0.0f, 0.0f};
-        qcs[i] = qc;
         qa_s[i] = qc.a;
         qc_s[i] = qc.c;
         const uint64_t tk = (APPEND && ok) ? a.tau[q] : 0ull;
@@ -239,9 +237,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         return SMALL ? !(p > bv) : !(p < bv);
     };
     auto score_of = [&](float p, int lq, float rowc) {
-        if (OP == OP_DOT) return fdiv_rn(fmul_rn(p, qcs[lq].a), 127.0f);
+        if (OP == OP_DOT) return fdiv_rn(fmul_rn(p, qa_s[lq]), 127.0f);
         if (OP == OP_COSINE) {
-            const float den = fmul_rn(qcs[lq].b, rowc);
+            const float den = fmul_rn(a.qconst[q0 + lq].b, rowc);
             return den == 0.0f ? 0.0f : fdiv_rn(p, den);
         }
         return fsqrt_rn(p < 0.0f ? 0.0f : p);
@@ -350,7 +348,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                         cnt_s[lq] = a.k;
                         if (minkey > tau_s[lq]) {
                             tau_s[lq] = minkey;
-                            bnd_s[lq] = mq_bound<OP>(minkey, qcs[lq], SMALL);
+                            bnd_s[lq] = mq_bound<OP>(minkey, a.qconst[q0 + lq], SMALL);
                         }
                     }
                     __syncthreads();
@@ -400,7 +398,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint64_t* buf = (uint64_t*)smem;           // [LCAP]
     int* pre = (int*)(smem + LCAP * 8);        // [R + 1]
-    __shared__ SelectShared ss;
+    __shared__ RadixShared rs;
     __shared__ int wsum[NW];
     __shared__ int wpos;
     __shared__ unsigned long long minkey;
@@ -437,22 +435,39 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     for (int i = tid; i < fill; i += NT) buf[i] = a.best[(int64_t)q * k + i];
     __syncthreads();
 
+    // keep the best k of buf[0..fill): the radix prefix, then a block-wide
+    // append of the kept keys to the front; the smallest kept key is the
+    // k-th best so far
     auto compact = [&]() {
+        if (tid == 0) {
+            wpos = 0;
+            minkey = ~0ull;
+        }
         uint64_t prefix, pmask;
-        block_radix_prefix(buf, fill, k, ss, prefix, pmask);
+        block_radix_prefix(buf, fill, k, rs, prefix, pmask);  // its barriers publish wpos/minkey
         uint64_t v[KPT];
         uint32_t keep = 0;
+        uint64_t lo = ~0ull;
 #pragma unroll
         for (int j = 0; j < KPT; j++) {
             const int i = tid + NT * j;
             v[j] = i < fill ? buf[i] : 0ull;
-            if (i < fill && (v[j] & pmask) >= prefix) keep |= 1u << j;
+            if (i < fill && (v[j] & pmask) >= prefix) {
+                keep |= 1u << j;
+                lo = v[j] < lo ? v[j] : lo;
+            }
         }
-        if (tid == 0) wpos = 0;
-        __syncthreads();
+        int pos = wave_append(__popc(keep), &wpos);
+        __syncthreads();  // every read of buf is done before the first write
 #pragma unroll
         for (int j = 0; j < KPT; j++)
-            if (keep & (1u << j)) buf[atomicAdd(&wpos, 1)] = v[j];
+            if (keep & (1u << j)) buf[pos++] = v[j];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const uint64_t t = __shfl_xor(lo, off);
+            lo = t < lo ? t : lo;
+        }
+        if ((tid & 63) == 0 && lo != ~0ull) atomicMin(&minkey, (unsigned long long)lo);
         __syncthreads();
         fill = k;
     };
@@ -489,29 +504,40 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
         base += take;
         if (fill > k && (fill == LCAP || base == M)) compact();
     }
-    if (fill > k) compact();
-
+    bool compacted = false;
+    if (fill > k) {
+        compact();
+        compacted = true;
+    }
     // threshold for the next pass: the k-th key once k keys exist
-    if (tid == 0) minkey = ~0ull;
-    __syncthreads();
-    if (fill == k) {
+    if (fill == k && !compacted) {
+        // exactly k keys arrived: their minimum (rare; no compaction ran)
+        if (tid == 0) minkey = ~0ull;
+        __syncthreads();
         uint64_t lo = ~0ull;
         for (int i = tid; i < fill; i += NT) lo = buf[i] < lo ? buf[i] : lo;
         if (lo != ~0ull) atomicMin(&minkey, (unsigned long long)lo);
+        __syncthreads();
     }
-    topk_sort(buf, fill);  // its barriers also order the minimum before its use
-    if (tid == 0) {
-        a.bcnt[q] = fill;
-        a.tau[q] = fill == k ? (uint64_t)minkey : 0ull;
-    }
+    const uint64_t kth = fill == k ? (uint64_t)minkey : 0ull;
     if (a.out_ids) {
+        // final pass: ids and scores in (value, index) order
+        const int S = next_pow2(fill < 2 ? 2 : fill);
+        for (int i = fill + tid; i < S; i += NT) buf[i] = 0;
+        __syncthreads();
+        block_sort_desc_regs<NT>(buf, S);
         for (int i = tid; i < k; i += NT) {
             const uint64_t key = i < fill ? buf[i] : 0ull;
             a.out_ids[(int64_t)q * k + i] = key ? (int32_t)key_index(key) : -1;
             if (a.out_scores) a.out_scores[(int64_t)q * k + i] = key ? key_score(key, a.smallest) : 0.0f;
         }
     } else {
+        // intermediate pass: the best keys in any order, and the threshold
         for (int i = tid; i < fill; i += NT) a.best[(int64_t)q * k + i] = buf[i];
+    }
+    if (tid == 0) {
+        a.bcnt[q] = fill;
+        a.tau[q] = kth;
     }
 }
 

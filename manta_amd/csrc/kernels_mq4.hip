@@ -61,14 +61,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     uint8_t* tiles = smem;                                   // [NBUF][TILE]
     uint8_t* consts = smem + NBUF * TILE;                    // [NBUF][CTILE]
     uint64_t* scratch_extra = (uint64_t*)(smem + NBUF * (TILE + CTILE));
-    __shared__ QConst qcs[QG];
     __shared__ uint64_t tau_s[QG];
     __shared__ __attribute__((aligned(16))) float bnd_s[QG];
     __shared__ __attribute__((aligned(16))) float qa_s[QG];   // QConst.a = qs
     __shared__ __attribute__((aligned(16))) float qc_s[QG];   // QConst.c = |q|^2
     __shared__ int cnt_s[QG];
     __shared__ uint64_t flags[2][NFW];
-    __shared__ SelectShared ss;
+    __shared__ RadixShared ss;
     __shared__ int wpos;
     __shared__ unsigned long long minkey;
 
@@ -84,7 +83,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         const int q = q0 + i;
         const bool ok = q < a.nq;
         const QConst qc = ok ? a.qconst[q] : QConst{1.0f, 0.0f, 0.0f, 0.0f};
-        qcs[i] = qc;
         qa_s[i] = qc.a;
         qc_s[i] = qc.c;
         const uint64_t tk = (APPEND && ok) ? a.tau[q] : 0ull;
@@ -243,7 +241,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     auto score_of = [&](float p, int lq, float rowc) {
         if (OP == OP_DOT) return p;
         if (OP == OP_COSINE) {
-            const float den = fmul_rn(qcs[lq].b, rowc);
+            const float den = fmul_rn(a.qconst[q0 + lq].b, rowc);
             return den == 0.0f ? 0.0f : fdiv_rn(p, den);
         }
         return fsqrt_rn(p < 0.0f ? 0.0f : p);
@@ -292,7 +290,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                         cnt_s[lq] = a.k;
                         if (minkey > tau_s[lq]) {
                             tau_s[lq] = minkey;
-                            bnd_s[lq] = mq4_bound<OP>(minkey, qcs[lq], SMALL);
+                            bnd_s[lq] = mq4_bound<OP>(minkey, a.qconst[q0 + lq], SMALL);
                         }
                     }
                     __syncthreads();

@@ -59,21 +59,34 @@ __device__ __forceinline__ void lds_load4(const void* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
 
+// Scratch of block_radix_prefix: histograms and results double-buffered by
+// round, so a round needs only two barriers.
+struct RadixShared {
+    int hist[2][256];
+    int digit[2];
+    int above[2];
+    int count[2];
+};
+
 // Radix select over keys[0..c) (c > k, keys distinct), whole workgroup:
 // finds (prefix, pmask) such that exactly k keys satisfy
 // (key & pmask) >= prefix.  8-bit digits, most significant first; a wave
 // whose matching lanes share one digit adds them with a single LDS atomic,
 // so the (typically uniform) leading digits of the keys cost no contention.
-__device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, SelectShared& ss,
+// Per round: histogram, barrier, wave 0 scans (and clears the histogram for
+// the round after next), barrier, every thread reads the result.
+__device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, RadixShared& rs,
                                           uint64_t& prefix_out, uint64_t& pmask_out) {
     const int tid = threadIdx.x;
     const int nt = blockDim.x;
     const int lane = tid & 63;
+    for (int i = tid; i < 512; i += nt) (&rs.hist[0][0])[i] = 0;
+    __syncthreads();
     uint64_t prefix = 0, pmask = 0;
     int remaining = k;
-    for (int shift = 56; shift >= 0; shift -= 8) {
-        for (int i = tid; i < 256; i += nt) ss.hist[i] = 0;
-        __syncthreads();
+    int b = 0;
+    for (int shift = 56; shift >= 0; shift -= 8, b ^= 1) {
+        int* hist = rs.hist[b];
         for (int i = tid; i < c; i += nt) {
             const uint64_t key = keys[i];
             const bool m = (key & pmask) == prefix;
@@ -84,9 +97,9 @@ __device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, Se
                 const int d0 = __shfl(dg, lead);
                 const uint64_t same = __ballot(m && dg == d0);
                 if (same == mm) {
-                    if (lane == lead) atomicAdd(&ss.hist[d0], __popcll(mm));
+                    if (lane == lead) atomicAdd(&hist[d0], __popcll(mm));
                 } else if (m) {
-                    atomicAdd(&ss.hist[dg], 1);
+                    atomicAdd(&hist[dg], 1);
                 }
             }
         }
@@ -97,7 +110,8 @@ __device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, Se
             int sum = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                h[j] = ss.hist[255 - 4 * tid - j];
+                h[j] = hist[255 - 4 * tid - j];
+                hist[255 - 4 * tid - j] = 0;  // ready for the round after next
                 sum += h[j];
             }
             int incl = sum;
@@ -110,23 +124,106 @@ __device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, Se
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 if (cum < remaining && cum + h[j] >= remaining) {
-                    ss.digit = 255 - 4 * tid - j;
-                    ss.above = cum;
+                    rs.digit[b] = 255 - 4 * tid - j;
+                    rs.above[b] = cum;
+                    rs.count[b] = h[j];
                 }
                 cum += h[j];
             }
         }
         __syncthreads();
-        const int d = ss.digit;
-        remaining -= ss.above;
+        const int d = rs.digit[b];
+        remaining -= rs.above[b];
         prefix |= (uint64_t)d << shift;
         pmask |= 0xFFull << shift;
-        const bool all_in = ss.hist[d] == remaining;
-        __syncthreads();
-        if (all_in) break;  // every key with this prefix is kept
+        if (rs.count[b] == remaining) break;  // every key with this prefix is kept
     }
     prefix_out = prefix;
     pmask_out = pmask;
+}
+
+// Offset of this thread's `cnt` items in a block-wide append through
+// `counter`: a wave prefix sum and one LDS atomic per wave.
+__device__ __forceinline__ int wave_append(int cnt, int* counter) {
+    const int lane = threadIdx.x & 63;
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (lane >= off) incl += t;
+    }
+    int base = 0;
+    if (lane == 63 && incl) base = atomicAdd(counter, incl);
+    base = __shfl(base, 63);
+    return base + incl - cnt;
+}
+
+// Sort keys[0..S) descending in place (S a power of two, S <= NT*16), whole
+// workgroup of NT threads.  Bitonic network over registers: thread t holds
+// elements t + j*NT; exchanges at strides below 64 are lane shuffles, at
+// strides of NT and more stay inside a thread, and only the strides in
+// between go through LDS (two barriers each).
+template <int NT>
+__device__ inline void block_sort_desc_regs(uint64_t* keys, int S) {
+    constexpr int MAXJ = 16;
+    const int tid = threadIdx.x;
+    const int J = (S + NT - 1) / NT;  // slots in use (uniform)
+    uint64_t v[MAXJ];
+#pragma unroll
+    for (int j = 0; j < MAXJ; j++) {
+        const int i = tid + j * NT;
+        v[j] = i < S ? keys[i] : 0ull;
+    }
+    auto pick = [](uint64_t mine, uint64_t other, bool desc, bool lower) {
+        const uint64_t hi = mine > other ? mine : other, lo = mine > other ? other : mine;
+        return desc == lower ? hi : lo;
+    };
+    for (int size = 2; size <= S; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= NT) {
+#pragma unroll
+                for (int lg = 0; lg < 4; lg++) {
+                    const int sj = 1 << lg;
+                    if (stride != sj * NT) continue;
+#pragma unroll
+                    for (int j = 0; j < MAXJ; j++) {
+                        if ((j & sj) || tid + (j | sj) * NT >= S) continue;
+                        const int jp = j | sj;
+                        const bool desc = ((tid + j * NT) & size) == 0;
+                        const uint64_t a = v[j], c = v[jp];
+                        v[j] = pick(a, c, desc, true);
+                        v[jp] = pick(c, a, desc, false);
+                    }
+                }
+            } else if (stride >= 64) {
+#pragma unroll
+                for (int j = 0; j < MAXJ; j++) {
+                    if (j >= J) break;
+                    if (tid + j * NT < S) keys[tid + j * NT] = v[j];
+                }
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < MAXJ; j++) {
+                    if (j >= J) break;
+                    const int i = tid + j * NT;
+                    if (i < S) v[j] = pick(v[j], keys[i ^ stride], (i & size) == 0, (i & stride) == 0);
+                }
+                __syncthreads();
+            } else {
+#pragma unroll
+                for (int j = 0; j < MAXJ; j++) {
+                    if (j >= J) break;
+                    const int i = tid + j * NT;
+                    const uint64_t other = __shfl_xor(v[j], stride);
+                    if (i < S) v[j] = pick(v[j], other, (i & size) == 0, (i & stride) == 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MAXJ; j++)
+        if (tid + j * NT < S) keys[tid + j * NT] = v[j];
+    __syncthreads();
 }
 
 // Chunk tiles per workgroup: as many (2..4) as fit in about 72 KB of LDS
