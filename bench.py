@@ -63,13 +63,14 @@ def cpu_baseline(codes, scales, queries, budget_s: float) -> dict:
     }
 
 
-def profiled_traffic(name: str):
-    """HBM bytes per launch measured by rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE,
-    copy-kernel calibrated) and recorded in the committed profile summary."""
+def profiled_traffic(name: str, key: str = "traffic_bytes_per_launch"):
+    """HBM bytes per launch (or per step) measured by rocprofv3 PMC
+    (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated) and recorded in the
+    committed profile summary."""
     path = os.path.join(ROOT, "profiles", name)
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(key + ":"):
                 return int(line.split(":", 1)[1].strip())
     except OSError:
         pass
@@ -209,6 +210,8 @@ def run_c3(rt, steps, warmup) -> dict:
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK, "scan_us_per_step": fam[dom][2] * 1000.0,
                      "bytes_per_step": nbytes,
+                     "traffic": profiled_traffic("mq_scan_c3_l2_smallest1000.md", "traffic_bytes_per_step"),
+                     "traffic_source": "profiles/mq_scan_c3_l2_smallest1000.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                      "note": "all threshold passes of the scan together cover the N rows once"},
     }
 

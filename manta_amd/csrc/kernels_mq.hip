@@ -5,12 +5,11 @@
 // Each wave keeps NA blocks of query codes resident in VGPRs as the A
 // operand of v_mfma_i32_32x32x32_i8 (32 A rows = 32 queries for E8 codes,
 // or 16 queries x {hi, lo} digit for E16 codes).  Candidate rows stream
-// through LDS in chunks: the workgroup loads a chunk with coalesced 16-byte
-// loads (rows are contiguous, so a chunk is one contiguous span of HBM),
-// stores it into a padded LDS tile, and every wave reads its B fragments
-// from there -- each candidate byte is fetched from HBM/L2 once per
-// workgroup and feeds 4*NA (WQ = 4) or NA (WQ = 1) MFMAs.  The next chunk's
-// loads are in flight while the current one is multiplied.
+// through LDS in chunks of 32 rows per wave: a chunk is one contiguous span
+// of HBM, moved by direct-to-LDS loads into a padded tile two to four chunks
+// ahead of its use, and every wave reads its B fragments from there -- with
+// the waves splitting the queries (WQ = 4) each candidate byte is fetched
+// once per workgroup and feeds 4*NA MFMAs.
 //
 // With the candidate on the MFMA output column, lane l ends a 32-row block
 // holding candidate l%32 against 16 A rows: 16 queries (E8), or 8 queries as
