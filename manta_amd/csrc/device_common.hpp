@@ -277,4 +277,61 @@ __device__ __forceinline__ void topk_maybe_compact(uint64_t* keys, TopKShared* s
     if (c + (int)blockDim.x > cap) topk_compact(keys, st, k);
 }
 
+// ------------------------------------------------- wave-resident top list
+
+// For k <= 64 a wave keeps its best keys seen so far sorted across its
+// lanes: lane i holds the i-th largest (0 = empty slot).  A key enters only
+// if it beats the k-th entry (thr), so after the first few batches almost
+// every offer is a single compare and ballot; nothing touches LDS and no
+// barrier is needed.  Keys are distinct (they carry the row index).
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Lane i receives lane i-1's value; lane 0 receives `first` (DPP wave_shr:1).
+__device__ __forceinline__ uint64_t wave_shr1_u64(uint64_t v, uint64_t first) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)first, (int)(uint32_t)v, 0x138,
+                                                               0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(first >> 32),
+                                                               (int)(uint32_t)(v >> 32), 0x138, 0xf, 0xf, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Insert the wave-uniform key x (not already present) into the sorted list:
+// lanes holding larger keys keep them, the first lane below x takes x, the
+// rest shift down one lane (the last entry drops off).
+__device__ __forceinline__ void wave_list_insert(uint64_t& list, uint64_t x) {
+    const uint64_t prev = wave_shr1_u64(list, ~0ull);
+    const bool keep = list > x;
+    list = keep ? list : (prev > x ? x : prev);
+}
+
+// Offer one key per lane (0 = nothing); thr is the list's k-th entry
+// (0 while fewer than k keys are held) and is kept current.
+__device__ __forceinline__ void wave_list_offer(uint64_t key, uint64_t& list, uint64_t& thr, int k) {
+    uint64_t mask = __ballot(key > thr);
+    while (mask) {
+        const int j = __ffsll((unsigned long long)mask) - 1;
+        wave_list_insert(list, readlane_u64(key, j));
+        thr = readlane_u64(list, k - 1);
+        mask &= mask - 1;
+        mask &= __ballot(key > thr);
+    }
+}
+
+// Merge the lists of all waves of the workgroup into wave 0's (whole
+// workgroup; buf holds blockDim.x keys of LDS).  Ends with a barrier.
+__device__ inline void wave_lists_merge(uint64_t& list, uint64_t& thr, int k, uint64_t* buf) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    buf[threadIdx.x] = lane < k ? list : 0ull;
+    __syncthreads();
+    if (wave == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) wave_list_offer(buf[w * 64 + lane], list, thr, k);
+    }
+    __syncthreads();
+}
+
 }  // namespace manta

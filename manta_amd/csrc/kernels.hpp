@@ -13,6 +13,7 @@ struct QConst;
 
 constexpr int kMaxQueryDim = 1024;  // longest query / row the device path takes
 constexpr int kMaxCapKeys = 4096;   // largest LDS key reservoir (32 KB)
+constexpr int kWaveListMaxK = 64;   // largest k kept in per-wave register lists
 
 // Arguments of the streaming scan kernels (one query per blockIdx.y).
 struct ScanArgs {
@@ -37,11 +38,14 @@ struct ScanArgs {
     int lds_keys;             // keys the dynamic LDS holds (>= cap; merge fast path)
     int mid_compact;          // 0: cap >= k + rounds*256, no compaction between rounds
     int smallest;
+    int wave_lists;           // 1: k <= 64 top lists held in registers (coalesced q8 kernel only)
 };
 
 hipError_t launch_query_encode(const uint16_t* q, int nq, int d, int pitch, int e16, int8_t* c8,
                                int8_t* hi, int8_t* lo, QConst* qc, hipStream_t s);
 hipError_t launch_q8_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s);
+// Pitches served by the coalesced q8 kernel (the others use the row-per-lane one).
+bool q8_scan_coalesced(int pitch);
 hipError_t launch_q4_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s);
 hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride, int64_t n, int d,
                              const uint16_t* queries, const int32_t* ids, int k, int nq, int e16,

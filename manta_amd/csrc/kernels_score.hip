@@ -184,6 +184,12 @@ struct ScanLds {
     int last;
 };
 
+// Kernels that keep the encoded query in registers.
+struct ScanTopkLds {
+    TopKShared st;
+    int last;
+};
+
 // Store the score, or offer it to the reservoir.
 __device__ __forceinline__ void emit_round(float score, bool valid, int64_t row, int64_t n, int qi,
                                            float* __restrict__ out_scores, uint64_t* keys,
@@ -204,7 +210,8 @@ __device__ __forceinline__ void emit_round(float score, bool valid, int64_t row,
 // scope (sc1), every thread waits for its stores to complete before the
 // barrier, the ticket is an agent-scope atomic, and the merging workgroup
 // reads the parts with agent-scope (sc1) loads.
-__device__ inline void finish_topk(const ScanArgs& a, uint64_t* keys, ScanLds& S, int qi) {
+template <class SL>
+__device__ inline void finish_topk(const ScanArgs& a, uint64_t* keys, SL& S, int qi) {
     __syncthreads();
     topk_compact(keys, &S.st, a.k);
     const int64_t per_q = (int64_t)gridDim.x * a.k;
@@ -250,84 +257,256 @@ __device__ inline void finish_topk(const ScanArgs& a, uint64_t* keys, ScanLds& S
     if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[qi], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// End of a top-k scan workgroup on the wave-list path (k <= 64): the waves'
+// lists merge into wave 0's, which publishes the workgroup's k best keys
+// (sorted) as finish_topk does; the last workgroup of the query merges all
+// parts with the same lists, 8 keys per lane in flight, and writes ids and
+// scores straight from wave 0's lanes.  buf: blockDim.x keys of LDS.
+template <class SL>
+__device__ inline void finish_wave_lists(const ScanArgs& a, uint64_t list, uint64_t thr, uint64_t* buf, SL& S,
+                                         int qi) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    wave_lists_merge(list, thr, a.k, buf);
+    const int64_t per_q = (int64_t)gridDim.x * a.k;
+    uint64_t* dst = a.partial + (int64_t)qi * per_q + (int64_t)blockIdx.x * a.k;
+    if (wave == 0 && lane < a.k) __hip_atomic_store(dst + lane, list, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        S.last = __hip_atomic_fetch_add(&a.tickets[qi], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 gridDim.x - 1;
+    __syncthreads();
+    if (!S.last) return;
+    const uint64_t* src = a.partial + (int64_t)qi * per_q;
+    list = 0;
+    thr = 0;
+    // batches of 64 keys go to the waves in turn; B batches per wave in flight
+    constexpr int B = 8;
+    const int64_t stride = (int64_t)blockDim.x;
+    for (int64_t base = (int64_t)wave * 64; base < per_q; base += stride * B) {
+        uint64_t kb[B];
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const int64_t i = base + b * stride + lane;
+            kb[b] = i < per_q ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        }
+#pragma unroll
+        for (int b = 0; b < B; b++) wave_list_offer(kb[b], list, thr, a.k);
+    }
+    wave_lists_merge(list, thr, a.k, buf);
+    if (wave == 0 && lane < a.k) {
+        a.out_ids[(int64_t)qi * a.k + lane] = list ? (int32_t)key_index(list) : -1;
+        if (a.out_topk_scores) a.out_topk_scores[(int64_t)qi * a.k + lane] = list ? key_score(list, a.smallest) : 0.0f;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[qi], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // -------------------------------------------------- q8, coalesced lanes
 
+// Sum over aligned groups of L lanes (L = 4, 8 or 16) with DPP moves inside
+// each 16-lane row; every lane of a group receives the group total.
+template <int L>
+__device__ __forceinline__ int group_sum(int s) {
+    s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    if (L >= 8) s += __builtin_amdgcn_update_dpp(0, s, 0x141, 0xf, 0xf, false);   // row_half_mirror
+    if (L >= 16) s += __builtin_amdgcn_update_dpp(0, s, 0x140, 0xf, 0xf, false);  // row_mirror
+    return s;
+}
+
+// Buffer resource over `bytes` bytes at p (raw, stride 0): loads at offsets
+// at or past `bytes` return zero instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_buffer(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// DPP move of a double: both 32-bit halves with the same pattern.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double x) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+template <int L>
+__device__ __forceinline__ float group_fmax(float m) {
+    m = fmaxf(m, dpp_f32<0xB1>(m));
+    m = fmaxf(m, dpp_f32<0x4E>(m));
+    if (L >= 8) m = fmaxf(m, dpp_f32<0x141>(m));
+    if (L >= 16) m = fmaxf(m, dpp_f32<0x140>(m));
+    return m;
+}
+
+// Exact while every partial sum stays below 2^53 (sums of squared codes).
+template <int L>
+__device__ __forceinline__ double group_dsum(double s) {
+    s += dpp_f64<0xB1>(s);
+    s += dpp_f64<0x4E>(s);
+    if (L >= 8) s += dpp_f64<0x141>(s);
+    if (L >= 16) s += dpp_f64<0x140>(s);
+    return s;
+}
+
+// Encode the query columns this lane multiplies straight into registers:
+// chunk c of lane p covers columns [16*(c*L + p), +16) (zero past d).  The L
+// lanes of a group cover every column, so group reductions give the
+// whole-query max |q| and sum of squared codes; codes and constants equal
+// encode_query_block's.  Whole wave, no LDS, no barrier.
 template <int OP, int L, int C>
+__device__ __forceinline__ QConst encode_query_lanes(const uint16_t* qrow, int d, int p, v4i* qa, v4i* qb) {
+    const __amdgpu_buffer_rsrc_t qr = byte_buffer(qrow, (uint32_t)d * 2u);
+    uint16_t hx[C][16];  // raw f16 bits, converted where used
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int col = c * 16 * L + p * 16 + e;
+            hx[c][e] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(qr, col * 2, 0, 0);
+            m = fmaxf(m, __builtin_fabsf(h2f(hx[c][e])));
+        }
+    m = group_fmax<L>(m);
+    if (OP == OP_DOT) {
+        const float qmax = fmaxf(1.0f, m);
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                int word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; b++) word |= (code_e8(h2f(hx[c][4 * w + b]), qmax) & 0xFF) << (8 * b);
+                qa[c][w] = word;
+            }
+            qb[c] = qa[c];
+        }
+        return QConst{qmax, 0.0f, 0.0f, 0.0f};
+    }
+    const float inv = m == 0.0f ? 0.0f : fdiv_rn(32639.0f, m);
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            int hw = 0, lw = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int code = m != 0.0f ? code_e16(h2f(hx[c][4 * w + b]), inv) : 0;
+                const int l = (int)(int8_t)(code & 0xFF);
+                const int h = (code - l) >> 8;
+                hw |= (h & 0xFF) << (8 * b);
+                lw |= (l & 0xFF) << (8 * b);
+                ss += (double)code * (double)code;
+            }
+            qa[c][w] = hw;
+            qb[c][w] = lw;
+        }
+    ss = group_dsum<L>(ss);
+    return e16_consts(m, (long long)ss);
+}
+
+// Pitch = 16*L*C bytes.  A wave scores a block of 64 rows per round; lane
+// group g (L lanes) owns rows g*L .. g*L+L-1 of the block.  Load (j, c)
+// reads row g*L + j, lane p of the group taking bytes [16p + 16Lc, +16), so
+// one load instruction reads 64/L whole rows.  The row sum is a DPP group
+// sum, and lane g*L + j keeps it: after a round every lane holds the
+// accumulator of its own row.  Loads go through a buffer resource clipped to
+// the workgroup's rows (no branch per load; rows past n read zero and are
+// masked by `valid`).
+template <int OP, int L, int C, bool LISTS>
 __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
     extern __shared__ uint64_t topk_keys[];
-    __shared__ ScanLds S;
-    constexpr int G = 64 / L;  // rows per wave per load step
+    __shared__ ScanTopkLds S;
+    constexpr int PITCH = 16 * L * C;
+    constexpr int JS0 = C == 1 ? 16 : (C == 2 ? 8 : 4);  // rows per load step (<= 16 loads)
+    constexpr int JS = JS0 < L ? JS0 : L;
+    static_assert(L % JS == 0, "load steps must tile the lane group");
     const int qi = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int p = lane % L;
     const int g = lane / L;
     const int64_t set_row0 = (int64_t)qi * a.set_stride;
-    const int8_t* __restrict__ codes = a.codes + set_row0 * a.pitch;
+    const int8_t* __restrict__ codes = a.codes + set_row0 * PITCH;
     const float* __restrict__ scales = (const float*)a.scales + set_row0;
 
-    encode_query_block(a.queries + (int64_t)qi * a.d, a.d, a.pitch, OP == OP_DOT ? ENC_E8 : ENC_E16, S.q);
-    const QConst kq = S.q.qc;
-    v4i qa[C], qb[C];
-#pragma unroll
-    for (int c = 0; c < C; c++) {
-        const int off = c * 16 * L + p * 16;
-        if (OP == OP_DOT) {
-            qa[c] = *(const v4i*)(S.q.c8 + off);
-            qb[c] = qa[c];
-        } else {
-            qa[c] = *(const v4i*)(S.q.hi + off);
-            qb[c] = *(const v4i*)(S.q.lo + off);
-        }
-    }
-    if (!a.out_scores) topk_init(topk_keys, &S.st);
-
     const int64_t wg_row0 = (int64_t)blockIdx.x * a.rounds * 256;
+    const int64_t left = a.n - wg_row0;  // > 0: the grid covers n exactly
+    const int wg_rows = left < (int64_t)a.rounds * 256 ? (int)left : a.rounds * 256;
+    const __amdgpu_buffer_rsrc_t rs = byte_buffer(codes + wg_row0 * PITCH, (uint32_t)wg_rows * PITCH);
+    const int lane_off = g * L * PITCH + p * 16;
+    // One load step: rows j0 .. j0+JS-1 of every lane group of the wave's
+    // block in round r.  On the wave-list path the next step's loads are
+    // issued as soon as the current step's values are consumed, so they
+    // overlap the epilogue and the top-k offer, and the first step's overlap
+    // the query encoding.
+    v4i v[JS][C];
+    auto load_step = [&](int r, int j0) {
+        const int vb = (r * 256 + wave * 64) * PITCH + lane_off;
+#pragma unroll
+        for (int j = 0; j < JS; j++)
+#pragma unroll
+            for (int c = 0; c < C; c++)
+                v[j][c] = __builtin_amdgcn_raw_buffer_load_b128(rs, vb + (j0 + j) * PITCH + c * 16 * L, 0, 2);
+    };
+    if (LISTS) load_step(0, 0);
+
+    v4i qa[C], qb[C];
+    const QConst kq = encode_query_lanes<OP, L, C>(a.queries + (int64_t)qi * a.d, a.d, p, qa, qb);
+    // LISTS: top-k through per-wave register lists (k <= 64, never score mode)
+    uint64_t list = 0, thr = 0;
+    if (!LISTS && !a.out_scores) topk_init(topk_keys, &S.st);
+
     for (int r = 0; r < a.rounds; r++) {
-        const int64_t row_base = wg_row0 + (int64_t)r * 256 + wave * 64;
-        v4i v[L][C];
-#pragma unroll
-        for (int it = 0; it < L; it++) {
-            const int64_t row = row_base + it * G + g;
-#pragma unroll
-            for (int c = 0; c < C; c++) {
-                if (row < a.n)
-                    v[it][c] = __builtin_nontemporal_load(
-                        (const v4i*)(codes + row * a.pitch + c * 16 * L + p * 16));
-                else
-                    v[it][c] = v4i{0, 0, 0, 0};
-            }
-        }
+        const int64_t row = wg_row0 + r * 256 + wave * 64 + lane;
+        const bool valid = row < a.n;
+        const int64_t crow = valid ? row : a.n - 1;
+        const float sc = scales[crow];
+        float dn = 0.0f, d2 = 0.0f;
+        if (OP == OP_COSINE) dn = a.dnorm[set_row0 + crow];
+        if (OP == OP_L2) d2 = a.dd[set_row0 + crow];
         int my_hi = 0, my_lo = 0;
 #pragma unroll
-        for (int it = 0; it < L; it++) {
-            int s_hi = 0, s_lo = 0;
+        for (int j0 = 0; j0 < L; j0 += JS) {
+            // the reservoir path loads each step when it starts (its offer
+            // and compaction would otherwise run with a step of loads held)
+            if (!LISTS) load_step(r, j0);
 #pragma unroll
-            for (int c = 0; c < C; c++) {
-                s_hi = dot16(v[it][c], qa[c], s_hi);
-                if (OP != OP_DOT) s_lo = dot16(v[it][c], qb[c], s_lo);
-            }
+            for (int j = 0; j < JS; j++) {
+                int s_hi = 0, s_lo = 0;
 #pragma unroll
-            for (int off = L / 2; off >= 1; off >>= 1) {
-                s_hi += __shfl_xor(s_hi, off);
-                if (OP != OP_DOT) s_lo += __shfl_xor(s_lo, off);
+                for (int c = 0; c < C; c++) {
+                    s_hi = dot16(v[j][c], qa[c], s_hi);
+                    if (OP != OP_DOT) s_lo = dot16(v[j][c], qb[c], s_lo);
+                }
+                s_hi = group_sum<L>(s_hi);
+                if (OP != OP_DOT) s_lo = group_sum<L>(s_lo);
+                if (p == j0 + j) {
+                    my_hi = s_hi;
+                    my_lo = s_lo;
+                }
             }
-            const int src = (lane % G) * L;
-            int t_hi = __shfl(s_hi, src);
-            int t_lo = (OP != OP_DOT) ? __shfl(s_lo, src) : 0;
-            if (lane / G == it) {
-                my_hi = t_hi;
-                my_lo = t_lo;
-            }
+            // the step's values are consumed before the next loads are
+            // issued (else the loads would be hoisted and double the
+            // registers held)
+            asm volatile("" : "+v"(my_hi), "+v"(my_lo));
+            asm volatile("" ::: "memory");
+            if (!LISTS) continue;
+            if (j0 + JS < L)
+                load_step(r, j0 + JS);
+            else if (r + 1 < a.rounds)
+                load_step(r + 1, 0);
         }
-        const int64_t row = row_base + lane;
-        const bool valid = row < a.n;
         float score = 0.0f;
-        if (valid) {
-            float dn = 0.0f, d2 = 0.0f;
-            if (OP == OP_COSINE) dn = a.dnorm[set_row0 + row];
-            if (OP == OP_L2) d2 = a.dd[set_row0 + row];
-            score = q8_epilogue<OP>(my_hi, my_lo, scales[row], kq, dn, d2);
+        if (valid) score = q8_epilogue<OP>(my_hi, my_lo, sc, kq, dn, d2);
+        if (LISTS) {
+            wave_list_offer(valid ? make_key(score, (uint32_t)row, a.smallest) : 0ull, list, thr, a.k);
+            continue;
         }
         const uint64_t tau = a.out_scores ? 0ull : S.st.tau;
         emit_round(score, valid, row, a.n, qi, a.out_scores, topk_keys, &S.st, tau, a.smallest);
@@ -336,7 +515,10 @@ __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
             topk_maybe_compact(topk_keys, &S.st, a.k, a.cap);
         }
     }
-    if (!a.out_scores) finish_topk(a, topk_keys, S, qi);
+    if (LISTS)
+        finish_wave_lists(a, list, thr, topk_keys, S, qi);
+    else if (!a.out_scores)
+        finish_topk(a, topk_keys, S, qi);
 }
 
 // --------------------------------------------- q8, any pitch (lane = row)
@@ -481,13 +663,22 @@ hipError_t launch_query_encode(const uint16_t* q, int nq, int d, int pitch, int 
     return hipGetLastError();
 }
 
+bool q8_scan_coalesced(int pitch) {
+    const int chunks = pitch / 16;
+    return pitch % 16 == 0 && (chunks == 4 || chunks == 8 || chunks == 12 || chunks == 16 || chunks == 24 ||
+                               chunks == 32 || chunks == 48 || chunks == 64);
+}
+
 template <int OP>
 static hipError_t launch_q8_op(const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     const int chunks = a.pitch / 16;
-#define MANTA_Q8(LL, CC)                                                               \
-    if (chunks == (LL) * (CC)) {                                                       \
-        hipLaunchKernelGGL((q8_scan_kernel<OP, LL, CC>), grid, dim3(256), lds, s, a); \
-        return hipGetLastError();                                                      \
+#define MANTA_Q8(LL, CC)                                                                           \
+    if (chunks == (LL) * (CC)) {                                                                   \
+        if (a.wave_lists && !a.out_scores)                                                         \
+            hipLaunchKernelGGL((q8_scan_kernel<OP, LL, CC, true>), grid, dim3(256), lds, s, a);  \
+        else                                                                                       \
+            hipLaunchKernelGGL((q8_scan_kernel<OP, LL, CC, false>), grid, dim3(256), lds, s, a); \
+        return hipGetLastError();                                                                  \
     }
     MANTA_Q8(4, 1)    // d <= 64
     MANTA_Q8(8, 1)    // 128

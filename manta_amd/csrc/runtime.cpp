@@ -597,8 +597,11 @@ int check_score_args(const MantaRocmCandidates* c, int op, const void* q, int64_
 
 // Rounds of 256 rows per workgroup: aim for about 2048 workgroups (8 per
 // CU), with at most 64 rounds.
+// Rounds of 256 rows per scan workgroup: about 512 workgroups in all (two per
+// CU, one resident generation), so each streams a long contiguous range and
+// the per-workgroup prologue and top-k publication are paid rarely.
 int choose_rounds(int64_t tiles, int64_t nq) {
-    int64_t r = tiles * nq / 2048;
+    int64_t r = (tiles * nq + 511) / 512;
     return (int)std::max<int64_t>(1, std::min<int64_t>(64, r));
 }
 
@@ -872,6 +875,12 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, i
     // the merge loads all parts at once when they fit in LDS (<= 4096 keys)
     a.lds_keys = (int)std::max<int64_t>(cap, parts * k <= manta::kMaxCapKeys ? parts * k : 0);
     a.smallest = order == MANTA_ROCM_SMALLEST;
+    // small k on the coalesced q8 kernel: sorted per-wave lists in registers
+    // (LDS only for merging the waves' lists)
+    if (c->format == MANTA_ROCM_Q8_ROWS && manta::q8_scan_coalesced(c->pitch) && k <= manta::kWaveListMaxK) {
+        a.wave_lists = 1;
+        a.lds_keys = 256;
+    }
     rc = launch_scan(rt, c, op, a, dim3((unsigned)parts, (unsigned)nq), (size_t)a.lds_keys * 8, err);
     if (rc) return rc;
     if (out_acc) {

@@ -82,6 +82,56 @@ def test_q8_score_topk_bit_exact(rt, op, smallest, sets, n, k):
     cands.close()
 
 
+def _check_q8_topk(rt, op, smallest, q, codes, scales, k):
+    """score_topk over per-query candidate sets against the oracle: ids,
+    scores and integer accumulators bit-exact."""
+    cands = rt.bind_q8(codes, scales)
+    ids, sc, acc = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
+    ids, sc, acc = ids.download(), sc.download(), acc.download()
+    want_s, want_acc = orc.score_q8(op, q, codes, scales, with_acc=True)
+    want_ids = orc.topk(want_s, k, smallest=smallest)
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_array_equal(sc, np.take_along_axis(want_s, want_ids, 1))
+    np.testing.assert_array_equal(acc, np.take_along_axis(want_acc, want_ids, 1))
+    cands.close()
+
+
+@pytest.mark.parametrize("op,smallest", [("dot", False), ("cosine", False), ("l2_distance", True),
+                                         ("dot", True)])
+@pytest.mark.parametrize("d", [64, 128, 192, 384, 512, 768, 1024])
+@pytest.mark.parametrize("k", [1, 33, 64])
+def test_q8_wave_list_topk_bit_exact(rt, op, smallest, d, k):
+    """k <= 64 keeps sorted per-wave lists in registers: every coalesced row
+    width, with a row count that leaves a partial last round."""
+    nq, n = 2, 5000 + d
+    q, codes, scales = _q8_case(d + k, nq, n, d, nq)
+    _check_q8_topk(rt, op, smallest, q, codes, scales, k)
+
+
+@pytest.mark.parametrize("k", [10, 64])
+def test_q8_wave_list_many_parts(rt, k):
+    """One query over 300000 rows: over a thousand workgroups publish their
+    lists, and the final merge walks all of them."""
+    q, codes, scales = _q8_case(7 + k, 1, 300000, 128, 1)
+    _check_q8_topk(rt, "dot", False, q, codes, scales, k)
+
+
+@pytest.mark.parametrize("op,smallest", [("dot", False), ("dot", True), ("l2_distance", True)])
+@pytest.mark.parametrize("k", [1, 10, 64])
+def test_q8_wave_list_all_ties(rt, op, smallest, k):
+    """Every row identical: every score ties, so the ids are the k lowest
+    row indices in order."""
+    n, d = 20000, 256
+    q, codes, scales = _q8_case(11, 2, n, d, 2)
+    codes[:] = codes[:, :1, :]
+    scales[:] = scales[:, :1]
+    _check_q8_topk(rt, op, smallest, q, codes, scales, k)
+    cands = rt.bind_q8(codes, scales)
+    ids, _, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    np.testing.assert_array_equal(ids.download(), np.tile(np.arange(k, dtype=np.int32), (2, 1)))
+    cands.close()
+
+
 @pytest.mark.parametrize("op", ["dot", "cosine", "l2_distance"])
 @pytest.mark.parametrize("d", [32, 384])
 def test_q4_score_and_topk_bit_exact(rt, op, d):
