@@ -497,9 +497,12 @@ __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
             asm volatile("" : "+v"(my_hi), "+v"(my_lo));
             asm volatile("" ::: "memory");
             if (!LISTS) continue;
+            // unconditional, so the wait counts stay static: after the last
+            // round these loads fall past the buffer and return zeros
+            // without touching memory
             if (j0 + JS < L)
                 load_step(r, j0 + JS);
-            else if (r + 1 < a.rounds)
+            else
                 load_step(r + 1, 0);
         }
         float score = 0.0f;
