@@ -96,6 +96,7 @@ struct MqSelectArgs {
 
 // Launch shape of the scan kernel for an op, K steps (pitch / 32) and query count.
 struct MqShape {
+    int kind = 0;        // 0: mq_scan / mq_q4 (256 threads); 1: mq8_scan (512 threads, q8 dot)
     int ks = 0;
     int na = 0;          // A blocks per wave
     int wq = 0;          // waves splitting the queries (1 or 4)
@@ -103,6 +104,7 @@ struct MqShape {
     int chunk = 0;       // candidate rows per LDS chunk
     int tile = 0;        // LDS bytes of one chunk tile
     int tile_bytes = 0;  // LDS bytes of all chunk tiles and their row constants
+    int threads = 256;   // workgroup size
 };
 
 MqShape mq_shape(int op, int ks, int64_t nq);
@@ -114,6 +116,11 @@ hipError_t launch_mq_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid,
 MqShape mq4_shape(int op, int nb, int64_t nq);
 bool mq4_supported_nb(int nb);
 hipError_t launch_mq4_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
+// q8 dot with many queries (kernels_mq8.hip): 512-thread workgroups of 512
+// queries on 16x16x64 i8 MFMAs, top-k mode only; pitch 128, 256 or 384.
+bool mq8_supported(int pitch);
+MqShape mq8_shape(int pitch);
+hipError_t launch_mq8_scan(const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
 int mq_select_threads(int64_t expect_keys);
 size_t mq_select_lds(int threads, int R);
 hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s);

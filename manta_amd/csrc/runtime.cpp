@@ -65,6 +65,7 @@ struct MantaRocmCandidates {
     float* dnorm = nullptr;
     float* dd = nullptr;
     size_t bytes = 0;
+    bool scales_finite = false;  // q8: every row scale is finite (the 512-query dot kernel needs it)
 };
 
 namespace {
@@ -454,6 +455,9 @@ int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* sca
     auto* c = new MantaRocmCandidates();
     c->rt = rt;
     c->format = MANTA_ROCM_Q8_ROWS;
+    bool finite = true;
+    for (int64_t r = 0; r < rows && finite; r++) finite = std::isfinite(scales[r]);
+    c->scales_finite = finite;
     c->sets = sets;
     c->n = n;
     c->d = d;
@@ -644,15 +648,16 @@ struct MqPlan {
     std::vector<MqPass> passes;
 };
 
-constexpr int kMqWorkgroups = 512;     // two workgroups per CU of a 256-CU MI355X
+constexpr int kMqWorkgroups = 512;     // two 256-thread workgroups per CU of a 256-CU MI355X
+constexpr int kMq8Workgroups = 256;    // one 512-thread workgroup per CU
 constexpr int64_t kMqSelectKeys = 16384;  // LDS keys of the select kernel
 
-MqPass mq_pass(int64_t begin, int64_t end, int chunk, int groups, int64_t max_rows_per_wg) {
+MqPass mq_pass(int64_t begin, int64_t end, int chunk, int groups, int64_t max_rows_per_wg, int wgs) {
     MqPass p;
     p.begin = begin;
     p.end = end;
     const int64_t chunks = (end - begin + chunk - 1) / chunk;
-    int64_t R = std::max<int64_t>(1, std::min<int64_t>(chunks, kMqWorkgroups / groups));
+    int64_t R = std::max<int64_t>(1, std::min<int64_t>(chunks, std::max(1, wgs / groups)));
     int64_t cpw = (chunks + R - 1) / R;
     if (max_rows_per_wg > 0) cpw = std::max<int64_t>(1, std::min<int64_t>(cpw, max_rows_per_wg / chunk));
     p.rows_per_wg = cpw * chunk;
@@ -665,8 +670,16 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
     if (c->sets != 1 || nq < 8) return p;
     const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
     if (c->format == MANTA_ROCM_Q8_ROWS) {
-        if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
-        p.sh = manta::mq_shape(dop, c->pitch / 32, nq);
+        // q8 dot with at least one full 512-query group: the 16x16x64 kernel
+        // (top-k only; its free chunk tile must hold a region for compaction)
+        const int rc8 = (int)(((2 * k + 2 * 64 + 64) + 63) / 64 * 64);
+        if (topk && dop == manta::OP_DOT && nq >= 512 && c->scales_finite && manta::mq8_supported(c->pitch) &&
+            (size_t)rc8 * 8 <= (size_t)manta::mq8_shape(c->pitch).tile) {
+            p.sh = manta::mq8_shape(c->pitch);
+        } else {
+            if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
+            p.sh = manta::mq_shape(dop, c->pitch / 32, nq);
+        }
     } else {
         if (!manta::mq4_supported_nb(c->nb)) return p;
         p.q4 = true;
@@ -675,8 +688,9 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
     p.groups = (int)((nq + p.sh.qg - 1) / p.sh.qg);
     if (p.groups > 65535) return p;
     const int chunk = p.sh.chunk;
+    const int wgs = p.sh.kind == 1 ? kMq8Workgroups : kMqWorkgroups;
     if (!topk) {
-        p.passes.push_back(mq_pass(0, c->n, chunk, p.groups, 0));
+        p.passes.push_back(mq_pass(0, c->n, chunk, p.groups, 0, wgs));
         p.rmax = p.passes[0].R;
         p.lds = (size_t)p.sh.tile_bytes;
         p.use = true;
@@ -685,10 +699,11 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
     // region: the best k after a compaction plus one chunk of appends, with
     // slack so a compaction frees at least k slots
     p.rc = (int)(((2 * k + 2 * chunk + 64) + 63) / 64 * 64);
-    p.lds = (size_t)p.sh.tile_bytes + ((size_t)p.rc * 8 > (size_t)p.sh.tile ? (size_t)p.rc * 8 : 0);
+    p.lds = (size_t)p.sh.tile_bytes +
+            (p.sh.kind == 0 && (size_t)p.rc * 8 > (size_t)p.sh.tile ? (size_t)p.rc * 8 : 0);
     // pass 0: everything is kept, so a workgroup takes at most rc - 2*chunk rows
     int64_t s = std::min<int64_t>(c->n, std::max<int64_t>(8 * k, 4096));
-    p.passes.push_back(mq_pass(0, s, chunk, p.groups, p.rc - 2 * chunk));
+    p.passes.push_back(mq_pass(0, s, chunk, p.groups, p.rc - 2 * chunk, wgs));
     p.passes.back().select_threads = manta::mq_select_threads(s);
     if (s < c->n) {
         // later passes grow the prefix by g: about k*g keys per query reach
@@ -701,7 +716,7 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
         for (int i = 0; i < npass; i++) {
             const int64_t e = i + 1 == npass ? c->n : std::min<int64_t>(c->n, (int64_t)std::ceil(s * g));
             if (e <= s) continue;
-            p.passes.push_back(mq_pass(s, e, chunk, p.groups, 0));
+            p.passes.push_back(mq_pass(s, e, chunk, p.groups, 0, wgs));
             p.passes.back().select_threads = manta::mq_select_threads(k + (int64_t)(k * (g - 1.0) * 1.5));
             s = e;
         }
@@ -715,6 +730,7 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
 
 hipError_t launch_mq_pass(const MqPlan& p, int dop, const manta::MqArgs& a, int R, hipStream_t s) {
     const dim3 grid((unsigned)R, (unsigned)p.groups);
+    if (p.sh.kind == 1) return manta::launch_mq8_scan(p.sh, a, grid, p.lds, s);
     return p.q4 ? manta::launch_mq4_scan(dop, p.sh, a, grid, p.lds, s) : manta::launch_mq_scan(dop, p.sh, a, grid, p.lds, s);
 }
 

@@ -305,6 +305,73 @@ def test_multi_query_all_ties(rt, op):
 
 
 # ---------------------------------------------------------------------------
+# q8 dot with 512 or more queries: the 512-query 16x16x64 kernel.
+
+@pytest.mark.parametrize("smallest", [False, True])
+@pytest.mark.parametrize("nq,n,d,k", [(512, 6000, 384, 50), (600, 5003, 128, 10), (1024, 4500, 256, 1),
+                                      (520, 3000, 384, 300)])
+def test_q8_dot_512_queries_bit_exact(rt, smallest, nq, n, d, k):
+    """A full and a partial 512-query group, row counts that leave a
+    partial last chunk; ids, scores and accumulators bit-exact."""
+    q, codes, scales = _q8_case(nq + n + d + k, nq, n, d, sets=1)
+    cands = rt.bind_q8(codes[0], scales[0])
+    ids, sc, acc = rt.score_topk(cands, "dot", rt.to_device(q), k, smallest=smallest, with_acc=True)
+    ids, sc, acc = ids.download(), sc.download(), acc.download()
+    want_s, want_acc = orc.score_q8("dot", q, codes[0], scales[0], with_acc=True)
+    want_ids = orc.topk(want_s, k, smallest=smallest)
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_array_equal(sc, np.take_along_axis(want_s, want_ids, 1))
+    np.testing.assert_array_equal(acc, np.take_along_axis(want_acc, want_ids, 1))
+    cands.close()
+
+
+@pytest.mark.parametrize("k", [7, 100])
+def test_q8_dot_512_queries_adversarial_row_order(rt, k):
+    """Rows ranked worst first for every query: regions fill and are
+    compacted inside the 512-query kernel."""
+    nq, n, d = 512, 60000, 128
+    q, codes, scales = _ordered_case("dot", nq, n, d, k)
+    cands = rt.bind_q8(codes, scales)
+    ids, sc, _ = rt.score_topk(cands, "dot", rt.to_device(q), k)
+    want_s = orc.score_q8("dot", q, codes, scales)
+    want_ids = orc.topk(want_s, k)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    cands.close()
+
+
+@pytest.mark.parametrize("smallest", [False, True])
+def test_q8_dot_512_queries_all_ties(rt, smallest):
+    nq, n, d, k = 512, 20000, 384, 64
+    q = synth.normal_f16(6, 0, nq, d, 1.0, normalize=True)
+    codes1, scale1 = synth.q8_rows(6, 1, 1, d, normalize=True)
+    codes = np.repeat(codes1, n, axis=0)
+    scales = np.repeat(scale1, n)
+    cands = rt.bind_q8(codes, scales)
+    ids, _, _ = rt.score_topk(cands, "dot", rt.to_device(q), k, smallest=smallest)
+    want = orc.topk(orc.score_q8("dot", q, codes, scales), k, smallest=smallest)
+    np.testing.assert_array_equal(ids.download(), want)
+    np.testing.assert_array_equal(want, np.tile(np.arange(k), (nq, 1)))
+    cands.close()
+
+
+def test_q8_dot_512_queries_negative_scales(rt):
+    """Negative row scales flip the order of a row's scores; the pre-filter
+    (scale*acc against the bound) and the exact test stay consistent."""
+    nq, n, d, k = 512, 3000, 128, 20
+    q, codes, scales = _q8_case(77, nq, n, d, sets=1)
+    scales = scales.copy()
+    scales[0, ::7] *= -1.0
+    cands = rt.bind_q8(codes[0], scales[0])
+    ids, sc, _ = rt.score_topk(cands, "dot", rt.to_device(q), k)
+    want_s = orc.score_q8("dot", q, codes[0], scales[0])
+    want_ids = orc.topk(want_s, k)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    cands.close()
+
+
+# ---------------------------------------------------------------------------
 # Many queries against one shared q4 matrix (the q4 matrix-core path).
 
 def _q4_case(seed, nq, n, d, normalize=True):
