@@ -92,6 +92,8 @@ struct MqSelectArgs {
     int32_t* out_ids;           // final pass: [nq][k] ids (else nullptr)
     float* out_scores;          // final pass: [nq][k] scores or nullptr
     int smallest;
+    int raw_dot;                // regions hold q8 dot pairs (bits of p = scale*acc) << 32 | row
+    const QConst* qconst;       // [nq] (raw_dot: the key's score is p*qmax/127)
 };
 
 // Launch shape of the scan kernel for an op, K steps (pitch / 32) and query count.

@@ -472,6 +472,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     };
 
     const uint64_t* regq = a.regions + (int64_t)q * a.rc;  // region w at regq + w*nq*rc
+    const float qmax = a.raw_dot ? a.qconst[q].a : 0.0f;
     for (int base = 0; base < M;) {
         const int take = (M - base) < (LCAP - fill) ? (M - base) : (LCAP - fill);
         // batches of 8 independent loads per thread keep many in flight
@@ -490,6 +491,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
                         else hi = mid;
                     }
                     v[t] = regq[(int64_t)lo * a.nq * a.rc + (g - pre[lo])];
+                    if (a.raw_dot) v[t] = dot_pair_key(v[t], qmax, a.smallest);
                 }
             }
 #pragma unroll

@@ -15,8 +15,10 @@
 // block.  The filter is one fma per (query, row): scale*acc - bound, with
 // the bound loosened past the exact test's, reduced by v_max3 over a query
 // block's 8 pairs per lane; only a block with a passing lane takes the
-// exact f32 test and builds keys.  Row scales must be finite (the runtime
-// routes candidates with a non-finite scale to kernels_mq.hip).
+// exact f32 test p = fmul_rn(scale, acc) against the bound.  A pair that
+// passes goes to its region as (bits of p) << 32 | row: the division and the
+// key are left to the select kernel, where every lane has one.  Row scales
+// must be finite (the runtime routes other candidates to kernels_mq.hip).
 //
 // The LDS tile stores row r's 16-byte column c at column c ^ ((r >> 1) & 7)
 // (PITCH is a multiple of 128, so a row holds a multiple of 8 columns): the
@@ -147,9 +149,8 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         return SMALL ? __fmaf_rn(-scale, (float)acc, b) : __fmaf_rn(scale, (float)acc, -b);
     };
 
-    // Exact scores and keys of one query block of a row pair, in a wave
-    // where one of its pairs passed the pre-filter: only those pairs take the
-    // exact test (the same f32 steps as the scalar dot epilogue).
+    // The pairs of one query block of a row pair that pass the exact test,
+    // appended as (pre-score, row) pairs (a wave where one passed the filter).
     auto survivors = [&](const v4i (&acc)[2][4], int qb, int64_t rb0, const float (&sc)[2], const float (&bq)[4]) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -160,14 +161,9 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                 if (!valid || !(pre(sc[h], acc[h][qb][r], bq[r]) >= 0.0f)) continue;
                 const int lq = lw + qb * 16 + 4 * g + r;
                 const float p = fmul_rn(sc[h], (float)acc[h][qb][r]);
-                const float bv = bnd_s[lq];
-                if (SMALL ? (p > bv) : (p < bv)) continue;
-                const float score = fdiv_rn(fmul_rn(p, qa_s[lq]), 127.0f);
-                const uint64_t key = make_key(score, (uint32_t)row, SMALL);
-                if (key > tau_s[lq]) {
-                    const int pos = atomicAdd(&cnt_s[lq], 1);
-                    wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = key;
-                }
+                if (SMALL ? (p > bnd_s[lq]) : (p < bnd_s[lq])) continue;
+                const int pos = atomicAdd(&cnt_s[lq], 1);
+                wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = dot_pair(p, (uint32_t)row);
             }
         }
     };
@@ -197,25 +193,31 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
             for (int w = 0; w < NFW; w++) any |= flags[par][w] != 0;
             if (any) {
-                // rare: compact full regions to their best k keys
-                uint64_t* scratch = (uint64_t*)(tiles + nbuf * TILE);
+                // rare: compact full regions to their best k pairs (the
+                // scratch tile holds the region's keys, then its pairs)
+                uint64_t* skeys = (uint64_t*)(tiles + nbuf * TILE);
+                uint64_t* spairs = skeys + a.rc;
                 for (int lq = 0; lq < QG; lq++) {
                     if (!((flags[par][lq >> 6] >> (lq & 63)) & 1)) continue;
                     uint64_t* reg = wreg + (uint32_t)((q0 + lq) * a.rc);
                     const int c = cnt_s[lq];
-                    for (int i = tid; i < c; i += kMq8Threads) scratch[i] = reg[i];
+                    for (int i = tid; i < c; i += kMq8Threads) {
+                        const uint64_t e = reg[i];
+                        spairs[i] = e;
+                        skeys[i] = dot_pair_key(e, qa_s[lq], SMALL);
+                    }
                     if (tid == 0) {
                         wpos = 0;
                         minkey = ~0ull;
                     }
                     __syncthreads();
                     uint64_t prefix, pmask;
-                    block_radix_prefix(scratch, c, a.k, ss, prefix, pmask);
+                    block_radix_prefix(skeys, c, a.k, ss, prefix, pmask);
                     uint64_t lo = ~0ull;
                     for (int i = tid; i < c; i += kMq8Threads) {
-                        const uint64_t key = scratch[i];
+                        const uint64_t key = skeys[i];
                         if ((key & pmask) >= prefix) {
-                            reg[atomicAdd(&wpos, 1)] = key;
+                            reg[atomicAdd(&wpos, 1)] = spairs[i];
                             lo = key < lo ? key : lo;
                         }
                     }

@@ -43,6 +43,16 @@ __device__ __forceinline__ float mq_bound(uint64_t tk, const QConst& qc, bool sm
     return fmul_rn(smallest ? loosen_up(ts) : loosen_down(ts), qc.b);
 }
 
+// q8 dot regions of the 512-query kernel hold (bits of p) << 32 | row with
+// p = fmul_rn(scale, acc); the key is the scalar dot epilogue's score.
+__device__ __forceinline__ uint64_t dot_pair(float p, uint32_t row) {
+    return ((uint64_t)__float_as_uint(p) << 32) | row;
+}
+__device__ __forceinline__ uint64_t dot_pair_key(uint64_t e, float qmax, bool smallest) {
+    const float p = __uint_as_float((uint32_t)(e >> 32));
+    return make_key(fdiv_rn(fmul_rn(p, qmax), 127.0f), (uint32_t)e, smallest);
+}
+
 // Direct global->LDS loads (gfx950): each lane's 16 (or 4) bytes land at
 // M0 + 16*lane (4*lane) of the wave's LDS segment.  Issued from inline asm so
 // the compiler does not wait for them around LDS reads of other tiles; the

@@ -671,10 +671,11 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
     const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
     if (c->format == MANTA_ROCM_Q8_ROWS) {
         // q8 dot with at least one full 512-query group: the 16x16x64 kernel
-        // (top-k only; its free chunk tile must hold a region for compaction)
+        // (top-k only; its free chunk tile holds a region's pairs and keys
+        // when it compacts one)
         const int rc8 = (int)(((2 * k + 2 * 64 + 64) + 63) / 64 * 64);
         if (topk && dop == manta::OP_DOT && nq >= 512 && c->scales_finite && manta::mq8_supported(c->pitch) &&
-            (size_t)rc8 * 8 <= (size_t)manta::mq8_shape(c->pitch).tile) {
+            (size_t)rc8 * 16 <= (size_t)manta::mq8_shape(c->pitch).tile) {
             p.sh = manta::mq8_shape(c->pitch);
         } else {
             if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
@@ -711,7 +712,11 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
         // smallest g that still needs no more of them.
         const double span = (double)c->n / (double)s;
         const double gmax = std::max(4.0, (double)kMqSelectKeys / (double)k);
-        const int npass = std::max(1, (int)std::ceil(std::log(span) / std::log(gmax) - 1e-9));
+        int npass = std::max(1, (int)std::ceil(std::log(span) / std::log(gmax) - 1e-9));
+        // the 512-query kernel appends about k*g pairs per query and pass:
+        // keep g near 10 (k*g*npass is smallest there for the spans that
+        // occur) at one select per pass
+        if (p.sh.kind == 1) npass = std::max(npass, (int)std::ceil(std::log(span) / std::log(12.0) - 1e-9));
         const double g = std::pow(span, 1.0 / npass);
         for (int i = 0; i < npass; i++) {
             const int64_t e = i + 1 == npass ? c->n : std::min<int64_t>(c->n, (int64_t)std::ceil(s * g));
@@ -802,6 +807,9 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
     sa.k = (int)k;
     sa.nq = (int)nq;
     sa.smallest = a.smallest;
+    // the 512-query kernel's regions hold (pre-score, row) pairs
+    sa.raw_dot = p.sh.kind == 1;
+    sa.qconst = qc;
     for (size_t i = 0; i < p.passes.size(); i++) {
         const MqPass& ps = p.passes[i];
         a.row_begin = ps.begin;
