@@ -137,7 +137,7 @@ def run_c1(rt, steps, warmup) -> dict:
     td, md, tbd, pd = (rt.to_device(x) for x in (tokens, mask, table, proj))
     out = rt.empty((b, e), np.uint16)
     step_s, fam, dev_ms = _timed(rt, lambda: rt.embed_pooled(td, md, tbd, pd, out=out), steps, warmup,
-                                 ["embed", "embed_finalize"])
+                                 ["embed", "embed_transpose", "embed_finalize"])
     flops = 2.0 * b * t * d * e
     k_ms = fam["embed"][1]
     achieved = flops / (k_ms / 1000.0) / 1e12
@@ -145,11 +145,12 @@ def run_c1(rt, steps, warmup) -> dict:
         "workload": "c1_embed_f16", "shape": {"b": b, "t": t, "vocab": table.shape[0], "d": d, "e": e},
         "value": b * t / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0,
         "device_ms_per_step": dev_ms,
-        "roofline": {"bound": "mfma", "kernel": "embed_gemm_kernel<gather,f16,pool> (f16 MFMA 32x32x16)",
+        "roofline": {"bound": "mfma", "kernel": "embed_gemm2_kernel<gather,f16,pool> (f16 MFMA 32x32x16)",
                      "achieved": achieved, "peak": F16_PEAK, "unit": "TFLOP/s", "frac": achieved / F16_PEAK,
                      "avg_launch_us": k_ms * 1000.0, "flops_per_launch": flops,
                      "note": "flops counted over all B*T positions (masked ones included), as the reference computes them"},
         "finalize_us": fam["embed_finalize"][1] * 1000.0,
+        "transpose_us": fam["embed_transpose"][1] * 1000.0,
     }
 
 
@@ -238,7 +239,7 @@ def run_c4(rt, steps, warmup) -> dict:
         rt.embed_pooled(td, md, tbd, pd, csd, out=emb)
         rt.score_topk(cands, "dot", emb, k, out=(ids, sc, None))
 
-    fams = ["embed", "embed_finalize", "mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
+    fams = ["embed", "embed_transpose", "embed_finalize", "mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
     step_s, fam, dev_ms = _timed(rt, step, steps, warmup, fams)
     flops_a = 2.0 * b * t * d * e
     ops_b = 2.0 * b * n * d

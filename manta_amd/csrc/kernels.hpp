@@ -149,6 +149,14 @@ struct EmbedArgs {
 };
 
 hipError_t launch_embed_gemm(const EmbedArgs& a, bool gather, bool q8b, bool pool, hipStream_t s);
+// Pipelined GEMM for K % 32 == 0 and N % 128 == 0: launch_embed_transpose_b
+// writes the projection as Bt (f16 [N][K], N*K*2 bytes, int8 codes widened
+// exactly), then launch_embed_gemm2 runs 256-row x 128-column workgroup tiles
+// over it; same outputs as launch_embed_gemm.
+bool embed_gemm2_supported(const EmbedArgs& a);
+hipError_t launch_embed_transpose_b(const EmbedArgs& a, bool q8b, uint16_t* Bt, hipStream_t s);
+hipError_t launch_embed_gemm2(const EmbedArgs& a, bool gather, bool q8b, bool pool, const uint16_t* Bt,
+                              hipStream_t s);
 hipError_t launch_embed_finalize(const float* P, int tiles, const int32_t* mask, int64_t B, int64_t T,
                                  int N, uint16_t* out, hipStream_t s);
 hipError_t launch_gather_rows_f16(const uint16_t* table, int64_t vocab, int64_t d, const int32_t* idx,

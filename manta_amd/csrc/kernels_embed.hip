@@ -201,6 +201,210 @@ __global__ __launch_bounds__(256) void embed_gemm_kernel(EmbedArgs a) {
     }
 }
 
+// ------------------------------------------------ pipelined GEMM (K%32, N%128)
+
+// Direct-to-LDS loads (gfx950): each lane's 16 bytes land at M0 + 16*lane.
+__device__ __forceinline__ void eg_lds_load16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+// vmcnt(J*L) + barrier while at least J chunks were issued after the current
+// one, else the next smaller J (a smaller count only waits longer).
+template <int L, int J>
+__device__ __forceinline__ void eg_wait_barrier(int after) {
+    if constexpr (J <= 0) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+        if (after >= J)
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(J * L) : "memory");
+        else
+            eg_wait_barrier<L, J - 1>(after);
+    }
+}
+
+// Bt[n][k] = B[k][n] as f16 (a q8 projection widened exactly; its column
+// scale is applied in the GEMM epilogue), so both MFMA operands are rows.
+__global__ void embed_transpose_b_kernel(const void* __restrict__ B, int q8, int K, int N,
+                                         uint16_t* __restrict__ Bt) {
+    __shared__ uint16_t t[32][33];
+    const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int r = ty; r < 32; r += 8) {
+        const int k = k0 + r, n = n0 + tx;
+        uint16_t v = 0;
+        if (k < K && n < N)
+            v = q8 ? f2h((float)((const int8_t*)B)[(int64_t)k * N + n]) : ((const uint16_t*)B)[(int64_t)k * N + n];
+        t[r][tx] = v;
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int n = n0 + r, k = k0 + tx;
+        if (n < N && k < K) Bt[(int64_t)n * K + k] = t[tx][r];
+    }
+}
+
+// Workgroup: 4 waves stacked in M, each a 64-row tile (pooled mode: 64
+// positions of one sequence) x 128 columns, as 2 x 4 tiles of
+// v_mfma_f32_32x32x16_f16.  K moves in chunks of 32 through a 3-stage ring
+// of LDS buffers filled by direct-to-LDS loads (A rows gathered by token id
+// straight from the table); each 64-byte LDS row stores its 16-byte column c
+// at c ^ ((row >> 2) & 3), so the 32 lanes reading one column of 32 rows
+// spread over the banks.  Rows past the tile's range, masked or with a bad
+// token id read row 0 and are left out of the store or the pool.
+constexpr int EG_WM = 64, EG_WN = 128, EG_KC = 32, EG_NST = 3;
+constexpr int EG_AST = 4 * EG_WM * EG_KC * 2;  // A bytes per stage (256 rows)
+constexpr int EG_BST = EG_WN * EG_KC * 2;      // B bytes per stage
+constexpr int EG_STAGE = EG_AST + EG_BST;
+
+template <bool GATHER, bool Q8B, bool POOL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void embed_gemm2_kernel(EmbedArgs a,
+                                                                                                 const uint16_t* Bt) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n0 = blockIdx.y * EG_WN;
+    const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+    const int64_t ntiles = POOL ? a.batches * a.tiles_per_seq : (a.M + EG_WM - 1) / EG_WM;
+    int64_t seq = 0, t0 = 0, m0 = 0;
+    if (POOL) {
+        seq = tile / a.tiles_per_seq;
+        t0 = (tile % a.tiles_per_seq) * EG_WM;
+    } else {
+        m0 = tile * EG_WM;
+    }
+
+    // source rows of this lane's 4 A segments: rows 16 s + lane/4 of the tile
+    const uint8_t* arow[4];
+#pragma unroll
+    for (int sg = 0; sg < 4; sg++) {
+        const int r = sg * 16 + (lane >> 2);
+        int64_t src = 0;  // row of the table (gather) or of A
+        if (tile < ntiles) {
+            if (POOL) {
+                const int64_t t = t0 + r;
+                if (t < a.T) {
+                    const int idx = a.tokens[seq * a.T + t];
+                    if (idx >= 0 && idx < a.vocab) src = idx;
+                    else report_bad_index(a.err, idx);
+                }
+            } else {
+                const int64_t m = m0 + r;
+                if (m < a.M) {
+                    if (GATHER) {
+                        const int idx = a.tokens[m];
+                        if (idx >= 0 && idx < a.vocab) src = idx;
+                        else report_bad_index(a.err, idx);
+                    } else {
+                        src = m;
+                    }
+                }
+            }
+        }
+        const int c = (lane & 3) ^ ((r >> 2) & 3);  // global 16-byte column of the stored one
+        arow[sg] = (const uint8_t*)(GATHER ? a.table : a.A) + src * a.K * 2 + c * 16;
+    }
+    const uint8_t* brow[2];
+#pragma unroll
+    for (int sg = 0; sg < 2; sg++) {
+        const int n = (wave * 2 + sg) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((n >> 2) & 3);
+        brow[sg] = (const uint8_t*)Bt + (int64_t)(n0 + n) * a.K * 2 + c * 16;
+    }
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
+    auto issue = [&](int kc, int st) {
+        const uint32_t sa = __builtin_amdgcn_readfirstlane(base + st * EG_STAGE + wave * 4 * 1024);
+#pragma unroll
+        for (int sg = 0; sg < 4; sg++) eg_lds_load16(arow[sg] + kc * EG_KC * 2, sa + sg * 1024);
+        const uint32_t sb = __builtin_amdgcn_readfirstlane(base + st * EG_STAGE + EG_AST + wave * 2 * 1024);
+#pragma unroll
+        for (int sg = 0; sg < 2; sg++) eg_lds_load16(brow[sg] + kc * EG_KC * 2, sb + sg * 1024);
+    };
+    const int nk = a.K / EG_KC;
+#pragma unroll
+    for (int st = 0; st < EG_NST - 1; st++)
+        if (st < nk) issue(st, st);
+
+    f16v acc[2][4];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
+
+    const int l32 = lane & 31, hf = lane >> 5;
+    int st = 0;
+    for (int kc = 0; kc < nk; kc++, st = st == EG_NST - 1 ? 0 : st + 1) {
+        eg_wait_barrier<6, EG_NST - 2>(nk - 1 - kc);
+        if (kc + EG_NST - 1 < nk) issue(kc + EG_NST - 1, st == 0 ? EG_NST - 1 : st - 1);
+        const uint8_t* As = smem + st * EG_STAGE + wave * EG_WM * EG_KC * 2;
+        const uint8_t* Bs = smem + st * EG_STAGE + EG_AST;
+#pragma unroll
+        for (int ks = 0; ks < EG_KC / 16; ks++) {
+            const int c = ks * 2 + hf;  // 16-byte column of this lane's 8 k
+            h8 av[2], bv[4];
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++) {
+                const int r = rb * 32 + l32;
+                av[rb] = *(const h8*)(As + r * 64 + ((c ^ ((r >> 2) & 3)) * 16));
+            }
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                const int n = cb * 32 + l32;
+                bv[cb] = *(const h8*)(Bs + n * 64 + ((c ^ ((n >> 2) & 3)) * 16));
+            }
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++)
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[rb], bv[cb], acc[rb][cb], 0, 0, 0);
+        }
+    }
+    if (tile >= ntiles) return;
+
+    // Output element (rb, cb, r): row rb*32 + 8*(r/4) + 4*(lane/32) + r%4 of
+    // the wave's tile, column cb*32 + lane%32.
+    if (!POOL) {
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++) {
+            const int n = n0 + cb * 32 + l32;
+            const float cs = Q8B ? a.colscale[n] : 1.0f;
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int64_t m = m0 + rb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+                    if (m < a.M) a.Y[m * a.N + n] = Q8B ? acc[rb][cb][r] * cs : acc[rb][cb][r];
+                }
+        }
+        return;
+    }
+    bool live[2][16];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int64_t t = t0 + rb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            live[rb][r] = t < a.T && (!a.mask || a.mask[seq * a.T + t] != 0);
+        }
+#pragma unroll
+    for (int cb = 0; cb < 4; cb++) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                if (live[rb][r]) sum += acc[rb][cb][r];
+        sum += __shfl_xor(sum, 32);
+        const int n = n0 + cb * 32 + l32;
+        if (hf == 0) {
+            if (Q8B) sum *= a.colscale[n];
+            a.P[(seq * a.tiles_per_seq + t0 / EG_WM) * a.N + n] = sum;
+        }
+    }
+}
+
 // Sum the row-tile partials of one sequence in order, divide by the number
 // of unmasked positions (count 0 -> zeros), L2-normalize (f64 sum of
 // squares, f32 norm, zero norm leaves the row unchanged) and round to f16.
@@ -292,6 +496,36 @@ __global__ void normalize_rows_kernel(float* __restrict__ x, int64_t rows, int64
 }
 
 // ----------------------------------------------------------------- hosts
+
+bool embed_gemm2_supported(const EmbedArgs& a) { return a.K % EG_KC == 0 && a.K > 0 && a.N % EG_WN == 0 && a.N > 0; }
+
+size_t embed_gemm2_lds() { return (size_t)EG_NST * EG_STAGE; }
+
+hipError_t launch_embed_transpose_b(const EmbedArgs& a, bool q8b, uint16_t* Bt, hipStream_t s) {
+    hipLaunchKernelGGL(embed_transpose_b_kernel, dim3((unsigned)((a.N + 31) / 32), (unsigned)((a.K + 31) / 32)),
+                       dim3(256), 0, s, a.B, q8b ? 1 : 0, a.K, a.N, Bt);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_gemm2(const EmbedArgs& a, bool gather, bool q8b, bool pool, const uint16_t* Bt,
+                              hipStream_t s) {
+    const int64_t tiles = pool ? a.batches * a.tiles_per_seq : (a.M + EG_WM - 1) / EG_WM;
+    dim3 grid((unsigned)((tiles + 3) / 4), (unsigned)(a.N / EG_WN));
+    const size_t lds = embed_gemm2_lds();
+#define MANTA_EG2(G, Q, P)                                                                          \
+    if (gather == G && q8b == Q && pool == P) {                                                     \
+        hipLaunchKernelGGL((embed_gemm2_kernel<G, Q, P>), grid, dim3(256), lds, s, a, Bt);                \
+        return hipGetLastError();                                                                   \
+    }
+    MANTA_EG2(true, false, true)
+    MANTA_EG2(true, true, true)
+    MANTA_EG2(false, false, false)
+    MANTA_EG2(false, true, false)
+    MANTA_EG2(true, false, false)
+    MANTA_EG2(true, true, false)
+#undef MANTA_EG2
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_embed_gemm(const EmbedArgs& a, bool gather, bool q8b, bool pool, hipStream_t s) {
     const int64_t rows_tiles = pool ? a.batches * a.tiles_per_seq : (a.M + EM - 1) / EM;

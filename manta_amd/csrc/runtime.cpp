@@ -1007,8 +1007,15 @@ int manta_rocm_matmul_f16(MantaRocm* rt, const uint16_t* lhs, int64_t m, int64_t
     a.B = rhs;
     a.colscale = col_scale;
     a.Y = out;
-    LAUNCH_TRY(manta::launch_embed_gemm(a, false, proj_kind == MANTA_ROCM_PROJ_Q8_COL, false, rt->stream),
-               "matmul");
+    const bool q8b = proj_kind == MANTA_ROCM_PROJ_Q8_COL;
+    if (manta::embed_gemm2_supported(a)) {
+        rc = ensure_workspace(rt, (size_t)n * k * 2 + 256, err);
+        if (rc) return rc;
+        LAUNCH_TRY(manta::launch_embed_transpose_b(a, q8b, (uint16_t*)rt->ws, rt->stream), "embed_transpose");
+        LAUNCH_TRY(manta::launch_embed_gemm2(a, false, q8b, false, (const uint16_t*)rt->ws, rt->stream), "matmul");
+        return MANTA_ROCM_OK;
+    }
+    LAUNCH_TRY(manta::launch_embed_gemm(a, false, q8b, false, rt->stream), "matmul");
     return MANTA_ROCM_OK;
 }
 
@@ -1043,7 +1050,8 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
     if (rc) return rc;
     const int64_t tiles = (t + 63) / 64;
     if (b * tiles > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: batch too large");
-    rc = ensure_workspace(rt, (size_t)(b * tiles * e) * sizeof(float) + 256, err);
+    const size_t pbytes = align_up((size_t)(b * tiles * e) * sizeof(float), 256);
+    rc = ensure_workspace(rt, pbytes + (size_t)d * e * 2 + 256, err);
     if (rc) return rc;
     manta::EmbedArgs a{};
     a.tokens = tokens;
@@ -1059,8 +1067,15 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
     a.colscale = col_scale;
     a.P = (float*)rt->ws;
     a.err = rt->err_word;
-    LAUNCH_TRY(manta::launch_embed_gemm(a, true, proj_kind == MANTA_ROCM_PROJ_Q8_COL, true, rt->stream),
-               "embed");
+    const bool q8b = proj_kind == MANTA_ROCM_PROJ_Q8_COL;
+    if (manta::embed_gemm2_supported(a)) {
+        // the projection transposed to f16 [e][d] after the partials
+        uint16_t* bt = (uint16_t*)((char*)rt->ws + pbytes);
+        LAUNCH_TRY(manta::launch_embed_transpose_b(a, q8b, bt, rt->stream), "embed_transpose");
+        LAUNCH_TRY(manta::launch_embed_gemm2(a, true, q8b, true, bt, rt->stream), "embed");
+    } else {
+        LAUNCH_TRY(manta::launch_embed_gemm(a, true, q8b, true, rt->stream), "embed");
+    }
     LAUNCH_TRY(manta::launch_embed_finalize(a.P, (int)tiles, mask, b, t, (int)e, out, rt->stream),
                "embed_finalize");
     rt->gather_pending = true;
