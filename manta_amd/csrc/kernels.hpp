@@ -43,6 +43,31 @@ struct ScanArgs {
 
 hipError_t launch_query_encode(const uint16_t* q, int nq, int d, int pitch, int e16, int8_t* c8,
                                int8_t* hi, int8_t* lo, QConst* qc, hipStream_t s);
+
+// Error bounds of the int8 shadow of a q4 matrix: maxima over its rows of
+// E_r = |x_r - t_r e_r| and F_r = t_r |e_r| (x_r the dequantized q4 row, e_r
+// its int8 codes, t_r their scale), divided by |x_r| for cosine, and of
+// |x_r|; f32 bit patterns (non-negative, so integer max is float max),
+// rounded up.
+struct ShadowInfo {
+    unsigned int me_cos, mf_cos;
+    unsigned int me_dot, mf_dot;
+    unsigned int maxn;
+    unsigned int pad[3];
+};
+// Build the shadow of n q4 rows of length d (d <= 384): int8 codes
+// [n][spitch] (zero padded), per-row scales t_r (dot) and t_r / dnorm_r
+// (cosine), and the bounds (info must hold zeros; see launch_shadow_info_clear).
+hipError_t launch_shadow_info_clear(ShadowInfo* info, hipStream_t s);
+hipError_t launch_q4_shadow_build(const uint8_t* packed, const uint16_t* scales, const float* dnorm, int64_t n,
+                                  int d, int spitch, int8_t* codes, float* sc_dot, float* sc_cos,
+                                  ShadowInfo* info, hipStream_t s);
+// Queries for the shadow scan: full-range int8 codes c8 [nq][spitch] with
+// qa = maxabs/127, E16 digit planes in the q4 order hi/lo [nq][d], E16
+// constants qc, and per query the margin m and factor f of shadow_bound for
+// op (OP_COSINE or OP_DOT): qb[2q] = m, qb[2q+1] = f.
+hipError_t launch_query_encode_shadow(const uint16_t* q, int nq, int d, int spitch, int op, const ShadowInfo* info,
+                                      int8_t* c8, int8_t* hi, int8_t* lo, QConst* qc, float* qb, hipStream_t s);
 hipError_t launch_q8_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s);
 // Pitches served by the coalesced q8 kernel (the others use the row-per-lane one).
 bool q8_scan_coalesced(int pitch);
@@ -76,6 +101,13 @@ struct MqArgs {
     int k;
     float* out_scores;          // score-matrix mode [nq][n], else nullptr
     int smallest;
+    // int8 shadow of a q4 matrix (mq8 kernel, shadow mode): codes / scales
+    // above are the shadow's, these the q4 matrix's for exact rescoring
+    const float* qbound;        // [nq][2] margin m and factor f (shadow_bound)
+    const uint8_t* q4codes;     // [n][d/2]
+    const uint16_t* q4scales;   // [n][d/32]
+    int d;
+    int op;                     // OP_COSINE or OP_DOT
 };
 
 // Arguments of the per-query merge after a pass.
@@ -92,13 +124,26 @@ struct MqSelectArgs {
     int32_t* out_ids;           // final pass: [nq][k] ids (else nullptr)
     float* out_scores;          // final pass: [nq][k] scores or nullptr
     int smallest;
-    int raw_dot;                // regions hold q8 dot pairs (bits of p = scale*acc) << 32 | row
-    const QConst* qconst;       // [nq] (raw_dot: the key's score is p*qmax/127)
+    int pairs;                  // region entries: 0 keys; 1 q8 dot pairs (bits of p = scale*acc) << 32 | row,
+                                // the key's score p*qmax/127; 2 shadow pairs, the key the exact q4 score
+    const QConst* qconst;       // [nq] (pairs 1: E8 qmax; pairs 2: E16 constants)
+    // pairs 2: the q4 matrix and the E16 digit planes in the q4 order [nq][d]
+    const uint8_t* q4codes;
+    const uint16_t* q4scales;
+    const float* dnorm;
+    const float* dd;
+    const int8_t* qhi;
+    const int8_t* qlo;
+    const float* qbound;        // [nq][2] the shadow margin m and factor f
+    int d;
+    int op;
 };
 
 // Launch shape of the scan kernel for an op, K steps (pitch / 32) and query count.
 struct MqShape {
-    int kind = 0;        // 0: mq_scan / mq_q4 (256 threads); 1: mq8_scan (512 threads, q8 dot)
+    int kind = 0;        // 0: mq_scan / mq_q4 (256 threads); 1: mq8_scan (512 threads, q8 dot or q4 shadow)
+    int ws = 1;          // kind 1: wave groups splitting a chunk's rows (queries per workgroup 512 / ws)
+    int shadow = 0;      // kind 1: q4 shadow mode
     int ks = 0;
     int na = 0;          // A blocks per wave
     int wq = 0;          // waves splitting the queries (1 or 4)
@@ -119,9 +164,10 @@ MqShape mq4_shape(int op, int nb, int64_t nq);
 bool mq4_supported_nb(int nb);
 hipError_t launch_mq4_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
 // q8 dot with many queries (kernels_mq8.hip): 512-thread workgroups of 512
-// queries on 16x16x64 i8 MFMAs, top-k mode only; pitch 128, 256 or 384.
+// (ws 1) or 256 (ws 2) queries on 16x16x64 i8 MFMAs, top-k mode only; pitch
+// 128, 256 or 384.  Shadow mode scans the int8 shadow of a q4 matrix.
 bool mq8_supported(int pitch);
-MqShape mq8_shape(int pitch);
+MqShape mq8_shape(int pitch, int ws, bool shadow);
 hipError_t launch_mq8_scan(const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s);
 int mq_select_threads(int64_t expect_keys);
 size_t mq_select_lds(int threads, int R);

@@ -27,6 +27,7 @@
 // mq_select_kernel then merges the previous best k with the pass's regions
 // into the new best k and the next pass's threshold.
 #include "mq_common.hpp"
+#include "q4_common.hpp"
 
 namespace manta {
 
@@ -389,8 +390,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 // threshold (the k-th key once k keys exist).  One workgroup per query.
 // Keys stream through an LDS buffer of NT*16 keys; whenever it fills, a
 // radix select keeps the best k.  The final pass writes ids and scores.
-template <int NT>
+template <int NT, int PM>
 __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
+    // PM: region entries are keys (0), q8 dot pairs (1) or shadow pairs (2)
     constexpr int KPT = 16;
     constexpr int LCAP = NT * KPT;
     constexpr int NW = NT / 64;
@@ -399,8 +401,10 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     int* pre = (int*)(smem + LCAP * 8);        // [R + 1]
     __shared__ RadixShared rs;
     __shared__ int wsum[NW];
-    __shared__ int wpos;
+    __shared__ int wpos, wpos2;
     __shared__ unsigned long long minkey;
+    __shared__ int qh_s[PM == 2 ? kMaxQueryDim / 4 : 1];
+    __shared__ int ql_s[PM == 2 ? kMaxQueryDim / 4 : 1];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int q = blockIdx.x;
@@ -472,9 +476,67 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     };
 
     const uint64_t* regq = a.regions + (int64_t)q * a.rc;  // region w at regq + w*nq*rc
-    const float qmax = a.raw_dot ? a.qconst[q].a : 0.0f;
+    const float qmax = PM == 1 ? a.qconst[q].a : 0.0f;
+    if (PM == 2) {
+        // the query's E16 digit planes, read by every rescoring below
+        const int words = a.d / 4;
+        for (int i = tid; i < words; i += NT) {
+            qh_s[i] = ((const int*)(a.qhi + (int64_t)q * a.d))[i];
+            ql_s[i] = ((const int*)(a.qlo + (int64_t)q * a.d))[i];
+        }
+        __syncthreads();
+    }
+    const QConst kq = PM == 2 ? a.qconst[q] : QConst{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Shadow pairs get their exact q4 score, one pair per thread: the row's
+    // nb <= 12 blocks and scales are loaded at once, then summed against the
+    // query planes and folded by the contract's fma chain in block order.
+    // e[i] holds raw pairs, or pre-score keys (pkeys) after pruning.
+    auto rescore = [&](uint64_t* e, int cnt, bool pkeys) {
+        const int nb = a.d / 32, hb = a.d / 2;
+        for (int i = tid; i < cnt; i += NT) {
+            // the query planes are re-read from LDS for every pair (kept in
+            // registers they would take 192 of them)
+            asm volatile("" ::: "memory");
+            const uint64_t v = e[i];
+            const uint32_t row = pkeys ? key_index(v) : (uint32_t)v;
+            const v4i* prow = (const v4i*)(a.q4codes + (int64_t)row * hb);
+            const uint16_t* srow = a.q4scales + (int64_t)row * nb;
+            v4i w[12];
+            uint16_t sb[12];
+#pragma unroll
+            for (int b = 0; b < 12; b++)
+                if (b < nb) w[b] = prow[b];
+            if ((nb & 3) == 0) {
+                // four scales per 8-byte load (a row's scales start 8-byte aligned)
+#pragma unroll
+                for (int b = 0; b < 12; b += 4) {
+                    if (b < nb) {
+                        const uint2 u = *(const uint2*)(srow + b);
+                        sb[b] = (uint16_t)u.x, sb[b + 1] = (uint16_t)(u.x >> 16);
+                        sb[b + 2] = (uint16_t)u.y, sb[b + 3] = (uint16_t)(u.y >> 16);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int b = 0; b < 12; b++)
+                    if (b < nb) sb[b] = srow[b];
+            }
+            const float dn = a.op == OP_COSINE ? a.dnorm[row] : 0.0f;
+            const float d2 = a.op == OP_L2 ? a.dd[row] : 0.0f;
+            float dotf = 0.0f;
+#pragma unroll
+            for (int b = 0; b < 12; b++)
+                if (b < nb) dotf = __fmaf_rn(h2f(sb[b]), (float)q4_block_acc(w[b], qh_s + 8 * b, ql_s + 8 * b), dotf);
+            e[i] = make_key(q4_finish_op(a.op, dotf, kq, dn, d2), row, a.smallest);
+        }
+    };
+    // all of a pass's shadow pairs fit: rank them by pre-score first
+    const bool prune = PM == 2 && M > k && M <= LCAP - fill;
+
     for (int base = 0; base < M;) {
         const int take = (M - base) < (LCAP - fill) ? (M - base) : (LCAP - fill);
+        int added = take;  // keys this batch leaves in buf (fewer after pruning)
         // batches of 8 independent loads per thread keep many in flight
         for (int j0 = 0; j0 < take; j0 += 8 * NT) {
             uint64_t v[8];
@@ -491,8 +553,13 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
                         else hi = mid;
                     }
                     v[t] = regq[(int64_t)lo * a.nq * a.rc + (g - pre[lo])];
-                    if (a.raw_dot) v[t] = dot_pair_key(v[t], qmax, a.smallest);
+                    if (PM == 1) v[t] = dot_pair_key(v[t], qmax, a.smallest);
                 }
+            }
+            if (PM == 2 && prune) {
+#pragma unroll
+                for (int t = 0; t < 8; t++)
+                    v[t] = make_key(__uint_as_float((uint32_t)(v[t] >> 32)), (uint32_t)v[t], a.smallest);
             }
 #pragma unroll
             for (int t = 0; t < 8; t++) {
@@ -501,7 +568,87 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
             }
         }
         __syncthreads();
-        fill += take;
+        if (PM == 2) {
+            if (prune) {
+                // Two stages.  The k pairs with the best pre-scores are
+                // rescored first; with the old best keys they give a k-th
+                // best exact key tk that the new k-th best can only exceed.
+                // A pair's exact score is within the margin of its pre-score,
+                // so of the other pairs only those passing shadow_bound(tk)
+                // (the scan's own threshold test) can still make the best k.
+                uint64_t prefix, pmask;
+                block_radix_prefix(buf + fill, take, k, rs, prefix, pmask);
+                // best-k pairs to the front, the rest after them
+                if (tid == 0) wpos = 0, wpos2 = 0;
+                uint64_t v[KPT];
+                uint32_t inT = 0, inR = 0;
+#pragma unroll
+                for (int j = 0; j < KPT; j++) {
+                    const int i = tid + NT * j;
+                    v[j] = i < take ? buf[fill + i] : 0ull;
+                    if (i < take) {
+                        if ((v[j] & pmask) >= prefix) inT |= 1u << j;
+                        else inR |= 1u << j;
+                    }
+                }
+                __syncthreads();  // counters set, every read of buf done
+                int pt = wave_append(__popc(inT), &wpos);
+                int pr = wave_append(__popc(inR), &wpos2);
+#pragma unroll
+                for (int j = 0; j < KPT; j++) {
+                    if (inT & (1u << j)) buf[fill + pt++] = v[j];
+                    if (inR & (1u << j)) buf[fill + k + pr++] = v[j];
+                }
+                __syncthreads();
+                const int nr = wpos2;
+                rescore(buf + fill, k, true);
+                __syncthreads();
+                // k-th best exact key of the old best and the rescored k
+                if (tid == 0) minkey = ~0ull;
+                uint64_t lo = ~0ull;
+                if (fill > 0) {
+                    block_radix_prefix(buf, fill + k, k, rs, prefix, pmask);
+                    for (int i = tid; i < fill + k; i += NT) {
+                        const uint64_t key = buf[i];
+                        if ((key & pmask) >= prefix) lo = key < lo ? key : lo;
+                    }
+                } else {
+                    __syncthreads();
+                    for (int i = tid; i < k; i += NT) lo = buf[fill + i] < lo ? buf[fill + i] : lo;
+                }
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) {
+                    const uint64_t t = __shfl_xor(lo, off);
+                    lo = t < lo ? t : lo;
+                }
+                if (lane == 0 && lo != ~0ull) atomicMin(&minkey, (unsigned long long)lo);
+                __syncthreads();
+                const float lbv = shadow_bound(minkey, a.qbound[2 * q], a.qbound[2 * q + 1], a.smallest);
+                // the other pairs within that bound, packed after the k
+                if (tid == 0) wpos = 0;
+                uint32_t keep = 0;
+#pragma unroll
+                for (int j = 0; j < KPT; j++) {
+                    const int i = tid + NT * j;
+                    v[j] = i < nr ? buf[fill + k + i] : 0ull;
+                    const float p = key_score(v[j], a.smallest);
+                    if (i < nr && (a.smallest ? p <= lbv : p >= lbv)) keep |= 1u << j;
+                }
+                __syncthreads();
+                int pos = wave_append(__popc(keep), &wpos);
+#pragma unroll
+                for (int j = 0; j < KPT; j++)
+                    if (keep & (1u << j)) buf[fill + k + pos++] = v[j];
+                __syncthreads();
+                added = k + wpos;
+                rescore(buf + fill + k, wpos, true);
+                __syncthreads();
+            } else {
+                rescore(buf + fill, added, false);
+                __syncthreads();
+            }
+        }
+        fill += added;
         base += take;
         if (fill > k && (fill == LCAP || base == M)) compact();
     }
@@ -637,12 +784,28 @@ int mq_select_threads(int64_t expect_keys) { return expect_keys > 4096 ? 1024 : 
 
 size_t mq_select_lds(int threads, int R) { return (size_t)threads * 16 * 8 + (size_t)(R + 1) * 4; }
 
+template <int PM>
+static void launch_mq_select_pm(const MqSelectArgs& a, int threads, size_t lds, hipStream_t s) {
+    if (threads == 1024)
+        hipLaunchKernelGGL((mq_select_kernel<1024, PM>), dim3((unsigned)a.nq), dim3(1024), lds, s, a);
+    else if (threads == 512)
+        hipLaunchKernelGGL((mq_select_kernel<512, PM>), dim3((unsigned)a.nq), dim3(512), lds, s, a);
+    else
+        hipLaunchKernelGGL((mq_select_kernel<256, PM>), dim3((unsigned)a.nq), dim3(256), lds, s, a);
+}
+
 hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s) {
     const size_t lds = mq_select_lds(threads, a.R);
-    if (threads == 1024)
-        hipLaunchKernelGGL(mq_select_kernel<1024>, dim3((unsigned)a.nq), dim3(1024), lds, s, a);
+    // shadow pairs: rows of at most 12 blocks (a row's blocks are in flight
+    // per thread)
+    if (a.pairs == 2 && (a.d % 32 != 0 || a.d > 384)) return hipErrorInvalidValue;
+    if (threads != 256 && threads != 512 && threads != 1024) return hipErrorInvalidValue;
+    if (a.pairs == 1)
+        launch_mq_select_pm<1>(a, threads, lds, s);
+    else if (a.pairs == 2)
+        launch_mq_select_pm<2>(a, threads, lds, s);
     else
-        hipLaunchKernelGGL(mq_select_kernel<256>, dim3((unsigned)a.nq), dim3(256), lds, s, a);
+        launch_mq_select_pm<0>(a, threads, lds, s);
     return hipGetLastError();
 }
 

@@ -25,7 +25,10 @@
 // 16 lanes reading one column of 16 consecutive rows hit distinct banks.
 // Top-k runs in the same threshold passes as kernels_mq.hip (regions per
 // (workgroup, query), compaction when a region might overflow).
+#include <algorithm>
+
 #include "mq_common.hpp"
+#include "q4_common.hpp"
 
 namespace manta {
 
@@ -36,24 +39,26 @@ constexpr int kMq8QG = kMq8Waves * 64;  // queries per workgroup
 constexpr int kMq8RB = 4;               // 16-row blocks per chunk
 constexpr int kMq8CH = kMq8RB * 16;     // rows per chunk
 
-// chunk tiles within 136 KB of dynamic LDS (the static arrays take ~15 KB of 160)
-constexpr int mq8_nbuf(int tile) {
-    int n = 136 * 1024 / tile;
+// chunk tiles (with their row scales) in the LDS the static arrays leave:
+// those take 24 bytes per query plus about 2 KB
+constexpr int mq8_nbuf(int tile, int qg) {
+    int n = (160 * 1024 - qg * 24 - 2560) / (tile + kMq8CH * 4);
     return n > 6 ? 6 : (n < 2 ? 2 : n);
 }
 }  // namespace
 
-template <int KS64, bool SMALL>
+template <int KS64, bool SMALL, int WS, bool SHADOW>
 __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))) void mq8_scan_kernel(MqArgs a) {
     constexpr int PITCH = KS64 * 64;
     constexpr int CH = kMq8CH;
     constexpr int TILE = CH * PITCH;                     // bytes per chunk tile
     constexpr int LPW = TILE / 1024 / kMq8Waves;         // 16-byte direct-to-LDS loads per wave per chunk
     static_assert(LPW * 1024 * kMq8Waves == TILE, "chunk tile must split evenly over the waves");
-    constexpr int NBUF = mq8_nbuf(TILE);
+    constexpr int QG = kMq8QG / WS;          // queries per workgroup
+    constexpr int NBUF = mq8_nbuf(TILE, QG);
     static_assert((NBUF - 2) * (LPW + 1) <= 63, "vmcnt range");
-    constexpr int QG = kMq8QG;
-    constexpr int NFW = QG / 64;
+    constexpr int NFW = QG / 64;             // waves per query group
+    static_assert(kMq8RB == 2 * 2 && (WS == 1 || WS == 2), "row pairs split over WS wave groups");
 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* tiles = smem;                               // [NBUF][TILE]
@@ -73,30 +78,8 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     const int wave = tid >> 6;
     const int g = lane >> 4, j = lane & 15;
     const int q0 = blockIdx.y * QG;
-    const int lw = wave * 64;  // this wave's first workgroup-local query
-
-    for (int i = tid; i < QG; i += kMq8Threads) {
-        const int q = q0 + i;
-        const bool ok = q < a.nq;
-        const QConst qc = ok ? a.qconst[q] : QConst{1.0f, 0.0f, 0.0f, 0.0f};
-        const uint64_t tk = ok ? a.tau[q] : 0ull;
-        qa_s[i] = qc.a;
-        tau_s[i] = ok ? tk : ~0ull;
-        bnd_s[i] = ok ? mq_bound<OP_DOT>(tk, qc, SMALL) : (SMALL ? -__builtin_inff() : __builtin_inff());
-        pre_s[i] = SMALL ? loosen_up(bnd_s[i]) : loosen_down(bnd_s[i]);
-        cnt_s[i] = 0;
-    }
-
-    // A operand: 4 blocks of 16 queries, K steps of 64 bytes
-    v4i av[4][KS64];
-#pragma unroll
-    for (int qb = 0; qb < 4; qb++) {
-        const int q = q0 + lw + qb * 16 + j;
-        const bool ok = q < a.nq;
-        const int8_t* src = a.qc8 + (int64_t)(ok ? q : 0) * PITCH + 16 * g;
-#pragma unroll
-        for (int ks = 0; ks < KS64; ks++) av[qb][ks] = ok ? *(const v4i*)(src + ks * 64) : v4i{0, 0, 0, 0};
-    }
+    const int lw = (wave % NFW) * 64;  // this wave's first workgroup-local query
+    const int rp0 = (wave / NFW) * 2;  // this wave's first row pair of a chunk
 
     uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.nq * a.rc;
     const int64_t r0 = a.row_begin + (int64_t)blockIdx.x * a.rows_per_wg;
@@ -132,12 +115,41 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
             lds_load4(a.scales + c0 + (lane < left ? lane : left - 1),
                       __builtin_amdgcn_readfirstlane(sbase + buf * CH * 4));
     };
-    __syncthreads();  // query state above is complete
-    // retire the A-fragment loads here, not at their first use in the loop
-    __builtin_amdgcn_s_waitcnt(0);
+    // the first chunks' loads go out first: the A fragments and the query
+    // state load under them
 #pragma unroll
     for (int b = 0; b < NBUF - 1; b++)
         if (r0 + b * CH < r1) issue_chunk(r0 + b * CH, b);
+
+    // A operand: 4 blocks of 16 queries, K steps of 64 bytes
+    v4i av[4][KS64];
+#pragma unroll
+    for (int qb = 0; qb < 4; qb++) {
+        const int q = q0 + lw + qb * 16 + j;
+        const bool ok = q < a.nq;
+        const int8_t* src = a.qc8 + (int64_t)(ok ? q : 0) * PITCH + 16 * g;
+#pragma unroll
+        for (int ks = 0; ks < KS64; ks++) av[qb][ks] = ok ? *(const v4i*)(src + ks * 64) : v4i{0, 0, 0, 0};
+    }
+
+    for (int i = tid; i < QG; i += kMq8Threads) {
+        const int q = q0 + i;
+        const bool ok = q < a.nq;
+        const QConst qc = ok ? a.qconst[q] : QConst{1.0f, 0.0f, 0.0f, 0.0f};
+        const uint64_t tk = ok ? a.tau[q] : 0ull;
+        qa_s[i] = qc.a;
+        tau_s[i] = ok ? tk : ~0ull;
+        float b = SMALL ? -__builtin_inff() : __builtin_inff();
+        if (ok) b = SHADOW ? shadow_bound(tk, a.qbound[2 * q], a.qbound[2 * q + 1], SMALL) : mq_bound<OP_DOT>(tk, qc, SMALL);
+        bnd_s[i] = b;
+        pre_s[i] = SMALL ? loosen_up(bnd_s[i]) : loosen_down(bnd_s[i]);
+        cnt_s[i] = 0;
+    }
+
+    __syncthreads();  // query state above is complete
+    // retire the A-fragment loads (and the first chunks) here, not at the
+    // fragments' first use in the loop
+    __builtin_amdgcn_s_waitcnt(0);
 
     // pre-filter bounds of a query block's 4 queries of this lane (one LDS read)
     auto load_bq = [&](int qb, float (&b)[4]) {
@@ -150,21 +162,33 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     };
 
     // The pairs of one query block of a row pair that pass the exact test,
-    // appended as (pre-score, row) pairs (a wave where one passed the filter).
-    auto survivors = [&](const v4i (&acc)[2][4], int qb, int64_t rb0, const float (&sc)[2], const float (&bq)[4]) {
+    // appended as (pre-score, row) pairs (a wave where one passed the filter):
+    // the lane's 8 tests go to a bit mask first, and the appends loop over
+    // its set bits, so a lane pays one LDS atomic per pair it appends.
+    auto survivors = [&](const v4i (&acc)[2][4], int qb, int64_t rb0, const float (&sc)[2]) {
+        const float4 b4 = *(const float4*)&bnd_s[lw + qb * 16 + 4 * g];
+        const float bx[4] = {b4.x, b4.y, b4.z, b4.w};
+        float pv[8];
+        uint32_t mask = 0;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const int64_t row = rb0 + h * 16 + j;
-            const bool valid = row < r1;
+            const bool valid = rb0 + h * 16 + j < r1;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                if (!valid || !(pre(sc[h], acc[h][qb][r], bq[r]) >= 0.0f)) continue;
-                const int lq = lw + qb * 16 + 4 * g + r;
                 const float p = fmul_rn(sc[h], (float)acc[h][qb][r]);
-                if (SMALL ? (p > bnd_s[lq]) : (p < bnd_s[lq])) continue;
-                const int pos = atomicAdd(&cnt_s[lq], 1);
-                wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = dot_pair(p, (uint32_t)row);
+                pv[h * 4 + r] = p;
+                if (valid && (SMALL ? p <= bx[r] : p >= bx[r])) mask |= 1u << (h * 4 + r);
             }
+        }
+        while (mask) {
+            const int b = __builtin_ctz(mask);
+            mask &= mask - 1;
+            float p = pv[0];
+#pragma unroll
+            for (int i = 1; i < 8; i++) p = b == i ? pv[i] : p;
+            const int lq = lw + qb * 16 + 4 * g + (b & 3);
+            const int pos = atomicAdd(&cnt_s[lq], 1);
+            wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = dot_pair(p, (uint32_t)(rb0 + (b >> 2) * 16 + j));
         }
     };
 
@@ -173,7 +197,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         // Flag regions that might not take one more chunk of keys (a count
         // read before the barrier may miss up to CH keys of the chunk other
         // waves are filtering: margin of two chunks, rc >= k + 2*CH + 1).
-        {
+        if (wave < NFW) {
             const int i = wave * 64 + lane;
             const uint64_t m = __ballot(cnt_s[i] > a.rc - 2 * CH);
             if (lane == 0) flags[par][wave] = m;
@@ -204,7 +228,16 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                     for (int i = tid; i < c; i += kMq8Threads) {
                         const uint64_t e = reg[i];
                         spairs[i] = e;
-                        skeys[i] = dot_pair_key(e, qa_s[lq], SMALL);
+                        if (SHADOW) {
+                            // the exact q4 score of the pair's row
+                            const int64_t q = q0 + lq;
+                            const float sc = q4_exact_score(a.op, a.q4codes, a.q4scales, a.dnorm, a.dd, a.d,
+                                                            (int64_t)(uint32_t)e, (const int*)(a.qhi + q * a.d),
+                                                            (const int*)(a.qlo + q * a.d), a.qconst[q]);
+                            skeys[i] = make_key(sc, (uint32_t)e, SMALL);
+                        } else {
+                            skeys[i] = dot_pair_key(e, qa_s[lq], SMALL);
+                        }
                     }
                     if (tid == 0) {
                         wpos = 0;
@@ -227,7 +260,9 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                         cnt_s[lq] = a.k;
                         if (minkey > tau_s[lq]) {
                             tau_s[lq] = minkey;
-                            bnd_s[lq] = mq_bound<OP_DOT>(minkey, a.qconst[q0 + lq], SMALL);
+                            const int q = q0 + lq;
+                            bnd_s[lq] = SHADOW ? shadow_bound(minkey, a.qbound[2 * q], a.qbound[2 * q + 1], SMALL)
+                                               : mq_bound<OP_DOT>(minkey, a.qconst[q], SMALL);
                             pre_s[lq] = SMALL ? loosen_up(bnd_s[lq]) : loosen_down(bnd_s[lq]);
                         }
                     }
@@ -238,7 +273,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         if (c0 + (NBUF - 1) * CH < r1) issue_chunk(c0 + (NBUF - 1) * CH, nbuf);
         const uint8_t* tile = tiles + buf * TILE;
 #pragma unroll
-        for (int rp = 0; rp < kMq8RB; rp += 2) {
+        for (int rp = rp0; rp < kMq8RB; rp += 2 * WS) {
             // B fragments one K step ahead of their MFMAs (the scheduling
             // barrier keeps the compiler from hoisting every step's reads,
             // which would hold all 2*KS64 fragments in registers)
@@ -280,7 +315,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                 for (int h = 0; h < 2; h++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) m = fmaxf(m, pre(sc[h], acc[h][qb][r], bq[r]));
-                if (__ballot(m >= 0.0f)) survivors(acc, qb, rb0, sc, bq);
+                if (__ballot(m >= 0.0f)) survivors(acc, qb, rb0, sc);
             }
         }
     }
@@ -289,42 +324,185 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         if (q0 + i < a.nq) a.counts[(int64_t)blockIdx.x * a.nq + q0 + i] = cnt_s[i];
 }
 
+// ------------------------------------------------------ q4 int8 shadow
+//
+// A q4 row x (x_j = f16 scale of j's block times its nibble code) gets int8
+// codes e_j = round(x_j / t) with t = maxabs(x) / 127 and the per-row scales
+// t (dot) and t / dnorm (cosine).  The shadow scan ranks rows by
+// p = scale * (e . c) against full-range int8 query codes c and keeps every
+// row the exact q4 score could place in the top k: with E = |x - t e| and
+// F = t |e|, |x . q - t e . qa c| <= E |q| + F |q - qa c|, so per-row error
+// bounds need only E, F (and |x| for cosine) -- their maxima over the rows
+// go to ShadowInfo.
+
+// An f32 at least v >= 0 (the cast rounds to nearest; the factor covers it).
+__device__ __forceinline__ float f32_up(double v) { return (float)(v * (1.0 + 9.5367431640625e-7)); }
+
+__global__ void shadow_info_clear_kernel(ShadowInfo* info) {
+    if (threadIdx.x < 8) (&info->me_cos)[threadIdx.x] = 0u;
+}
+
+// One wave per row (grid-stride); lane i holds bytes i, i+64, i+128 of the
+// packed row, i.e. elements 2i and 2i+1 of each (d <= 384).
+__global__ __launch_bounds__(256) void q4_shadow_build_kernel(const uint8_t* __restrict__ packed,
+                                                              const uint16_t* __restrict__ scales,
+                                                              const float* __restrict__ dnorm, int64_t n, int d,
+                                                              int spitch, int8_t* __restrict__ codes,
+                                                              float* __restrict__ sc_dot, float* __restrict__ sc_cos,
+                                                              ShadowInfo* __restrict__ info) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * 4;
+    const int hb = d / 2;
+    const int nb = d / 32;
+    float me_c = 0.0f, mf_c = 0.0f, me_d = 0.0f, mf_d = 0.0f, mn = 0.0f;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < n; row += nw) {
+        float x[3][2];
+        float m = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 3; u++) {
+            const int i = lane + 64 * u;
+            x[u][0] = x[u][1] = 0.0f;
+            if (i < hb) {
+                const int byte = packed[row * hb + i];
+                const float sc = h2f(scales[row * nb + (2 * i) / 32]);
+                // f16 significand (11 bits) times a 4-bit code: exact in f32
+                x[u][0] = fmul_rn(sc, (float)((int)(int8_t)(byte << 4) >> 4));
+                x[u][1] = fmul_rn(sc, (float)((int)(int8_t)byte >> 4));
+                m = fmaxf(m, fmaxf(__builtin_fabsf(x[u][0]), __builtin_fabsf(x[u][1])));
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float t = fdiv_rn(m, 127.0f);
+        double e2 = 0.0, f2 = 0.0, n2 = 0.0;
+        int8_t* crow = codes + row * spitch;
+#pragma unroll
+        for (int u = 0; u < 3; u++) {
+            const int i = lane + 64 * u;
+            if (i >= hb) continue;
+            int e[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const double xv = (double)x[u][h];
+                int c = 0;
+                if (t > 0.0f) {
+                    const double r = __builtin_rint(xv / (double)t);
+                    c = (int)(r > 127.0 ? 127.0 : (r < -127.0 ? -127.0 : r));
+                }
+                e[h] = c;
+                const double ex = xv - (double)t * (double)c;
+                e2 += ex * ex;
+                f2 += (double)(c * c);
+                n2 += xv * xv;
+            }
+            *(uint16_t*)(crow + 2 * i) = (uint16_t)((uint8_t)e[0] | ((uint16_t)(uint8_t)e[1] << 8));
+        }
+        for (int c = d + 2 * lane; c < spitch; c += 128) *(uint16_t*)(crow + c) = 0;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            e2 += __shfl_xor(e2, off);
+            f2 += __shfl_xor(f2, off);
+            n2 += __shfl_xor(n2, off);
+        }
+        if (lane == 0) {
+            const float dn = dnorm[row];
+            sc_dot[row] = t;
+            sc_cos[row] = dn > 0.0f ? fdiv_rn(t, dn) : 0.0f;
+        }
+        const double E = __builtin_sqrt(e2), F = (double)t * __builtin_sqrt(f2), N = __builtin_sqrt(n2);
+        me_d = fmaxf(me_d, f32_up(E));
+        mf_d = fmaxf(mf_d, f32_up(F));
+        mn = fmaxf(mn, f32_up(N));
+        if (N > 0.0) {
+            me_c = fmaxf(me_c, f32_up(E / N));
+            mf_c = fmaxf(mf_c, f32_up(F / N));
+        }
+    }
+    // workgroup maxima, then one atomic per value that raises the global one
+    __shared__ float red[4][5];
+    if (lane == 0) {
+        const int w = threadIdx.x >> 6;
+        red[w][0] = me_c, red[w][1] = mf_c, red[w][2] = me_d, red[w][3] = mf_d, red[w][4] = mn;
+    }
+    __syncthreads();
+    if (threadIdx.x < 5) {
+        const int i = threadIdx.x;
+        const float v = fmaxf(fmaxf(red[0][i], red[1][i]), fmaxf(red[2][i], red[3][i]));
+        unsigned int* dst = &info->me_cos + i;
+        if (__float_as_uint(v) > *(volatile unsigned int*)dst) atomicMax(dst, __float_as_uint(v));
+    }
+}
+
+hipError_t launch_shadow_info_clear(ShadowInfo* info, hipStream_t s) {
+    hipLaunchKernelGGL(shadow_info_clear_kernel, dim3(1), dim3(64), 0, s, info);
+    return hipGetLastError();
+}
+
+hipError_t launch_q4_shadow_build(const uint8_t* packed, const uint16_t* scales, const float* dnorm, int64_t n,
+                                  int d, int spitch, int8_t* codes, float* sc_dot, float* sc_cos,
+                                  ShadowInfo* info, hipStream_t s) {
+    if (d % 32 != 0 || d > 384 || spitch < d || spitch % 2 != 0) return hipErrorInvalidValue;
+    const int64_t wgs = std::min<int64_t>(8192, (n + 3) / 4);
+    hipLaunchKernelGGL(q4_shadow_build_kernel, dim3((unsigned)wgs), dim3(256), 0, s, packed, scales, dnorm, n, d,
+                       spitch, codes, sc_dot, sc_cos, info);
+    return hipGetLastError();
+}
+
 // pitch 512 would exceed the register budget (A fragments alone take 128)
 bool mq8_supported(int pitch) { return pitch == 128 || pitch == 256 || pitch == 384; }
 
-MqShape mq8_shape(int pitch) {
+MqShape mq8_shape(int pitch, int ws, bool shadow) {
     MqShape s;
     s.kind = 1;
     s.ks = pitch / 64;
     s.na = 4;
-    s.wq = kMq8Waves;
-    s.qg = kMq8QG;
+    s.wq = kMq8Waves / ws;
+    s.ws = ws;
+    s.shadow = shadow ? 1 : 0;
+    s.qg = kMq8QG / ws;
     s.chunk = kMq8CH;
     s.tile = kMq8CH * pitch;
-    s.tile_bytes = mq8_nbuf(s.tile) * (s.tile + kMq8CH * 4);  // chunk tiles + row scales
+    s.tile_bytes = mq8_nbuf(s.tile, s.qg) * (s.tile + kMq8CH * 4);  // chunk tiles + row scales
     s.threads = kMq8Threads;
     return s;
 }
 
-template <int KS64, bool SMALL>
+template <int KS64, bool SMALL, int WS, bool SHADOW>
 static hipError_t launch_mq8_one(const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)mq8_scan_kernel<KS64, SMALL>,
+        hipError_t e = hipFuncSetAttribute((const void*)mq8_scan_kernel<KS64, SMALL, WS, SHADOW>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((mq8_scan_kernel<KS64, SMALL>), grid, dim3(kMq8Threads), lds, s, a);
+    hipLaunchKernelGGL((mq8_scan_kernel<KS64, SMALL, WS, SHADOW>), grid, dim3(kMq8Threads), lds, s, a);
     return hipGetLastError();
 }
 
-hipError_t launch_mq8_scan(const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+template <int KS64>
+static hipError_t launch_mq8_ks(const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     const bool sm = a.smallest != 0;
+#define MANTA_MQ8(SM, W, SH)                                     \
+    if (sm == SM && sh.ws == W && (sh.shadow != 0) == SH)        \
+        return launch_mq8_one<KS64, SM, W, SH>(a, grid, lds, s);
+    MANTA_MQ8(false, 1, false)
+    MANTA_MQ8(true, 1, false)
+    MANTA_MQ8(false, 2, false)
+    MANTA_MQ8(true, 2, false)
+    MANTA_MQ8(false, 1, true)
+    MANTA_MQ8(true, 1, true)
+    MANTA_MQ8(false, 2, true)
+    MANTA_MQ8(true, 2, true)
+#undef MANTA_MQ8
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_mq8_scan(const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     switch (sh.ks) {
-        case 2: return sm ? launch_mq8_one<2, true>(a, grid, lds, s) : launch_mq8_one<2, false>(a, grid, lds, s);
-        case 4: return sm ? launch_mq8_one<4, true>(a, grid, lds, s) : launch_mq8_one<4, false>(a, grid, lds, s);
-        case 6: return sm ? launch_mq8_one<6, true>(a, grid, lds, s) : launch_mq8_one<6, false>(a, grid, lds, s);
+        case 2: return launch_mq8_ks<2>(sh, a, grid, lds, s);
+        case 4: return launch_mq8_ks<4>(sh, a, grid, lds, s);
+        case 6: return launch_mq8_ks<6>(sh, a, grid, lds, s);
         default: return hipErrorInvalidValue;
     }
 }

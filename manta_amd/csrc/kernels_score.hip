@@ -23,6 +23,7 @@
 //                                f16scale_b * f32(acc_b); then as above.
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "q4_common.hpp"
 
 namespace manta {
 
@@ -131,6 +132,84 @@ __global__ __launch_bounds__(256) void query_encode_kernel(const uint16_t* __res
     if (threadIdx.x == 0) qc[qi] = L.qc;
 }
 
+// Shadow-scan query encoding (one workgroup per query): the E16 planes in
+// the q4 order and constants as above, full-range int8 codes
+// c = round(q * 127/maxabs) with qa = maxabs/127 for the shadow's A operand,
+// and shadow_bound's margin m and factor f.  With q^ the E16-dequantized
+// query and G = |q^ - qa c|, a row's exact score and its shadow pre-score
+// p differ by at most E/|x| + (F/|x|) G/|q^| (cosine, in score units; p
+// scaled by f = |q^|/qa) or E|q^| + F G (dot, f = 1/qa), E and F the
+// shadow's row error terms (ShadowInfo maxima); m adds 2^-16 (times the
+// largest |x||q^| for dot), far above every f32 rounding on either side.
+__global__ __launch_bounds__(256) void query_encode_shadow_kernel(const uint16_t* __restrict__ q, int d, int spitch,
+                                                                  int op, const ShadowInfo* __restrict__ info,
+                                                                  int8_t* __restrict__ c8, int8_t* __restrict__ hi,
+                                                                  int8_t* __restrict__ lo, QConst* __restrict__ qc,
+                                                                  float* __restrict__ qb) {
+    __shared__ QueryLds L;
+    __shared__ double g2s[4];
+    __shared__ long long sss[4];
+    const int qi = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const uint16_t* qrow = q + (int64_t)qi * d;
+    encode_query_block(qrow, d, d, ENC_E16_Q4, L);
+    const float maxabs = fmaxf(fmaxf(L.redf[0], L.redf[1]), fmaxf(L.redf[2], L.redf[3]));
+    const float qs = L.qc.a;
+    const float inv16 = maxabs == 0.0f ? 0.0f : fdiv_rn(32639.0f, maxabs);
+    const float qa = fdiv_rn(maxabs, 127.0f);
+    const float inv8 = maxabs == 0.0f ? 0.0f : fdiv_rn(127.0f, maxabs);
+    double g2 = 0.0;
+    long long ss = 0;
+    for (int c = tid; c < spitch; c += 256) {
+        int k8 = 0;
+        if (c < d && maxabs != 0.0f) {
+            const float x = h2f(qrow[c]);
+            k8 = (int)fminf(127.0f, fmaxf(-127.0f, round_half_away(fmul_rn(x, inv8))));
+            const int k16 = code_e16(x, inv16);
+            const double diff = (double)k16 * (double)qs - (double)k8 * (double)qa;
+            g2 += diff * diff;
+            ss += (long long)k16 * k16;
+        }
+        c8[(int64_t)qi * spitch + c] = (int8_t)k8;
+    }
+    for (int c = tid; c < d; c += 256) {
+        hi[(int64_t)qi * d + c] = L.hi[c];
+        lo[(int64_t)qi * d + c] = L.lo[c];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        g2 += __shfl_xor(g2, off);
+        ss += __shfl_xor(ss, off);
+    }
+    if (lane == 0) {
+        g2s[wave] = g2;
+        sss[wave] = ss;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        qc[qi] = L.qc;
+        const double G = __builtin_sqrt(g2s[0] + g2s[1] + g2s[2] + g2s[3]);
+        const double qn = __builtin_sqrt((double)(sss[0] + sss[1] + sss[2] + sss[3])) * (double)qs;
+        const double up = 1.0 + 9.5367431640625e-7;
+        float m = 0.0f, f = 0.0f;
+        if (qn > 0.0) {
+            const double me_c = __uint_as_float(info->me_cos), mf_c = __uint_as_float(info->mf_cos);
+            const double me_d = __uint_as_float(info->me_dot), mf_d = __uint_as_float(info->mf_dot);
+            const double mn = __uint_as_float(info->maxn);
+            if (op == OP_COSINE) {
+                m = (float)((me_c + mf_c * G / qn + 1.52587890625e-05) * up);
+                f = (float)(qn / (double)qa);
+            } else {
+                m = (float)((me_d * qn + mf_d * G + 1.52587890625e-05 * mn * qn) * up);
+                f = (float)(1.0 / (double)qa);
+            }
+        }
+        qb[2 * qi] = m;
+        qb[2 * qi + 1] = f;
+    }
+}
+
 // ----------------------------------------------------------- epilogues
 
 template <int OP>
@@ -144,20 +223,6 @@ __device__ __forceinline__ float q8_epilogue(int acc_or_hi, int lo, float scale,
     // f32(256*hi + lo) with one rounding: both terms are exact in f32.
     float dotf = __fmaf_rn(256.0f, (float)acc_or_hi, (float)lo);
     float qd = fmul_rn(fmul_rn(scale, k.a), dotf);
-    if (OP == OP_COSINE) {
-        float den = fmul_rn(k.b, dnorm);
-        return den == 0.0f ? 0.0f : fdiv_rn(qd, den);
-    }
-    float t = fadd_rn(k.c, dd);
-    float dist2 = fsub_rn(t, fmul_rn(2.0f, qd));
-    dist2 = dist2 < 0.0f ? 0.0f : dist2;
-    return fsqrt_rn(dist2);
-}
-
-template <int OP>
-__device__ __forceinline__ float q4_finish(float dotf, const QConst& k, float dnorm, float dd) {
-    float qd = fmul_rn(dotf, k.a);
-    if (OP == OP_DOT) return qd;
     if (OP == OP_COSINE) {
         float den = fmul_rn(k.b, dnorm);
         return den == 0.0f ? 0.0f : fdiv_rn(qd, den);
@@ -572,10 +637,8 @@ __global__ __launch_bounds__(256) void q8_scan_generic_kernel(ScanArgs a) {
 
 // ------------------------------------------------------- q4 (lane = row)
 
-// Nibbles to 16x-scaled int8 lanes: (w << 4) & 0xF0F0F0F0 holds the even
-// nibbles of w as 16*code, w & 0xF0F0F0F0 the odd ones; the query digit
-// planes are permuted to match (q4_perm_pos).  Block sums are 16x the true
-// sums and are divided back exactly.
+// Each thread scores one row per round (q4_row_dotf); the query digit
+// planes are permuted to the nibble order (q4_perm_pos).
 template <int OP>
 __global__ __launch_bounds__(256) void q4_scan_kernel(ScanArgs a) {
     extern __shared__ uint64_t topk_keys[];
@@ -594,28 +657,7 @@ __global__ __launch_bounds__(256) void q4_scan_kernel(ScanArgs a) {
         const int64_t row = wg_row0 + (int64_t)r * 256 + threadIdx.x;
         const bool valid = row < a.n;
         float dotf = 0.0f;
-        if (valid) {
-            const v4i* rp = (const v4i*)(packed + row * a.pitch);
-            const uint16_t* sr = scales + row * a.nb;
-            for (int b = 0; b < a.nb; b++) {
-                v4i w = rp[b];
-                int sh = 0, sl = 0;
-                int ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    int even = (ws[j] << 4) & (int)0xF0F0F0F0;
-                    int odd = ws[j] & (int)0xF0F0F0F0;
-                    const int base = b * 8 + j * 2;
-                    sh = __builtin_amdgcn_sdot4(even, qh[base], sh, false);
-                    sh = __builtin_amdgcn_sdot4(odd, qh[base + 1], sh, false);
-                    sl = __builtin_amdgcn_sdot4(even, ql[base], sl, false);
-                    sl = __builtin_amdgcn_sdot4(odd, ql[base + 1], sl, false);
-                }
-                // block sum = (256*sh + sl) / 16, exact
-                int acc = (sh * 16) + (sl >> 4);
-                dotf = __fmaf_rn(h2f(sr[b]), (float)acc, dotf);
-            }
-        }
+        if (valid) dotf = q4_row_dotf(packed + row * a.pitch, scales + row * a.nb, a.nb, qh, ql);
         float score = 0.0f;
         if (valid) {
             float dn = 0.0f, d2 = 0.0f;
@@ -663,6 +705,14 @@ __global__ __launch_bounds__(256) void q8_rescore_acc_kernel(const int8_t* __res
 hipError_t launch_query_encode(const uint16_t* q, int nq, int d, int pitch, int e16, int8_t* c8,
                                int8_t* hi, int8_t* lo, QConst* qc, hipStream_t s) {
     hipLaunchKernelGGL(query_encode_kernel, dim3(nq), dim3(256), 0, s, q, d, pitch, e16, c8, hi, lo, qc);
+    return hipGetLastError();
+}
+
+hipError_t launch_query_encode_shadow(const uint16_t* q, int nq, int d, int spitch, int op, const ShadowInfo* info,
+                                      int8_t* c8, int8_t* hi, int8_t* lo, QConst* qc, float* qb, hipStream_t s) {
+    if (d % 32 != 0 || d > kMaxQueryDim || spitch < d) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(query_encode_shadow_kernel, dim3(nq), dim3(256), 0, s, q, d, spitch, op, info, c8, hi, lo, qc,
+                       qb);
     return hipGetLastError();
 }
 

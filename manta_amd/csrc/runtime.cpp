@@ -64,8 +64,15 @@ struct MantaRocmCandidates {
     void* scales = nullptr;
     float* dnorm = nullptr;
     float* dd = nullptr;
-    size_t bytes = 0;
-    bool scales_finite = false;  // q8: every row scale is finite (the 512-query dot kernel needs it)
+    mutable size_t bytes = 0;
+    bool scales_finite = false;  // every row / block scale is finite (the 512-query kernel needs it)
+    // q4: int8 shadow for many-query top-k (built on first use): codes
+    // [n][shadow_pitch], scales [2][n] (dot, cosine), error bounds
+    mutable int shadow_state = 0;  // 0 not built, 1 built, -1 unavailable
+    mutable int shadow_pitch = 0;
+    mutable int8_t* shadow_codes = nullptr;
+    mutable float* shadow_scales = nullptr;
+    mutable manta::ShadowInfo* shadow_info = nullptr;
 };
 
 namespace {
@@ -232,8 +239,14 @@ int free_candidates_memory(MantaRocmCandidates* c) {
     if (c->scales) (void)hipFree(c->scales);
     if (c->dnorm) (void)hipFree(c->dnorm);
     if (c->dd) (void)hipFree(c->dd);
+    if (c->shadow_codes) (void)hipFree(c->shadow_codes);
+    if (c->shadow_scales) (void)hipFree(c->shadow_scales);
+    if (c->shadow_info) (void)hipFree(c->shadow_info);
     c->codes = c->scales = nullptr;
     c->dnorm = c->dd = nullptr;
+    c->shadow_codes = nullptr;
+    c->shadow_scales = nullptr;
+    c->shadow_info = nullptr;
     return 0;
 }
 
@@ -519,6 +532,9 @@ int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16
     auto* c = new MantaRocmCandidates();
     c->rt = rt;
     c->format = MANTA_ROCM_Q4_BLOCKS;
+    bool finite = true;  // f16 exponent field below all-ones
+    for (int64_t i = 0; i < rows * nb && finite; i++) finite = (scales[i] & 0x7C00u) != 0x7C00u;
+    c->scales_finite = finite;
     c->sets = sets;
     c->n = n;
     c->d = d;
@@ -639,7 +655,8 @@ struct MqPass {
 
 struct MqPlan {
     bool use = false;
-    bool q4 = false;     // q4 blocks (kernels_mq4.hip), else q8 rows
+    bool q4 = false;     // q4 blocks (kernels_mq4.hip, or the shadow scan), else q8 rows
+    bool shadow = false; // q4 through its int8 shadow on the 512-query kernel
     manta::MqShape sh;
     int groups = 0;
     int rc = 0;          // region capacity (keys per query and workgroup)
@@ -665,26 +682,79 @@ MqPass mq_pass(int64_t begin, int64_t end, int chunk, int groups, int64_t max_ro
     return p;
 }
 
+// Region capacity of the 512-query kernel for k; its free chunk tile must
+// hold a region's pairs and keys when it compacts one.
+int mq8_rc(int64_t k) { return (int)(((2 * k + 2 * 64 + 64) + 63) / 64 * 64); }
+
+bool mq8_fits(int pitch, int64_t k) {
+    return manta::mq8_supported(pitch) && (size_t)mq8_rc(k) * 16 <= (size_t)manta::mq8_shape(pitch, 1, false).tile;
+}
+
+// q4 cosine / dot top-k with at least 256 queries goes through the int8
+// shadow (built on first use).
+bool q4_shadow_wanted(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k) {
+    return c->format == MANTA_ROCM_Q4_BLOCKS && c->sets == 1 && (op == MANTA_ROCM_COSINE || op == MANTA_ROCM_DOT) &&
+           nq >= 256 && c->d <= 384 && c->scales_finite && mq8_fits((int)align_up((size_t)c->d, 128), k);
+}
+
+// Build the int8 shadow of a q4 matrix on its first many-query top-k call
+// (stream-ordered kernels; the allocation is the only host-side work).  If
+// the memory is not there the q4 kernels keep serving such calls.
+void ensure_q4_shadow(MantaRocm* rt, const MantaRocmCandidates* c) {
+    if (c->shadow_state != 0) return;
+    const int sp = (int)align_up((size_t)c->d, 128);
+    const int64_t n = c->n;
+    int8_t* codes = nullptr;
+    float* sc = nullptr;
+    manta::ShadowInfo* info = nullptr;
+    hipError_t e = hipMalloc(&codes, (size_t)n * sp);
+    if (e == hipSuccess) e = hipMalloc(&sc, (size_t)n * 8);
+    if (e == hipSuccess) e = hipMalloc(&info, sizeof(manta::ShadowInfo));
+    if (e == hipSuccess) e = manta::launch_shadow_info_clear(info, rt->stream);
+    if (e == hipSuccess)
+        e = manta::launch_q4_shadow_build((const uint8_t*)c->codes, (const uint16_t*)c->scales, c->dnorm, n,
+                                          (int)c->d, sp, codes, sc, sc + n, info, rt->stream);
+    if (e != hipSuccess) {
+        if (codes) (void)hipFree(codes);
+        if (sc) (void)hipFree(sc);
+        if (info) (void)hipFree(info);
+        (void)hipGetLastError();
+        c->shadow_state = -1;
+        return;
+    }
+    c->shadow_codes = codes;
+    c->shadow_scales = sc;
+    c->shadow_info = info;
+    c->shadow_pitch = sp;
+    c->shadow_state = 1;
+    const size_t extra = (size_t)n * sp + (size_t)n * 8 + sizeof(manta::ShadowInfo);
+    c->bytes += extra;
+    rt->stats.candidate_bytes += extra;
+}
+
 MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool topk) {
     MqPlan p;
     if (c->sets != 1 || nq < 8) return p;
     const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
+    // the 16x16x64 kernel: 512-query groups, or 256 with the rows of a chunk
+    // split over two wave groups
+    const int ws8 = nq >= 512 ? 1 : 2;
     if (c->format == MANTA_ROCM_Q8_ROWS) {
-        // q8 dot with at least one full 512-query group: the 16x16x64 kernel
-        // (top-k only; its free chunk tile holds a region's pairs and keys
-        // when it compacts one)
-        const int rc8 = (int)(((2 * k + 2 * 64 + 64) + 63) / 64 * 64);
-        if (topk && dop == manta::OP_DOT && nq >= 512 && c->scales_finite && manta::mq8_supported(c->pitch) &&
-            (size_t)rc8 * 16 <= (size_t)manta::mq8_shape(c->pitch).tile) {
-            p.sh = manta::mq8_shape(c->pitch);
+        if (topk && dop == manta::OP_DOT && nq >= 256 && c->scales_finite && mq8_fits(c->pitch, k)) {
+            p.sh = manta::mq8_shape(c->pitch, ws8, false);
         } else {
             if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
             p.sh = manta::mq_shape(dop, c->pitch / 32, nq);
         }
     } else {
-        if (!manta::mq4_supported_nb(c->nb)) return p;
         p.q4 = true;
-        p.sh = manta::mq4_shape(dop, c->nb, nq);
+        if (topk && c->shadow_state == 1 && q4_shadow_wanted(c, op, nq, k)) {
+            p.shadow = true;
+            p.sh = manta::mq8_shape(c->shadow_pitch, ws8, true);
+        } else {
+            if (!manta::mq4_supported_nb(c->nb)) return p;
+            p.sh = manta::mq4_shape(dop, c->nb, nq);
+        }
     }
     p.groups = (int)((nq + p.sh.qg - 1) / p.sh.qg);
     if (p.groups > 65535) return p;
@@ -706,6 +776,9 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
     int64_t s = std::min<int64_t>(c->n, std::max<int64_t>(8 * k, 4096));
     p.passes.push_back(mq_pass(0, s, chunk, p.groups, p.rc - 2 * chunk, wgs));
     p.passes.back().select_threads = manta::mq_select_threads(s);
+    // shadow pairs are rescored by the select: 512 threads keep many row
+    // loads in flight within the register budget
+    if (p.shadow) p.passes.back().select_threads = 512;
     if (s < c->n) {
         // later passes grow the prefix by g: about k*g keys per query reach
         // the select.  Fewest passes the select's buffer allows, then the
@@ -722,7 +795,9 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
             const int64_t e = i + 1 == npass ? c->n : std::min<int64_t>(c->n, (int64_t)std::ceil(s * g));
             if (e <= s) continue;
             p.passes.push_back(mq_pass(s, e, chunk, p.groups, 0, wgs));
-            p.passes.back().select_threads = manta::mq_select_threads(k + (int64_t)(k * (g - 1.0) * 1.5));
+            // (shadow pairs: the margins let a few times more through)
+            p.passes.back().select_threads =
+                p.shadow ? 512 : manta::mq_select_threads(k + (int64_t)(k * (g - 1.0) * 1.5));
             s = e;
         }
     }
@@ -744,14 +819,15 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
            int64_t k, const MqPlan& p, float* out_scores, int32_t* out_ids, float* out_topk_scores,
            char** err) {
     // query planes: E8 codes or E16 digits, one row per query, as wide as a
-    // q8 row (pitch) or a q4 row in elements (d)
-    const int width = p.q4 ? (int)c->d : c->pitch;
+    // q8 row (pitch) or a q4 row in elements (d); the shadow scan's E8
+    // codes are as wide as a shadow row, its E16 planes [nq][d]
+    const int width = p.shadow ? c->shadow_pitch : (p.q4 ? (int)c->d : c->pitch);
     const size_t plane = (size_t)nq * width;
     const bool topk = out_scores == nullptr;
     const size_t regions = topk ? (size_t)nq * p.rmax * p.rc : 0;
     const size_t counts = topk ? (size_t)nq * p.rmax : 0;
     size_t need = 3 * (plane + 256) + (size_t)nq * sizeof(QConst) + 256 + (size_t)nq * 12 + 512 +
-                  (size_t)nq * (size_t)k * 8 + 256 + regions * 8 + 256 + counts * 4 + 256;
+                  (size_t)nq * (size_t)k * 8 + 256 + regions * 8 + 256 + counts * 4 + 256 + (size_t)nq * 8 + 256;
     int rc = ensure_workspace(rt, need, err);
     if (rc) return rc;
     Carver cv(rt->ws);
@@ -764,16 +840,29 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
     uint64_t* best = cv.take<uint64_t>(topk ? (size_t)nq * k : 1);
     uint64_t* reg = cv.take<uint64_t>(regions ? regions : 1);
     int* cnt = cv.take<int>(counts ? counts : 1);
-    const int e16 = p.q4 ? 2 : (op != MANTA_ROCM_DOT ? 1 : 0);
-    LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, width, e16, c8, hi, lo, qc, rt->stream),
-               "query_encode");
+    float* qb = cv.take<float>((size_t)nq * 2);
+    const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
+    if (p.shadow) {
+        LAUNCH_TRY(manta::launch_query_encode_shadow(q, (int)nq, (int)c->d, width, dop, c->shadow_info, c8, hi, lo,
+                                                     qc, qb, rt->stream),
+                   "query_encode");
+    } else {
+        const int e16 = p.q4 ? 2 : (op != MANTA_ROCM_DOT ? 1 : 0);
+        LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, width, e16, c8, hi, lo, qc, rt->stream),
+                   "query_encode");
+    }
     manta::MqArgs a{};
-    a.codes = (const int8_t*)c->codes;
-    a.scales = (const float*)c->scales;
+    a.codes = p.shadow ? c->shadow_codes : (const int8_t*)c->codes;
+    a.scales = p.shadow ? c->shadow_scales + (dop == manta::OP_COSINE ? c->n : 0) : (const float*)c->scales;
     a.dnorm = c->dnorm;
     a.dd = c->dd;
     a.n = c->n;
-    a.pitch = c->pitch;
+    a.pitch = p.shadow ? c->shadow_pitch : c->pitch;
+    a.qbound = qb;
+    a.q4codes = (const uint8_t*)c->codes;
+    a.q4scales = (const uint16_t*)c->scales;
+    a.d = (int)c->d;
+    a.op = dop;
     a.nq = (int)nq;
     a.qc8 = c8;
     a.qhi = hi;
@@ -786,7 +875,6 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
     a.k = (int)k;
     a.out_scores = out_scores;
     a.smallest = order == MANTA_ROCM_SMALLEST;
-    const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
     if (!topk) {
         const MqPass& ps = p.passes[0];
         a.row_begin = ps.begin;
@@ -807,9 +895,19 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
     sa.k = (int)k;
     sa.nq = (int)nq;
     sa.smallest = a.smallest;
-    // the 512-query kernel's regions hold (pre-score, row) pairs
-    sa.raw_dot = p.sh.kind == 1;
+    // the 512-query kernel's regions hold (pre-score, row) pairs: q8 dot
+    // keys follow from the pre-score, shadow pairs are rescored exactly
+    sa.pairs = p.sh.kind == 1 ? (p.shadow ? 2 : 1) : 0;
     sa.qconst = qc;
+    sa.q4codes = (const uint8_t*)c->codes;
+    sa.q4scales = (const uint16_t*)c->scales;
+    sa.dnorm = c->dnorm;
+    sa.dd = c->dd;
+    sa.qhi = hi;
+    sa.qlo = lo;
+    sa.qbound = qb;
+    sa.d = (int)c->d;
+    sa.op = dop;
     for (size_t i = 0; i < p.passes.size(); i++) {
         const MqPass& ps = p.passes[i];
         a.row_begin = ps.begin;
@@ -863,6 +961,7 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, i
     if (!out_ids) return fail(err, MANTA_ROCM_ERROR, "nil topk output");
     if (out_acc && c->format != MANTA_ROCM_Q8_ROWS)
         return fail(err, MANTA_ROCM_ERROR, "accumulator output needs q8 candidates");
+    if (q4_shadow_wanted(c, op, nq, k)) ensure_q4_shadow(rt, c);
     const MqPlan plan = mq_plan(c, op, nq, k, true);
     if (plan.use) {
         rc = run_mq(rt, c, op, order, q, nq, k, plan, nullptr, out_ids, out_scores, err);

@@ -309,10 +309,11 @@ def test_multi_query_all_ties(rt, op):
 
 @pytest.mark.parametrize("smallest", [False, True])
 @pytest.mark.parametrize("nq,n,d,k", [(512, 6000, 384, 50), (600, 5003, 128, 10), (1024, 4500, 256, 1),
-                                      (520, 3000, 384, 300)])
+                                      (520, 3000, 384, 300), (256, 6000, 384, 50), (300, 5003, 256, 10)])
 def test_q8_dot_512_queries_bit_exact(rt, smallest, nq, n, d, k):
-    """A full and a partial 512-query group, row counts that leave a
-    partial last chunk; ids, scores and accumulators bit-exact."""
+    """A full and a partial 512-query group (and 256-query groups for fewer
+    than 512 queries), row counts that leave a partial last chunk; ids,
+    scores and accumulators bit-exact."""
     q, codes, scales = _q8_case(nq + n + d + k, nq, n, d, sets=1)
     cands = rt.bind_q8(codes[0], scales[0])
     ids, sc, acc = rt.score_topk(cands, "dot", rt.to_device(q), k, smallest=smallest, with_acc=True)
@@ -424,4 +425,76 @@ def test_q4_multi_query_adversarial_row_order(rt, k):
     want_ids = orc.topk(want_s, k)
     np.testing.assert_array_equal(ids.download(), want_ids)
     np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    cands.close()
+
+
+# ---------------------------------------------------------------------------
+# q4 cosine / dot top-k with 256 or more queries: the int8 shadow of the q4
+# matrix on the 512-query kernel, every survivor rescored with the exact q4
+# score.  Results must equal the q4 contract's, bit for bit.
+
+def _check_q4_topk(rt, cands, op, q, packed, s4, d, k, smallest=False):
+    ids, sc, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    want_s = orc.score_q4(op, q, packed, s4, d)
+    want_ids = orc.topk(want_s, k, smallest=smallest)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    return want_ids
+
+
+@pytest.mark.parametrize("op,smallest", [("cosine", False), ("cosine", True), ("dot", False), ("dot", True)])
+@pytest.mark.parametrize("nq,n,d,k", [(256, 6000, 384, 100), (300, 5003, 128, 10), (512, 4500, 256, 1),
+                                      (520, 3000, 384, 300), (256, 20000, 96, 50)])
+def test_q4_shadow_topk_bit_exact(rt, op, smallest, nq, n, d, k):
+    """One and two wave groups per 256 queries, partial query groups and
+    chunks, shadow pitches 128/256/384 (d = 96 pads to 128)."""
+    q, packed, s4 = _q4_case(nq + n + d + k, nq, n, d)
+    cands = rt.bind_q4(packed, s4, d)
+    _check_q4_topk(rt, cands, op, q, packed, s4, d, k, smallest)
+    # a second call reuses the shadow built by the first
+    _check_q4_topk(rt, cands, op, q[: nq // 2 + 128], packed, s4, d, k, smallest)
+    cands.close()
+
+
+@pytest.mark.parametrize("op", ["cosine", "dot"])
+@pytest.mark.parametrize("k", [7, 100])
+def test_q4_shadow_adversarial_row_order(rt, op, k):
+    """Rows ranked worst first for every query (cosine: a row turns from a
+    random direction towards the queries' common direction with its index;
+    dot: block scales grow with it): every pass lets the later rows through,
+    so regions fill and are compacted on exact scores inside the scan."""
+    nq, n, d = 256, 60000, 128
+    rng = np.random.default_rng(k)
+    base = rng.standard_normal(d)
+    other = rng.standard_normal(d)
+    q = orc.f32_to_f16((base + 0.05 * rng.standard_normal((nq, d))).astype(np.float32))
+    if op == "cosine":
+        w = (np.arange(n, dtype=np.float64) / n)[:, None]
+        rows = (w * base[None, :] + (1.0 - w) * other[None, :]).astype(np.float32)
+        packed, s4 = orc.pack_q4_blocks(rows)
+    else:
+        packed1, s1 = orc.pack_q4_blocks(base.astype(np.float32).reshape(1, -1))
+        packed = np.repeat(packed1, n, axis=0)
+        grow = (1.0 + np.arange(n, dtype=np.float64) / n)[:, None]
+        s4 = orc.f32_to_f16((orc.f16_to_f32(s1) * grow).astype(np.float32))
+    cands = rt.bind_q4(packed, s4, d)
+    _check_q4_topk(rt, cands, op, q, packed, s4, d, k)
+    cands.close()
+
+
+@pytest.mark.parametrize("op,smallest", [("cosine", False), ("dot", True)])
+def test_q4_shadow_all_ties_zero_rows_and_zero_query(rt, op, smallest):
+    """Identical rows tie for every query (lowest indices win); all-zero
+    rows and an all-zero query score 0 under the contract."""
+    nq, n, d, k = 256, 20000, 384, 64
+    q, _, _ = _q4_case(9, nq, 1, d)
+    q = q.copy()
+    q[17] = 0
+    packed1, s1 = synth.q4_rows(209, 1, 1, d, normalize=True)
+    packed = np.repeat(packed1, n, axis=0)
+    s4 = np.repeat(s1, n, axis=0)
+    packed[5::11] = 0
+    s4[5::11] = 0
+    cands = rt.bind_q4(packed, s4, d)
+    _check_q4_topk(rt, cands, op, q, packed, s4, d, k, smallest)
     cands.close()
