@@ -192,6 +192,8 @@ struct EmbedArgs {
     float* Y;                   // f32 [M][N] (matmul)
     float* P;                   // f32 [batches][tiles_per_seq][N] (pooled partial sums)
     unsigned long long* err;    // first out-of-range gather index
+    unsigned int* tickets;      // [batches] zero between calls (single-pass pooled kernel)
+    uint16_t* out;              // f16 [batches][N] embeddings (single-pass pooled kernel)
 };
 
 hipError_t launch_embed_gemm(const EmbedArgs& a, bool gather, bool q8b, bool pool, hipStream_t s);
@@ -203,6 +205,13 @@ bool embed_gemm2_supported(const EmbedArgs& a);
 hipError_t launch_embed_transpose_b(const EmbedArgs& a, bool q8b, uint16_t* Bt, hipStream_t s);
 hipError_t launch_embed_gemm2(const EmbedArgs& a, bool gather, bool q8b, bool pool, const uint16_t* Bt,
                               hipStream_t s);
+// Single-pass GEMM for an f16 projection with N == 384 and K % 32 == 0: the
+// projection is read as stored ([K][N]) through LDS transpose reads, one
+// workgroup per 32-row tile.  Pooled mode (tiles_per_seq = ceil(T / 32))
+// also finishes the embeddings: partial sums go to P, and the last tile of
+// each sequence writes out[seq] (tickets must hold zeros; they are reset).
+bool embed_gemm3_supported(const EmbedArgs& a, bool q8b);
+hipError_t launch_embed_gemm3(const EmbedArgs& a, bool gather, bool pool, hipStream_t s);
 hipError_t launch_embed_finalize(const float* P, int tiles, const int32_t* mask, int64_t B, int64_t T,
                                  int N, uint16_t* out, hipStream_t s);
 hipError_t launch_gather_rows_f16(const uint16_t* table, int64_t vocab, int64_t d, const int32_t* idx,

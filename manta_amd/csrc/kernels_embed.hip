@@ -497,6 +497,265 @@ __global__ void normalize_rows_kernel(float* __restrict__ x, int64_t rows, int64
 
 // ----------------------------------------------------------------- hosts
 
+// ------------------------------------- single-pass GEMM (f16 B, N = 384)
+//
+// Workgroup = one 32-row tile x all 384 columns: 4 waves of 96 columns,
+// each three 32x32 tiles of v_mfma_f32_32x32x16_f16.  K moves in chunks of
+// 32 through a 5-stage ring of LDS buffers filled by direct-to-LDS loads:
+// the A chunk (32 rows x 64 bytes, rows gathered by token id) by 4-byte
+// loads, the projection chunk (32 k-rows x 768 bytes, row-major as stored)
+// by 16-byte loads.  The projection's MFMA operand (8 consecutive k of one
+// column per lane) comes from two ds_read_tr16_b64: lane i of a 16-lane
+// group receives element i%4 of the 8 bytes that lane 4j + i/4 of the group
+// addresses, j = 0..3, so a group addresses 4 k-rows x 16 columns and lane
+// i gets column i at those 4 k.  A projection row stores its 16-byte chunk
+// c at c ^ 2*(k%4), so the 4 rows a group reads hit distinct banks; an A row
+// stores its 16-byte column c at c ^ ((row >> 2) & 3) as in the pipelined
+// kernel.
+constexpr int E3_WM = 32, E3_N = 384, E3_KC = 32, E3_NST = 5;
+constexpr int E3_AST = E3_WM * E3_KC * 2;  // A bytes per stage (2 KB)
+constexpr int E3_BST = E3_KC * E3_N * 2;   // projection bytes per stage (24 KB)
+constexpr int E3_STAGE = E3_AST + E3_BST;
+
+__device__ __forceinline__ void eg_lds_load4(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// ds_read_tr16_b64 at an LDS byte address given as a generic pointer
+__device__ __forceinline__ v4s lds_read_tr16(const uint8_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+}
+
+template <bool GATHER, bool POOL>
+__global__ __launch_bounds__(256) void embed_gemm3_kernel(EmbedArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float rowv[E3_N];
+    __shared__ double dred[4];
+    __shared__ int ired[4];
+    __shared__ int last;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t tile = blockIdx.x;
+    int64_t seq = 0, t0 = 0, m0 = 0;
+    if (POOL) {
+        seq = tile / a.tiles_per_seq;
+        t0 = (tile % a.tiles_per_seq) * E3_WM;
+    } else {
+        m0 = tile * E3_WM;
+    }
+    const int K = a.K;
+
+    // A loads: this wave's two 256-byte pieces of a stage (rows 4L .. 4L+3,
+    // L = 2*wave + u); lane i fills stored dword i%16 of row 4L + i/16.
+    const uint8_t* asrc[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int r = 4 * (2 * wave + u) + (lane >> 4);
+        int64_t src = 0;
+        if (POOL) {
+            const int64_t t = t0 + r;
+            if (t < a.T) {
+                const int idx = a.tokens[seq * a.T + t];
+                if (idx >= 0 && idx < a.vocab) src = idx;
+                else report_bad_index(a.err, idx);
+            }
+        } else {
+            const int64_t m = m0 + r;
+            if (m < a.M) {
+                if (GATHER) {
+                    const int idx = a.tokens[m];
+                    if (idx >= 0 && idx < a.vocab) src = idx;
+                    else report_bad_index(a.err, idx);
+                } else {
+                    src = m;
+                }
+            }
+        }
+        const int c = ((lane & 15) >> 2) ^ ((r >> 2) & 3);
+        asrc[u] = (const uint8_t*)(GATHER ? a.table : a.A) + src * K * 2 + c * 16 + (lane & 3) * 4;
+    }
+    // projection loads: this wave's six 1 KB pieces of a stage
+    int boff[6];
+#pragma unroll
+    for (int u = 0; u < 6; u++) {
+        const int x = (6 * wave + u) * 1024 + lane * 16;
+        const int kr = x / (E3_N * 2);
+        const int c = ((x % (E3_N * 2)) / 16) ^ (2 * (kr & 3));
+        boff[u] = kr * E3_N * 2 + c * 16;
+    }
+    const uint8_t* bsrc = (const uint8_t*)a.B;
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
+    // Workgroups walk the K chunks from different starting points, so the
+    // CUs do not all ask L2 for the same projection lines at once.
+    const int nk = K / E3_KC;
+    const int rot = (int)(tile % nk);
+    auto issue = [&](int kci, int st) {
+        const int kc = kci + rot < nk ? kci + rot : kci + rot - nk;
+        const uint32_t sa = __builtin_amdgcn_readfirstlane(base + st * E3_STAGE + wave * 2 * 256);
+#pragma unroll
+        for (int u = 0; u < 2; u++) eg_lds_load4(asrc[u] + kc * E3_KC * 2, sa + u * 256);
+        const uint32_t sb = __builtin_amdgcn_readfirstlane(base + st * E3_STAGE + E3_AST + wave * 6 * 1024);
+        const uint8_t* bk = bsrc + (int64_t)kc * E3_KC * E3_N * 2;
+#pragma unroll
+        for (int u = 0; u < 6; u++) eg_lds_load16(bk + boff[u], sb + u * 1024);
+    };
+#pragma unroll
+    for (int st = 0; st < E3_NST - 1; st++)
+        if (st < nk) issue(st, st);
+
+    // transpose-read offsets of this lane's projection operands: group G =
+    // lane/16 takes k-half G>>1 and 16-column half G&1 of a 32-column tile;
+    // lane s of the group addresses k-row s/4, columns 4*(s%4) .. +3
+    const int G = lane >> 4, s16 = lane & 15;
+    const int trow = (8 * (G >> 1) + (s16 >> 2)) * E3_N * 2 + 8 * (s16 & 1);
+    int tcol[3];
+#pragma unroll
+    for (int cb = 0; cb < 3; cb++) {
+        const int c = (wave * 96 + cb * 32 + 16 * (G & 1)) / 8 + ((s16 & 3) >> 1);
+        tcol[cb] = (c ^ (2 * (s16 >> 2))) * 16;
+    }
+
+    f16v acc[3];
+#pragma unroll
+    for (int cb = 0; cb < 3; cb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[cb][r] = 0.0f;
+
+    const int l32 = lane & 31, hf = lane >> 5;
+    int st = 0;
+    for (int kc = 0; kc < nk; kc++, st = st == E3_NST - 1 ? 0 : st + 1) {
+        eg_wait_barrier<8, E3_NST - 2>(nk - 1 - kc);
+        if (kc + E3_NST - 1 < nk) issue(kc + E3_NST - 1, st == 0 ? E3_NST - 1 : st - 1);
+        const uint8_t* As = smem + st * E3_STAGE;
+        const uint8_t* Bs = As + E3_AST;
+#pragma unroll
+        for (int ks = 0; ks < E3_KC / 16; ks++) {
+            const int c = ks * 2 + hf;
+            const h8 av = *(const h8*)(As + l32 * 64 + ((c ^ ((l32 >> 2) & 3)) * 16));
+#pragma unroll
+            for (int cb = 0; cb < 3; cb++) {
+                const uint8_t* p = Bs + trow + tcol[cb] + ks * 16 * E3_N * 2;
+                // k 0..3 of the lane's 8, then k 4..7 (four k-rows further)
+                const v4s lo = lds_read_tr16(p);
+                const v4s hi = lds_read_tr16(p + 4 * E3_N * 2);
+                const h8 bv = __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[cb], 0, 0, 0);
+            }
+        }
+    }
+
+    // Output element (cb, r): row 8*(r/4) + 4*(lane/32) + r%4 of the tile,
+    // column wave*96 + cb*32 + lane%32.
+    if (!POOL) {
+#pragma unroll
+        for (int cb = 0; cb < 3; cb++) {
+            const int n = wave * 96 + cb * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = m0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+                if (m < a.M) a.Y[m * E3_N + n] = acc[cb][r];
+            }
+        }
+        return;
+    }
+    bool live[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int64_t t = t0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+        live[r] = t < a.T && (!a.mask || a.mask[seq * a.T + t] != 0);
+    }
+    // publish the tile's column sums (agent-scope stores, then the ticket)
+    unsigned int* pdst = (unsigned int*)(a.P + (seq * a.tiles_per_seq + t0 / E3_WM) * E3_N);
+#pragma unroll
+    for (int cb = 0; cb < 3; cb++) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if (live[r]) sum += acc[cb][r];
+        sum += __shfl_xor(sum, 32);
+        if (hf == 0)
+            __hip_atomic_store(pdst + wave * 96 + cb * 32 + l32, __float_as_uint(sum), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(&a.tickets[seq], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(a.tiles_per_seq - 1);
+    __syncthreads();
+    if (!last) return;
+    // the sequence's embedding: partials added in tile order, divided by the
+    // count of unmasked positions, L2-normalized (as embed_finalize_kernel)
+    int cnt = 0;
+    for (int64_t t = tid; t < a.T; t += 256) cnt += (!a.mask || a.mask[seq * a.T + t] != 0) ? 1 : 0;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off);
+    if (lane == 0) ired[wave] = cnt;
+    __syncthreads();
+    const int count = ired[0] + ired[1] + ired[2] + ired[3];
+    const float inv = count ? 1.0f / (float)count : 0.0f;
+    const unsigned int* psrc = (const unsigned int*)(a.P + seq * a.tiles_per_seq * E3_N);
+    double ss = 0.0;
+    for (int c = tid; c < E3_N; c += 256) {
+        // 8 tiles' partials in flight at a time, added in tile order
+        float v = 0.0f;
+        for (int s0 = 0; s0 < a.tiles_per_seq; s0 += 8) {
+            unsigned int pv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                pv[u] = s0 + u < a.tiles_per_seq
+                            ? __hip_atomic_load(psrc + (s0 + u) * E3_N + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : 0u;
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (s0 + u < a.tiles_per_seq) v += __uint_as_float(pv[u]);
+        }
+        v = count ? v * inv : 0.0f;
+        rowv[c] = v;
+        ss += (double)v * (double)v;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) dred[wave] = ss;
+    __syncthreads();
+    const float norm = (float)__builtin_sqrt(dred[0] + dred[1] + dred[2] + dred[3]);
+    for (int c = tid; c < E3_N; c += 256) {
+        float v = rowv[c];
+        if (norm != 0.0f) v = v / norm;
+        a.out[seq * E3_N + c] = f2h(v);
+    }
+    if (tid == 0) __hip_atomic_store(&a.tickets[seq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+bool embed_gemm3_supported(const EmbedArgs& a, bool q8b) {
+    return !q8b && a.N == E3_N && a.K % E3_KC == 0 && a.K > 0;
+}
+
+hipError_t launch_embed_gemm3(const EmbedArgs& a, bool gather, bool pool, hipStream_t s) {
+    const int64_t tiles = pool ? a.batches * a.tiles_per_seq : (a.M + E3_WM - 1) / E3_WM;
+    const size_t lds = (size_t)E3_NST * E3_STAGE;
+#define MANTA_EG3(G, P)                                                                                \
+    if (gather == G && pool == P) {                                                                    \
+        static bool attr = false;                                                                      \
+        if (!attr) {                                                                                   \
+            hipError_t e = hipFuncSetAttribute((const void*)embed_gemm3_kernel<G, P>,                  \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            if (e != hipSuccess) return e;                                                             \
+            attr = true;                                                                               \
+        }                                                                                              \
+        hipLaunchKernelGGL((embed_gemm3_kernel<G, P>), dim3((unsigned)tiles), dim3(256), lds, s, a);   \
+        return hipGetLastError();                                                                      \
+    }
+    MANTA_EG3(true, true)
+    MANTA_EG3(false, false)
+    MANTA_EG3(true, false)
+#undef MANTA_EG3
+    return hipErrorInvalidValue;
+}
+
 bool embed_gemm2_supported(const EmbedArgs& a) { return a.K % EG_KC == 0 && a.K > 0 && a.N % EG_WN == 0 && a.N > 0; }
 
 size_t embed_gemm2_lds() { return (size_t)EG_NST * EG_STAGE; }

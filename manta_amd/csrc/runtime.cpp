@@ -79,6 +79,7 @@ namespace {
 
 constexpr int64_t kMaxDim = 1024;     // exactness bound of the int32 / f32 accumulators
 constexpr int64_t kMaxDeviceK = 2048;  // reservoir capacity bound (LDS, cap <= 4096)
+constexpr int64_t kTickets = 65536;    // last-workgroup tickets (queries / sequences per call)
 
 char* dup_printf(const char* fmt, va_list ap) {
     va_list ap2;
@@ -299,8 +300,8 @@ int manta_rocm_create(int device, MantaRocm** out, char** err) {
     rt->stream = rt->own_stream;
     e = hipMalloc((void**)&rt->err_word, sizeof(unsigned long long));
     if (e == hipSuccess) e = hipMemset(rt->err_word, 0, sizeof(unsigned long long));
-    if (e == hipSuccess) e = hipMalloc((void**)&rt->tickets, 65536 * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(rt->tickets, 0, 65536 * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void**)&rt->tickets, kTickets * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(rt->tickets, 0, kTickets * sizeof(uint32_t));
     if (e != hipSuccess) {
         (void)hipStreamDestroy(rt->own_stream);
         delete rt;
@@ -1107,6 +1108,10 @@ int manta_rocm_matmul_f16(MantaRocm* rt, const uint16_t* lhs, int64_t m, int64_t
     a.colscale = col_scale;
     a.Y = out;
     const bool q8b = proj_kind == MANTA_ROCM_PROJ_Q8_COL;
+    if (manta::embed_gemm3_supported(a, q8b)) {
+        LAUNCH_TRY(manta::launch_embed_gemm3(a, false, false, rt->stream), "matmul");
+        return MANTA_ROCM_OK;
+    }
     if (manta::embed_gemm2_supported(a)) {
         rc = ensure_workspace(rt, (size_t)n * k * 2 + 256, err);
         if (rc) return rc;
@@ -1147,11 +1152,7 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
                     (long long)t, (long long)vocab, (long long)d);
     int rc = check_proj(proj_kind, proj, col_scale, d, e, err);
     if (rc) return rc;
-    const int64_t tiles = (t + 63) / 64;
-    if (b * tiles > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: batch too large");
-    const size_t pbytes = align_up((size_t)(b * tiles * e) * sizeof(float), 256);
-    rc = ensure_workspace(rt, pbytes + (size_t)d * e * 2 + 256, err);
-    if (rc) return rc;
+    const bool q8b = proj_kind == MANTA_ROCM_PROJ_Q8_COL;
     manta::EmbedArgs a{};
     a.tokens = tokens;
     a.mask = mask;
@@ -1159,14 +1160,31 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
     a.vocab = vocab;
     a.T = t;
     a.batches = b;
-    a.tiles_per_seq = (int)tiles;
     a.K = (int)d;
     a.N = (int)e;
     a.B = proj;
     a.colscale = col_scale;
-    a.P = (float*)rt->ws;
     a.err = rt->err_word;
-    const bool q8b = proj_kind == MANTA_ROCM_PROJ_Q8_COL;
+    if (manta::embed_gemm3_supported(a, q8b) && b <= kTickets) {
+        // one launch: 32-row tiles, the last tile of each sequence finishes it
+        a.tiles_per_seq = (int)((t + 31) / 32);
+        if (b * a.tiles_per_seq > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: batch too large");
+        rc = ensure_workspace(rt, align_up((size_t)(b * a.tiles_per_seq * e) * sizeof(float), 256), err);
+        if (rc) return rc;
+        a.P = (float*)rt->ws;
+        a.tickets = rt->tickets;
+        a.out = out;
+        LAUNCH_TRY(manta::launch_embed_gemm3(a, true, true, rt->stream), "embed");
+        rt->gather_pending = true;
+        return MANTA_ROCM_OK;
+    }
+    const int64_t tiles = (t + 63) / 64;
+    if (b * tiles > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: batch too large");
+    const size_t pbytes = align_up((size_t)(b * tiles * e) * sizeof(float), 256);
+    rc = ensure_workspace(rt, pbytes + (size_t)d * e * 2 + 256, err);
+    if (rc) return rc;
+    a.tiles_per_seq = (int)tiles;
+    a.P = (float*)rt->ws;
     if (manta::embed_gemm2_supported(a)) {
         // the projection transposed to f16 [e][d] after the partials
         uint16_t* bt = (uint16_t*)((char*)rt->ws + pbytes);

@@ -42,7 +42,8 @@ def test_gather_rows_bit_exact_and_errors(rt):
     res.free()
 
 
-@pytest.mark.parametrize("m,k,n", [(64, 384, 384), (100, 384, 200), (8192, 384, 384), (3, 64, 130)])
+@pytest.mark.parametrize("m,k,n", [(64, 384, 384), (100, 384, 200), (8192, 384, 384), (3, 64, 130),
+                                   (100, 64, 384), (33, 768, 384)])
 def test_matmul_f16(rt, m, k, n):
     a = synth.normal_f16(12, 0, m, k, 0.02)
     b = synth.normal_f16(12, 1, k, n, 1.0 / np.sqrt(k))
@@ -105,8 +106,11 @@ def test_embed_config4_q8_projection_slice(rt):
     assert _cos_rows(orc.f16_to_f32(got), want32).min() >= 0.9999
 
 
-def test_embed_ragged_and_empty_sequences(rt):
-    b, t, v, d, e = 7, 100, 500, 64, 96
+@pytest.mark.parametrize("d,e", [(64, 96), (384, 384), (128, 384)])
+def test_embed_ragged_and_empty_sequences(rt, d, e):
+    """Lengths 0 .. T with T = 100 (not a multiple of the 32- and 64-row
+    tiles); e = 384 with an f16 projection takes the single-pass kernel."""
+    b, t, v = 7, 100, 500
     tokens = synth.uniform_i32(16, 0, b * t, 0, v).reshape(b, t)
     lengths = np.array([0, 1, 63, 64, 65, 99, 100], np.int32)
     mask = (np.arange(t)[None, :] < lengths[:, None]).astype(np.int32)
@@ -119,8 +123,9 @@ def test_embed_ragged_and_empty_sequences(rt):
     assert _cos_rows(got[1:], want32[1:]).min() >= 0.9999
 
 
-def test_embed_out_of_range_token(rt):
-    tokens, mask, table, proj = synth.config1(b=4, t=32, vocab=100, d=64, e=64)
+@pytest.mark.parametrize("d,e", [(64, 64), (384, 384)])
+def test_embed_out_of_range_token(rt, d, e):
+    tokens, mask, table, proj = synth.config1(b=4, t=32, vocab=100, d=d, e=e)
     tokens[2, 31] = 100
     mask[2, 31] = 0  # the reference gathers every position, masked or not
     rt.embed_pooled(rt.to_device(tokens), rt.to_device(mask), rt.to_device(table), rt.to_device(proj))
