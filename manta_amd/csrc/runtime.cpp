@@ -790,7 +790,16 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
         // the 512-query kernel appends about k*g pairs per query and pass:
         // keep g near 10 (k*g*npass is smallest there for the spans that
         // occur) at one select per pass
-        if (p.sh.kind == 1) npass = std::max(npass, (int)std::ceil(std::log(span) / std::log(12.0) - 1e-9));
+        if (p.sh.kind == 1 && !p.shadow)
+            npass = std::max(npass, (int)std::ceil(std::log(span) / std::log(12.0) - 1e-9));
+        // shadow pairs: every pair the select keeps is rescored from a random
+        // row, so fewer, larger passes win as long as a pass's pairs (about
+        // 4*k*g with the margins) fit the 512-thread select's 8K-key buffer,
+        // which is what lets it prune before rescoring
+        if (p.shadow) {
+            const double gs = std::max(4.0, (8192.0 - (double)k) / (4.0 * (double)k));
+            npass = std::max(1, (int)std::ceil(std::log(span) / std::log(gs) - 1e-9));
+        }
         const double g = std::pow(span, 1.0 / npass);
         for (int i = 0; i < npass; i++) {
             const int64_t e = i + 1 == npass ? c->n : std::min<int64_t>(c->n, (int64_t)std::ceil(s * g));
