@@ -153,7 +153,7 @@ def run_c1(rt, steps, warmup) -> dict:
         "workload": "c1_embed_f16", "shape": {"b": b, "t": t, "vocab": table.shape[0], "d": d, "e": e},
         "value": b * t / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0,
         "device_ms_per_step": dev_ms,
-        "roofline": {"bound": "mfma", "kernel": "embed_gemm3_kernel<gather,pool> (f16 MFMA 32x32x16, LDS transpose "
+        "roofline": {"bound": "mfma", "kernel": "embed_gemm4_kernel (f16 MFMA 32x32x16, 128x96 tiles, LDS transpose "
                                                 "reads of the projection, finalize fused)",
                      "achieved": achieved, "peak": F16_PEAK, "unit": "TFLOP/s", "frac": achieved / F16_PEAK,
                      "avg_launch_us": k_ms * 1000.0, "flops_per_launch": flops,

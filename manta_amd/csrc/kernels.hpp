@@ -212,6 +212,9 @@ hipError_t launch_embed_gemm2(const EmbedArgs& a, bool gather, bool q8b, bool po
 // each sequence writes out[seq] (tickets must hold zeros; they are reset).
 bool embed_gemm3_supported(const EmbedArgs& a, bool q8b);
 hipError_t launch_embed_gemm3(const EmbedArgs& a, bool gather, bool pool, hipStream_t s);
+// The pooled embed of embed_gemm3 with 128-row x 96-column tiles
+// (tiles_per_seq = ceil(T / 128); same requirements, P and tickets).
+hipError_t launch_embed_gemm4(const EmbedArgs& a, hipStream_t s);
 hipError_t launch_embed_finalize(const float* P, int tiles, const int32_t* mask, int64_t B, int64_t T,
                                  int N, uint16_t* out, hipStream_t s);
 hipError_t launch_gather_rows_f16(const uint16_t* table, int64_t vocab, int64_t d, const int32_t* idx,

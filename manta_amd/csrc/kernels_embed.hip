@@ -730,6 +730,191 @@ __global__ __launch_bounds__(256) void embed_gemm3_kernel(EmbedArgs a) {
     if (tid == 0) __hip_atomic_store(&a.tickets[seq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Pooled embed, 128-row x 96-column workgroup tiles (4 waves of 32 rows,
+// each three 32x32 tiles): a workgroup reads a quarter of the projection and
+// 128 gathered rows per K pass, about half the bytes of a 32-row x 384-column
+// tile, which at C1's size is what bounds the K loop.  Same K ring (A by
+// 16-byte loads, projection rows by 4-byte loads, unswizzled: rows 192 bytes
+// apart put the 4 k-rows of a transpose read on distinct banks), same
+// publication and last-tile finish as embed_gemm3_kernel (partials of the 4
+// column slices of a row tile side by side).
+constexpr int E4_WM = 128, E4_WN = 96, E4_NST = 6;
+constexpr int E4_AST = E4_WM * E3_KC * 2;   // 8 KB
+constexpr int E4_BST = E3_KC * E4_WN * 2;   // 6 KB
+constexpr int E4_STAGE = E4_AST + E4_BST;
+
+__global__ __launch_bounds__(256) void embed_gemm4_kernel(EmbedArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float rowv[E3_N];
+    __shared__ float colw[4][E4_WN];
+    __shared__ double dred[4];
+    __shared__ int ired[4];
+    __shared__ int last;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t tile = blockIdx.x;
+    const int slice = blockIdx.y;
+    const int nb0 = slice * E4_WN;
+    const int64_t seq = tile / a.tiles_per_seq;
+    const int64_t t0 = (tile % a.tiles_per_seq) * E4_WM;
+    const int K = a.K;
+
+    // A loads: this wave's 32 rows, two 1 KB loads of 16 rows; lane i fills
+    // stored column i%4 of row 16u + i/4
+    const uint8_t* asrc[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int r = 32 * wave + 16 * u + (lane >> 2);
+        int64_t src = 0;
+        const int64_t t = t0 + r;
+        if (t < a.T) {
+            const int idx = a.tokens[seq * a.T + t];
+            if (idx >= 0 && idx < a.vocab) src = idx;
+            else report_bad_index(a.err, idx);
+        }
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        asrc[u] = (const uint8_t*)a.table + src * K * 2 + c * 16;
+    }
+    // projection loads: six 256-byte pieces of the stage per wave
+    int boff[6];
+#pragma unroll
+    for (int v = 0; v < 6; v++) {
+        const int x = (6 * wave + v) * 256 + lane * 4;
+        boff[v] = (x / (E4_WN * 2)) * E3_N * 2 + nb0 * 2 + x % (E4_WN * 2);
+    }
+    const uint8_t* bsrc = (const uint8_t*)a.B;
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
+    const int nk = K / E3_KC;
+    const int rot = (int)((tile * 4 + slice) % nk);
+    auto issue = [&](int kci, int st) {
+        const int kc = kci + rot < nk ? kci + rot : kci + rot - nk;
+        const uint32_t sa = __builtin_amdgcn_readfirstlane(base + st * E4_STAGE + wave * 2 * 1024);
+#pragma unroll
+        for (int u = 0; u < 2; u++) eg_lds_load16(asrc[u] + kc * E3_KC * 2, sa + u * 1024);
+        const uint32_t sb = __builtin_amdgcn_readfirstlane(base + st * E4_STAGE + E4_AST + wave * 6 * 256);
+        const uint8_t* bk = bsrc + (int64_t)kc * E3_KC * E3_N * 2;
+#pragma unroll
+        for (int v = 0; v < 6; v++) eg_lds_load4(bk + boff[v], sb + v * 256);
+    };
+#pragma unroll
+    for (int st = 0; st < E4_NST - 1; st++)
+        if (st < nk) issue(st, st);
+
+    const int G = lane >> 4, s16 = lane & 15;
+    const int trow = (8 * (G >> 1) + (s16 >> 2)) * E4_WN * 2;
+    const int tcol = (16 * (G & 1) + 4 * (s16 & 3)) * 2;
+
+    f16v acc[3];
+#pragma unroll
+    for (int cb = 0; cb < 3; cb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[cb][r] = 0.0f;
+
+    const int l32 = lane & 31, hf = lane >> 5;
+    int st = 0;
+    for (int kc = 0; kc < nk; kc++, st = st == E4_NST - 1 ? 0 : st + 1) {
+        eg_wait_barrier<8, E4_NST - 2>(nk - 1 - kc);
+        if (kc + E4_NST - 1 < nk) issue(kc + E4_NST - 1, st == 0 ? E4_NST - 1 : st - 1);
+        const uint8_t* As = smem + st * E4_STAGE + wave * 32 * 64;
+        const uint8_t* Bs = smem + st * E4_STAGE + E4_AST;
+#pragma unroll
+        for (int ks = 0; ks < E3_KC / 16; ks++) {
+            const int c = ks * 2 + hf;
+            const h8 av = *(const h8*)(As + l32 * 64 + ((c ^ ((l32 >> 2) & 3)) * 16));
+#pragma unroll
+            for (int cb = 0; cb < 3; cb++) {
+                const uint8_t* p = Bs + trow + tcol + cb * 64 + ks * 16 * E4_WN * 2;
+                const v4s lo = lds_read_tr16(p);
+                const v4s hi = lds_read_tr16(p + 4 * E4_WN * 2);
+                const h8 bv = __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[cb], 0, 0, 0);
+            }
+        }
+    }
+
+    // column sums of the wave's unmasked rows, then of the 4 waves in order
+    bool live[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int64_t t = t0 + 32 * wave + 8 * (r >> 2) + 4 * hf + (r & 3);
+        live[r] = t < a.T && (!a.mask || a.mask[seq * a.T + t] != 0);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 3; cb++) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if (live[r]) sum += acc[cb][r];
+        sum += __shfl_xor(sum, 32);
+        if (hf == 0) colw[wave][cb * 32 + l32] = sum;
+    }
+    __syncthreads();
+    unsigned int* pdst = (unsigned int*)(a.P + (seq * a.tiles_per_seq + t0 / E4_WM) * E3_N + nb0);
+    if (tid < E4_WN) {
+        const float v = ((colw[0][tid] + colw[1][tid]) + colw[2][tid]) + colw[3][tid];
+        __hip_atomic_store(pdst + tid, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(&a.tickets[seq], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(4 * a.tiles_per_seq - 1);
+    __syncthreads();
+    if (!last) return;
+    int cnt = 0;
+    for (int64_t t = tid; t < a.T; t += 256) cnt += (!a.mask || a.mask[seq * a.T + t] != 0) ? 1 : 0;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off);
+    if (lane == 0) ired[wave] = cnt;
+    __syncthreads();
+    const int count = ired[0] + ired[1] + ired[2] + ired[3];
+    const float inv = count ? 1.0f / (float)count : 0.0f;
+    const unsigned int* psrc = (const unsigned int*)(a.P + seq * a.tiles_per_seq * E3_N);
+    double ss = 0.0;
+    for (int c = tid; c < E3_N; c += 256) {
+        float v = 0.0f;
+        for (int s0 = 0; s0 < a.tiles_per_seq; s0 += 8) {
+            unsigned int pv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                pv[u] = s0 + u < a.tiles_per_seq
+                            ? __hip_atomic_load(psrc + (s0 + u) * E3_N + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : 0u;
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (s0 + u < a.tiles_per_seq) v += __uint_as_float(pv[u]);
+        }
+        v = count ? v * inv : 0.0f;
+        rowv[c] = v;
+        ss += (double)v * (double)v;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) dred[wave] = ss;
+    __syncthreads();
+    const float norm = (float)__builtin_sqrt(dred[0] + dred[1] + dred[2] + dred[3]);
+    for (int c = tid; c < E3_N; c += 256) {
+        float v = rowv[c];
+        if (norm != 0.0f) v = v / norm;
+        a.out[seq * E3_N + c] = f2h(v);
+    }
+    if (tid == 0) __hip_atomic_store(&a.tickets[seq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+hipError_t launch_embed_gemm4(const EmbedArgs& a, hipStream_t s) {
+    const size_t lds = (size_t)E4_NST * E4_STAGE;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)embed_gemm4_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL(embed_gemm4_kernel, dim3((unsigned)(a.batches * a.tiles_per_seq), 4u), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
 bool embed_gemm3_supported(const EmbedArgs& a, bool q8b) {
     return !q8b && a.N == E3_N && a.K % E3_KC == 0 && a.K > 0;
 }

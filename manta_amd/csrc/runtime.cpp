@@ -1175,15 +1175,16 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
     a.colscale = col_scale;
     a.err = rt->err_word;
     if (manta::embed_gemm3_supported(a, q8b) && b <= kTickets) {
-        // one launch: 32-row tiles, the last tile of each sequence finishes it
-        a.tiles_per_seq = (int)((t + 31) / 32);
+        // one launch: 128-row x 96-column tiles, the last tile of each
+        // sequence finishes it
+        a.tiles_per_seq = (int)((t + 127) / 128);
         if (b * a.tiles_per_seq > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: batch too large");
         rc = ensure_workspace(rt, align_up((size_t)(b * a.tiles_per_seq * e) * sizeof(float), 256), err);
         if (rc) return rc;
         a.P = (float*)rt->ws;
         a.tickets = rt->tickets;
         a.out = out;
-        LAUNCH_TRY(manta::launch_embed_gemm3(a, true, true, rt->stream), "embed");
+        LAUNCH_TRY(manta::launch_embed_gemm4(a, rt->stream), "embed");
         rt->gather_pending = true;
         return MANTA_ROCM_OK;
     }
