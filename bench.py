@@ -178,6 +178,12 @@ def run_c2(rt, steps, warmup) -> dict:
     fams = ["mq_scan", "mq_select", "q4_scan", "topk_merge", "query_encode", "mq_clear"]
     step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "cosine", qd, k, out=(ids, sc, None)),
                                  steps, warmup, fams)
+    # the presets' step after top-k: candidate ids, packed rows and scales of
+    # the selected rows
+    cid = rt.to_device(np.arange(n, dtype=np.int64) * 7 + 3)
+    pack_s, pfam, _ = _timed(rt, lambda: rt.pack_candidates(cands, ids, cid), steps, warmup, ["pack_candidates"],
+                             min_warm_s=0.1)
+    pack_bytes = nq * k * (4 + 8 + d // 2 + d // 16 + 8 + d // 2 + d // 16)  # reads + writes
     dom = "mq_scan" if fam["mq_scan"][0] else "q4_scan"
     # the scan reads the q4 matrix's int8 shadow: 384 code bytes and one f32
     # scale per row (built once, on the first call)
@@ -196,6 +202,9 @@ def run_c2(rt, steps, warmup) -> dict:
                      "i8_tops": ops / (fam[dom][2] / 1000.0) / 1e12, "i8_frac": ops / (fam[dom][2] / 1000.0) / 1e12 / I8_PEAK,
                      "note": "all threshold passes of the scan together cover the N rows once; survivors are "
                              "rescored with the exact q4 contract in mq_select"},
+        "pack_candidates": {"us_per_call": pfam["pack_candidates"][1] * 1000.0, "rows": nq * k,
+                            "bytes_per_call": pack_bytes,
+                            "GB_s": pack_bytes / (pfam["pack_candidates"][1] / 1000.0) / 1e9},
     }
 
 

@@ -179,6 +179,21 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* cands, int o
                           int32_t* out_ids_dev, float* out_scores_dev, int64_t* out_acc_dev,
                           char** err);
 
+/* The retrieval presets' last steps after top-k (compiler/compiler.go:539-570):
+ * gather(candidate_ids, top), gather(docs, top) and pack_candidates
+ * (tensor_ops.go:66-82, the pack holding ids, scores and docs, tensor.go:27-31),
+ * on device and on the packed rows themselves.  top_dev: int32 [nq, k] row
+ * indices (as manta_rocm_score_topk returns them); candidate_ids_dev: int64
+ * [sets, n] or NULL; outputs: out_ids_dev int64 [nq, k] (skipped when
+ * candidate_ids_dev is NULL), out_rows_dev [nq, k, row_bytes] with row_bytes =
+ * d (q8) or d/2 (q4), out_scales_dev [nq, k, s] with s = 1 f32 (q8) or d/32
+ * f16 (q4).  With sets == nq query q takes rows of set q.  The scores are the
+ * top-k call's.  An index outside [0, n) zero-fills its slot and is reported
+ * by the next synchronizing call as "gather index %d out of range". */
+int manta_rocm_pack_candidates(MantaRocm* rt, const MantaRocmCandidates* cands, const int32_t* top_dev,
+                               int64_t nq, int64_t k, const int64_t* candidate_ids_dev, int64_t* out_ids_dev,
+                               void* out_rows_dev, void* out_scales_dev, char** err);
+
 /* top-k over an f32 score matrix [rows, cols] (rows == 1 is the rank-1
  * form).  Replaces topKTensor (tensor_ops.go:1523-1592). */
 int manta_rocm_topk(MantaRocm* rt, const float* scores_dev, int64_t rows, int64_t cols, int64_t k,

@@ -70,6 +70,7 @@ SIGNATURES = {
     ),
     "manta_rocm_topk": (C.c_int, [_p, _p, _i64, _i64, _i64, C.c_int, _p, _p, _err]),
     "manta_rocm_gather_rows_f16": (C.c_int, [_p, _p, _i64, _i64, _p, _i64, _p, _err]),
+    "manta_rocm_pack_candidates": (C.c_int, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p, _err]),
     "manta_rocm_matmul_f16": (C.c_int, [_p, _p, _i64, _i64, _p, C.c_int, _p, _i64, _p, _err]),
     "manta_rocm_mean_pool_masked": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, _p, _err]),
     "manta_rocm_normalize_rows": (C.c_int, [_p, _p, _i64, _i64, _err]),

@@ -174,6 +174,24 @@ size_t mq_select_lds(int threads, int R);
 hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s);
 hipError_t launch_mq_clear(uint64_t* tau, int* bcnt, int nq, hipStream_t s);
 
+// Candidate pack after top-k (kernels_topk.hip).
+struct PackArgs {
+    const int32_t* top;         // [nq][k] row indices
+    int64_t nq, k, n;
+    int sets;                   // 1 (shared rows) or nq (set q per query)
+    const uint8_t* codes;       // [sets][n][pitch]
+    int64_t pitch;              // bytes between rows
+    int row_bytes;              // bytes copied per row
+    const uint8_t* scales;      // [sets][n][scale_bytes]
+    int scale_bytes;
+    const int64_t* ids;         // [sets][n] or nullptr
+    int64_t* ids_out;           // [nq][k] or nullptr
+    uint8_t* rows_out;          // [nq][k][row_bytes]
+    uint8_t* scales_out;        // [nq][k][scale_bytes]
+    unsigned long long* err;    // first out-of-range index
+};
+hipError_t launch_pack_candidates(const PackArgs& a, hipStream_t s);
+
 // Arguments of the embed GEMM kernels (kernels_embed.hip).
 struct EmbedArgs {
     const int32_t* tokens;      // [batches*T] (pooled) or [M] (gathered matmul)

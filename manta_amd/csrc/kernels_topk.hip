@@ -82,4 +82,38 @@ hipError_t launch_topk_merge(const uint64_t* partial, int64_t rows, int64_t per_
     return hipGetLastError();
 }
 
+// ------------------------------------------------------ candidate pack
+
+// One wave per (query, rank): the candidate id (int64), the packed row's
+// bytes (4-byte words when row_bytes and pitch allow, else bytes) and its
+// scales.  An index outside [0, n) zero-fills the slot and is reported.
+__global__ __launch_bounds__(256) void pack_candidates_kernel(PackArgs a) {
+    const int64_t slot = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (slot >= a.nq * a.k) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t q = slot / a.k;
+    const int idx = a.top[slot];
+    const bool ok = idx >= 0 && (int64_t)idx < a.n;
+    if (!ok && lane == 0 && a.err) atomicCAS(a.err, 0ull, (1ull << 32) | (unsigned long long)(uint32_t)idx);
+    const int64_t row = (a.sets == 1 ? 0 : q * a.n) + (ok ? idx : 0);
+    if (a.ids_out && lane == 0) a.ids_out[slot] = (a.ids && ok) ? a.ids[row] : 0;
+    uint8_t* dst = a.rows_out + slot * a.row_bytes;
+    const uint8_t* src = a.codes + row * a.pitch;
+    if ((a.row_bytes & 3) == 0 && (a.pitch & 3) == 0) {
+        for (int w = lane; w < a.row_bytes / 4; w += 64)
+            ((uint32_t*)dst)[w] = ok ? ((const uint32_t*)src)[w] : 0u;
+    } else {
+        for (int b = lane; b < a.row_bytes; b += 64) dst[b] = ok ? src[b] : (uint8_t)0;
+    }
+    uint8_t* sdst = a.scales_out + slot * a.scale_bytes;
+    const uint8_t* ssrc = a.scales + row * a.scale_bytes;
+    for (int b = lane; b < a.scale_bytes; b += 64) sdst[b] = ok ? ssrc[b] : (uint8_t)0;
+}
+
+hipError_t launch_pack_candidates(const PackArgs& a, hipStream_t s) {
+    const int64_t slots = a.nq * a.k;
+    hipLaunchKernelGGL(pack_candidates_kernel, dim3((unsigned)((slots + 3) / 4)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace manta

@@ -1025,6 +1025,37 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, i
     return MANTA_ROCM_OK;
 }
 
+int manta_rocm_pack_candidates(MantaRocm* rt, const MantaRocmCandidates* c, const int32_t* top, int64_t nq,
+                               int64_t k, const int64_t* candidate_ids, int64_t* out_ids, void* out_rows,
+                               void* out_scales, char** err) {
+    RT_CHECK(rt);
+    if (!c || !top || !out_rows || !out_scales) return fail(err, MANTA_ROCM_ERROR, "nil pack_candidates input");
+    if (nq <= 0 || k <= 0) return fail(err, MANTA_ROCM_ERROR, "pack_candidates expects nq > 0 and k > 0");
+    if (c->sets != 1 && c->sets != nq)
+        return fail(err, MANTA_ROCM_ERROR, "pack_candidates: %lld queries for %lld candidate sets", (long long)nq,
+                    (long long)c->sets);
+    if (out_ids && !candidate_ids) return fail(err, MANTA_ROCM_ERROR, "pack_candidates: ids output without candidate ids");
+    manta::PackArgs a{};
+    a.top = top;
+    a.nq = nq;
+    a.k = k;
+    a.n = c->n;
+    a.sets = (int)c->sets;
+    a.codes = (const uint8_t*)c->codes;
+    a.pitch = c->pitch;
+    a.row_bytes = c->format == MANTA_ROCM_Q8_ROWS ? (int)c->d : (int)(c->d / 2);
+    a.scales = (const uint8_t*)c->scales;
+    a.scale_bytes = c->format == MANTA_ROCM_Q8_ROWS ? 4 : (int)(c->nb * 2);
+    a.ids = candidate_ids;
+    a.ids_out = out_ids;
+    a.rows_out = (uint8_t*)out_rows;
+    a.scales_out = (uint8_t*)out_scales;
+    a.err = rt->err_word;
+    LAUNCH_TRY(manta::launch_pack_candidates(a, rt->stream), "pack_candidates");
+    rt->gather_pending = true;
+    return MANTA_ROCM_OK;
+}
+
 int manta_rocm_topk(MantaRocm* rt, const float* scores, int64_t rows, int64_t cols, int64_t k,
                     int order, int32_t* out_ids, float* out_values, char** err) {
     RT_CHECK(rt);

@@ -201,6 +201,21 @@ class Runtime:
              C.c_int64(k), ids.ptr, _ptr(sc), _ptr(acc))
         return ids, sc, acc
 
+    def pack_candidates(self, cands: Candidates, top: DeviceArray,
+                        candidate_ids: Optional[DeviceArray] = None):
+        """Candidate ids (int64, when given), packed rows and row scales of
+        the top-k rows: (ids or None, rows [nq, k, row_bytes] int8 (q8) or
+        uint8 nibble pairs (q4), scales [nq, k, s] f32 (q8) or f16 bits (q4))."""
+        nq, k = top.shape
+        q8 = cands.format == _lib.Q8_ROWS
+        row_bytes = cands.d if q8 else cands.d // 2
+        rows = self.empty((nq, k, row_bytes), np.int8 if q8 else np.uint8)
+        scales = self.empty((nq, k, 1), np.float32) if q8 else self.empty((nq, k, cands.d // 32), np.uint16)
+        ids = self.empty((nq, k), np.int64) if candidate_ids is not None else None
+        call("manta_rocm_pack_candidates", self.handle, cands.handle, top.ptr, C.c_int64(nq), C.c_int64(k),
+             _ptr(candidate_ids), _ptr(ids), rows.ptr, scales.ptr)
+        return ids, rows, scales
+
     def topk(self, scores: DeviceArray, k: int, smallest: bool = False):
         rows, cols = (1, scores.shape[0]) if len(scores.shape) == 1 else scores.shape
         ids = self.empty((rows, k), np.int32)

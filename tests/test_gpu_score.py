@@ -498,3 +498,58 @@ def test_q4_shadow_all_ties_zero_rows_and_zero_query(rt, op, smallest):
     cands = rt.bind_q4(packed, s4, d)
     _check_q4_topk(rt, cands, op, q, packed, s4, d, k, smallest)
     cands.close()
+
+
+# ---------------------------------------------------------------------------
+# After top-k: candidate ids, packed rows and scales of the selected rows
+# (gather + pack_candidates of the retrieval presets), bit for bit.
+
+@pytest.mark.parametrize("fmt,sets,d", [("q8", 1, 256), ("q8", 3, 100), ("q4", 1, 384), ("q4", 3, 64)])
+def test_pack_candidates_bit_exact(rt, fmt, sets, d):
+    nq, n, k = 3, 5000, 37
+    rng = np.random.default_rng(d + sets)
+    if fmt == "q8":
+        q, codes, scales = _q8_case(d + sets, nq, n, d, sets=sets)
+        codes, scales = (codes[0], scales[0]) if sets == 1 else (codes, scales)
+        cands = rt.bind_q8(codes, scales)
+        rows_ref, scales_ref = codes, scales[..., None]
+    else:
+        q = synth.normal_f16(300 + d, 0, nq, d, 1.0, normalize=True)
+        packed = np.empty((sets, n, d // 2), np.uint8)
+        s4 = np.empty((sets, n, d // 32), np.uint16)
+        for s_ in range(sets):
+            packed[s_], s4[s_] = synth.q4_rows(300 + d, 1 + s_, n, d, normalize=True)
+        packed, s4 = (packed[0], s4[0]) if sets == 1 else (packed, s4)
+        cands = rt.bind_q4(packed, s4, d)
+        rows_ref, scales_ref = packed, s4
+    cid = rng.integers(-2**62, 2**62, size=(sets, n) if sets > 1 else (n,), dtype=np.int64)
+    top, _, _ = rt.score_topk(cands, "dot", rt.to_device(q), k)
+    ids, rows, sc = rt.pack_candidates(cands, top, rt.to_device(cid))
+    t = top.download()
+    if sets == 1:
+        want_ids, want_rows, want_sc = cid[t], rows_ref[t], scales_ref[t]
+    else:
+        qi = np.arange(nq)[:, None]
+        want_ids, want_rows, want_sc = cid[qi, t], rows_ref[qi, t], scales_ref[qi, t]
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(rows.download(), want_rows)
+    np.testing.assert_array_equal(sc.download().view(np.uint8), np.ascontiguousarray(want_sc).view(np.uint8))
+    # without candidate ids: rows and scales only
+    none_ids, rows2, _ = rt.pack_candidates(cands, top)
+    assert none_ids is None
+    np.testing.assert_array_equal(rows2.download(), want_rows)
+    cands.close()
+
+
+def test_pack_candidates_out_of_range_index(rt):
+    nq, n, d, k = 2, 300, 128, 4
+    q, codes, scales = _q8_case(7, nq, n, d, sets=1)
+    cands = rt.bind_q8(codes[0], scales[0])
+    top = np.array([[0, 1, 2, 3], [4, n, 5, 6]], np.int32)
+    ids, rows, _ = rt.pack_candidates(cands, rt.to_device(top), rt.to_device(np.arange(n, dtype=np.int64)))
+    with pytest.raises(MantaRocmError, match="gather index %d out of range" % n):
+        rt.synchronize()
+    got = rows.download()
+    np.testing.assert_array_equal(got[1, 1], 0)  # the bad slot is zero-filled
+    np.testing.assert_array_equal(got[0], codes[0][top[0]])
+    cands.close()
