@@ -233,6 +233,12 @@ hipError_t launch_embed_gemm3(const EmbedArgs& a, bool gather, bool pool, hipStr
 // The pooled embed of embed_gemm3 with 128-row x 96-column tiles
 // (tiles_per_seq = ceil(T / 128); same requirements, P and tickets).
 hipError_t launch_embed_gemm4(const EmbedArgs& a, hipStream_t s);
+// Pooled embed with the projection pre-transposed (launch_embed_transpose_b)
+// for N == 384, K % 32 == 0, T in {64, 128, 256} and batches*T a multiple of
+// 256: 256-row workgroups of whole sequences finish their embeddings in one
+// launch (no P, no tickets).
+bool embed_gemm5_supported(const EmbedArgs& a);
+hipError_t launch_embed_gemm5(const EmbedArgs& a, bool q8b, const uint16_t* Bt, hipStream_t s);
 hipError_t launch_embed_finalize(const float* P, int tiles, const int32_t* mask, int64_t B, int64_t T,
                                  int N, uint16_t* out, hipStream_t s);
 hipError_t launch_gather_rows_f16(const uint16_t* table, int64_t vocab, int64_t d, const int32_t* idx,

@@ -915,6 +915,193 @@ hipError_t launch_embed_gemm4(const EmbedArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Pooled embed for large batches of short sequences (T = 64, 128 or 256):
+// one workgroup of 8 waves = 256 rows (whole sequences) x all N = 384
+// columns, each wave 64 rows x 192 columns (2 x 6 tiles of
+// v_mfma_f32_32x32x16_f16), operands as in embed_gemm2_kernel (projection
+// pre-transposed to f16 [N][K]).  A 256 x 384 tile moves 5 bytes per output
+// through L2 against 9 for 256 x 128, and the tile holds whole sequences, so
+// pooling, the count, the norm and the f16 store all happen in the
+// workgroup: one launch after the transpose, no partials, no finalize.
+constexpr int E5_WM = 256, E5_N = 384, E5_NST = 3;
+constexpr int E5_AST = E5_WM * E3_KC * 2;   // 16 KB
+constexpr int E5_BST = E5_N * E3_KC * 2;    // 24 KB
+constexpr int E5_STAGE = E5_AST + E5_BST;
+
+template <bool Q8B>
+__global__ __launch_bounds__(512) void embed_gemm5_kernel(EmbedArgs a, const uint16_t* Bt) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ double dred[8];
+    __shared__ int ired[8];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int rg = wave & 3, cg = wave >> 2;
+    const int64_t row0 = (int64_t)blockIdx.x * E5_WM;  // first row of b*T
+    const int K = a.K;
+
+    const uint8_t* asrc[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int r = 16 * (2 * wave + u) + (lane >> 2);
+        const int idx = a.tokens[row0 + r];
+        int64_t src = 0;
+        if (idx >= 0 && idx < a.vocab) src = idx;
+        else report_bad_index(a.err, idx);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        asrc[u] = (const uint8_t*)a.table + src * K * 2 + c * 16;
+    }
+    const uint8_t* bsrc[3];
+#pragma unroll
+    for (int u = 0; u < 3; u++) {
+        const int n = 16 * (3 * wave + u) + (lane >> 2);
+        const int c = (lane & 3) ^ ((n >> 2) & 3);
+        bsrc[u] = (const uint8_t*)Bt + (int64_t)n * K * 2 + c * 16;
+    }
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
+    auto issue = [&](int kc, int st) {
+        const uint32_t sa = __builtin_amdgcn_readfirstlane(base + st * E5_STAGE + wave * 2 * 1024);
+#pragma unroll
+        for (int u = 0; u < 2; u++) eg_lds_load16(asrc[u] + kc * E3_KC * 2, sa + u * 1024);
+        const uint32_t sb = __builtin_amdgcn_readfirstlane(base + st * E5_STAGE + E5_AST + wave * 3 * 1024);
+#pragma unroll
+        for (int u = 0; u < 3; u++) eg_lds_load16(bsrc[u] + kc * E3_KC * 2, sb + u * 1024);
+    };
+    const int nk = K / E3_KC;
+#pragma unroll
+    for (int st = 0; st < E5_NST - 1; st++)
+        if (st < nk) issue(st, st);
+
+    f16v acc[2][6];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 6; cb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
+
+    const int l32 = lane & 31, hf = lane >> 5;
+    int st = 0;
+    for (int kc = 0; kc < nk; kc++, st = st == E5_NST - 1 ? 0 : st + 1) {
+        eg_wait_barrier<5, E5_NST - 2>(nk - 1 - kc);
+        if (kc + E5_NST - 1 < nk) issue(kc + E5_NST - 1, st == 0 ? E5_NST - 1 : st - 1);
+        const uint8_t* As = smem + st * E5_STAGE;
+        const uint8_t* Bs = As + E5_AST;
+#pragma unroll
+        for (int ks = 0; ks < E3_KC / 16; ks++) {
+            const int c = ks * 2 + hf;
+            h8 av[2];
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++) {
+                const int r = 64 * rg + 32 * rb + l32;
+                av[rb] = *(const h8*)(As + r * 64 + ((c ^ ((r >> 2) & 3)) * 16));
+            }
+#pragma unroll
+            for (int cb = 0; cb < 6; cb++) {
+                const int n = 192 * cg + 32 * cb + l32;
+                const h8 bv = *(const h8*)(Bs + n * 64 + ((c ^ ((n >> 2) & 3)) * 16));
+#pragma unroll
+                for (int rb = 0; rb < 2; rb++)
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[rb], bv, acc[rb][cb], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();  // every wave is done with the stage buffers
+
+    // Column sums of the wave's unmasked rows (its 64 rows lie in one
+    // sequence), then per sequence over its row groups in order.  Output
+    // element (rb, cb, r): row 64*rg + 32*rb + 8*(r/4) + 4*(lane/32) + r%4,
+    // column 192*cg + 32*cb + lane%32.
+    float* part = (float*)smem;                 // [4][384]
+    float* rowv = part + 4 * E5_N;              // [4][384]
+    const int64_t T = a.T;
+    const int64_t seq_w = (row0 + 64 * rg) / T;
+    const int64_t tw = (row0 + 64 * rg) % T;
+    bool live[2][16];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int64_t t = tw + 32 * rb + 8 * (r >> 2) + 4 * hf + (r & 3);
+            live[rb][r] = !a.mask || a.mask[seq_w * T + t] != 0;
+        }
+#pragma unroll
+    for (int cb = 0; cb < 6; cb++) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                if (live[rb][r]) sum += acc[rb][cb][r];
+        sum += __shfl_xor(sum, 32);
+        const int n = 192 * cg + 32 * cb + l32;
+        if (hf == 0) part[rg * E5_N + n] = Q8B ? sum * a.colscale[n] : sum;
+    }
+    __syncthreads();
+    // 128 threads per sequence (at most 4 sequences of the tile)
+    const int S = (int)(E5_WM / T);
+    const int sl = tid >> 7, j = tid & 127;
+    const int gps = (int)(T / 64);  // row groups per sequence
+    const int64_t seq = row0 / T + sl;
+    int cnt = 0;
+    if (sl < S)
+        for (int64_t t = j; t < T; t += 128) cnt += (!a.mask || a.mask[seq * T + t] != 0) ? 1 : 0;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off);
+    if (lane == 0) ired[wave] = cnt;
+    __syncthreads();
+    const int count = sl < S ? ired[2 * sl] + ired[2 * sl + 1] : 0;
+    const float inv = count ? 1.0f / (float)count : 0.0f;
+    double ss = 0.0;
+    if (sl < S) {
+        for (int c = j; c < E5_N; c += 128) {
+            float v = 0.0f;
+            for (int g2 = 0; g2 < gps; g2++) v += part[(sl * gps + g2) * E5_N + c];
+            v = count ? v * inv : 0.0f;
+            rowv[sl * E5_N + c] = v;
+            ss += (double)v * (double)v;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) dred[wave] = ss;
+    __syncthreads();
+    if (sl < S) {
+        const float norm = (float)__builtin_sqrt(dred[2 * sl] + dred[2 * sl + 1]);
+        for (int c = j; c < E5_N; c += 128) {
+            float v = rowv[sl * E5_N + c];
+            if (norm != 0.0f) v = v / norm;
+            a.out[seq * E5_N + c] = f2h(v);
+        }
+    }
+}
+
+bool embed_gemm5_supported(const EmbedArgs& a) {
+    return a.N == E5_N && a.K % E3_KC == 0 && a.K > 0 && (a.T == 64 || a.T == 128 || a.T == 256) &&
+           (a.batches * a.T) % E5_WM == 0;
+}
+
+hipError_t launch_embed_gemm5(const EmbedArgs& a, bool q8b, const uint16_t* Bt, hipStream_t s) {
+    const size_t lds = (size_t)E5_NST * E5_STAGE;
+    const unsigned grid = (unsigned)(a.batches * a.T / E5_WM);
+#define MANTA_EG5(Q)                                                                                   \
+    if (q8b == Q) {                                                                                    \
+        static bool attr = false;                                                                      \
+        if (!attr) {                                                                                   \
+            hipError_t e = hipFuncSetAttribute((const void*)embed_gemm5_kernel<Q>,                     \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            if (e != hipSuccess) return e;                                                             \
+            attr = true;                                                                               \
+        }                                                                                              \
+        hipLaunchKernelGGL((embed_gemm5_kernel<Q>), dim3(grid), dim3(512), lds, s, a, Bt);              \
+        return hipGetLastError();                                                                      \
+    }
+    MANTA_EG5(true)
+    MANTA_EG5(false)
+#undef MANTA_EG5
+    return hipErrorInvalidValue;
+}
+
 bool embed_gemm3_supported(const EmbedArgs& a, bool q8b) {
     return !q8b && a.N == E3_N && a.K % E3_KC == 0 && a.K > 0;
 }

@@ -1205,6 +1205,18 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
     a.B = proj;
     a.colscale = col_scale;
     a.err = rt->err_word;
+    if (manta::embed_gemm5_supported(a) && b * t / 256 >= 128) {
+        // many short sequences: 256-row workgroups of whole sequences finish
+        // their embeddings themselves (after the projection's transpose)
+        rc = ensure_workspace(rt, (size_t)d * e * 2 + 256, err);
+        if (rc) return rc;
+        a.out = out;
+        uint16_t* bt = (uint16_t*)rt->ws;
+        LAUNCH_TRY(manta::launch_embed_transpose_b(a, q8b, bt, rt->stream), "embed_transpose");
+        LAUNCH_TRY(manta::launch_embed_gemm5(a, q8b, bt, rt->stream), "embed");
+        rt->gather_pending = true;
+        return MANTA_ROCM_OK;
+    }
     if (manta::embed_gemm3_supported(a, q8b) && b <= kTickets) {
         // one launch: 128-row x 96-column tiles, the last tile of each
         // sequence finishes it

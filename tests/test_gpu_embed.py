@@ -151,3 +151,31 @@ def test_step_by_step_pipeline_matches_fused(rt):
     _, want32 = orc.embed(tokens, mask, table, proj_f16=proj)
     assert _cos_rows(steps, want32).min() >= 0.9999
     assert _cos_rows(fused, steps).min() >= 0.9999
+
+
+@pytest.mark.parametrize("nq,t,q8", [(512, 64, True), (256, 128, False), (128, 256, True)])
+def test_embed_large_batch_whole_sequence_tiles(rt, nq, t, q8):
+    """Batches large enough for 256-row workgroups of whole sequences
+    (T = 64, 128, 256), ragged and empty sequences, q8 and f16 projections."""
+    d = e = 384
+    tokens = synth.uniform_i32(17, 0, nq * t, 0, 32000).reshape(nq, t)
+    lengths = synth.uniform_i32(17, 1, nq, 0, t + 1)
+    lengths[::37] = 0
+    lengths[1::41] = t
+    mask = (np.arange(t)[None, :] < lengths[:, None]).astype(np.int32)
+    table = synth.normal_f16(17, 2, 32000, d, 0.02)
+    if q8:
+        pcodes = synth.uniform_i8(17, 3, d * e, -127, 127).reshape(d, e)
+        cs = (np.arange(e, dtype=np.float32) + 1.0) / (127.0 * np.sqrt(d) * e)
+        got = rt.embed_pooled(rt.to_device(tokens), rt.to_device(mask), rt.to_device(table),
+                              rt.to_device(pcodes), rt.to_device(cs.astype(np.float32))).download()
+        _, want32 = orc.embed(tokens, mask, table, proj_codes=pcodes, col_scale=cs.astype(np.float32))
+    else:
+        proj = synth.normal_f16(17, 3, d, e, 1.0 / np.sqrt(d))
+        got = rt.embed_pooled(rt.to_device(tokens), rt.to_device(mask), rt.to_device(table),
+                              rt.to_device(proj)).download()
+        _, want32 = orc.embed(tokens, mask, table, proj_f16=proj)
+    g = orc.f16_to_f32(got)
+    empty = lengths == 0
+    assert np.all(g[empty] == 0) and np.all(want32[empty] == 0)
+    assert _cos_rows(g[~empty], want32[~empty]).min() >= 0.9999
