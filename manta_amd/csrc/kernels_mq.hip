@@ -786,9 +786,13 @@ size_t mq_select_lds(int threads, int R) { return (size_t)threads * 16 * 8 + (si
 
 template <int PM>
 static void launch_mq_select_pm(const MqSelectArgs& a, int threads, size_t lds, hipStream_t s) {
-    if (threads == 1024)
-        hipLaunchKernelGGL((mq_select_kernel<1024, PM>), dim3((unsigned)a.nq), dim3(1024), lds, s, a);
-    else if (threads == 512)
+    if constexpr (PM != 2) {
+        if (threads == 1024) {
+            hipLaunchKernelGGL((mq_select_kernel<1024, PM>), dim3((unsigned)a.nq), dim3(1024), lds, s, a);
+            return;
+        }
+    }
+    if (threads == 512)
         hipLaunchKernelGGL((mq_select_kernel<512, PM>), dim3((unsigned)a.nq), dim3(512), lds, s, a);
     else
         hipLaunchKernelGGL((mq_select_kernel<256, PM>), dim3((unsigned)a.nq), dim3(256), lds, s, a);
@@ -799,6 +803,9 @@ hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s) {
     // shadow pairs: rows of at most 12 blocks (a row's blocks are in flight
     // per thread)
     if (a.pairs == 2 && (a.d % 32 != 0 || a.d > 384)) return hipErrorInvalidValue;
+    // shadow pairs: at most 512 threads (the rescoring's registers at 1024
+    // threads spill)
+    if (a.pairs == 2 && threads > 512) return hipErrorInvalidValue;
     if (threads != 256 && threads != 512 && threads != 1024) return hipErrorInvalidValue;
     if (a.pairs == 1)
         launch_mq_select_pm<1>(a, threads, lds, s);

@@ -168,19 +168,20 @@ __device__ __forceinline__ int wave_append(int cnt, int* counter) {
     return base + incl - cnt;
 }
 
-// Sort keys[0..S) descending in place (S a power of two, S <= NT*16), whole
-// workgroup of NT threads.  Bitonic network over registers: thread t holds
-// elements t + j*NT; exchanges at strides below 64 are lane shuffles, at
-// strides of NT and more stay inside a thread, and only the strides in
-// between go through LDS (two barriers each).
-template <int NT>
-__device__ inline void block_sort_desc_regs(uint64_t* keys, int S) {
-    constexpr int MAXJ = 16;
+// Sort keys[0..S) descending in place, whole workgroup of NT threads, with
+// J = S / NT slots per thread known at compile time (S a power of two,
+// NT / 2 < S <= J * NT when J > 1).  Bitonic network over registers: thread
+// t holds elements t + j*NT; exchanges at strides below 64 are lane
+// shuffles, at strides of NT and more stay inside a thread, and only the
+// strides in between go through LDS (two barriers each).  J must be a
+// constant: with a run-time slot count the slot loops stay rolled and every
+// step indexes the register array dynamically.
+template <int NT, int J>
+__device__ __forceinline__ void block_sort_desc_regs_j(uint64_t* keys, int S) {
     const int tid = threadIdx.x;
-    const int J = (S + NT - 1) / NT;  // slots in use (uniform)
-    uint64_t v[MAXJ];
+    uint64_t v[J];
 #pragma unroll
-    for (int j = 0; j < MAXJ; j++) {
+    for (int j = 0; j < J; j++) {
         const int i = tid + j * NT;
         v[j] = i < S ? keys[i] : 0ull;
     }
@@ -192,12 +193,11 @@ __device__ inline void block_sort_desc_regs(uint64_t* keys, int S) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             if (stride >= NT) {
 #pragma unroll
-                for (int lg = 0; lg < 4; lg++) {
-                    const int sj = 1 << lg;
+                for (int sj = 1; sj < J; sj <<= 1) {
                     if (stride != sj * NT) continue;
 #pragma unroll
-                    for (int j = 0; j < MAXJ; j++) {
-                        if ((j & sj) || tid + (j | sj) * NT >= S) continue;
+                    for (int j = 0; j < J; j++) {
+                        if (j & sj) continue;
                         const int jp = j | sj;
                         const bool desc = ((tid + j * NT) & size) == 0;
                         const uint64_t a = v[j], c = v[jp];
@@ -207,22 +207,18 @@ __device__ inline void block_sort_desc_regs(uint64_t* keys, int S) {
                 }
             } else if (stride >= 64) {
 #pragma unroll
-                for (int j = 0; j < MAXJ; j++) {
-                    if (j >= J) break;
+                for (int j = 0; j < J; j++)
                     if (tid + j * NT < S) keys[tid + j * NT] = v[j];
-                }
                 __syncthreads();
 #pragma unroll
-                for (int j = 0; j < MAXJ; j++) {
-                    if (j >= J) break;
+                for (int j = 0; j < J; j++) {
                     const int i = tid + j * NT;
                     if (i < S) v[j] = pick(v[j], keys[i ^ stride], (i & size) == 0, (i & stride) == 0);
                 }
                 __syncthreads();
             } else {
 #pragma unroll
-                for (int j = 0; j < MAXJ; j++) {
-                    if (j >= J) break;
+                for (int j = 0; j < J; j++) {
                     const int i = tid + j * NT;
                     const uint64_t other = __shfl_xor(v[j], stride);
                     if (i < S) v[j] = pick(v[j], other, (i & size) == 0, (i & stride) == 0);
@@ -231,9 +227,19 @@ __device__ inline void block_sort_desc_regs(uint64_t* keys, int S) {
         }
     }
 #pragma unroll
-    for (int j = 0; j < MAXJ; j++)
+    for (int j = 0; j < J; j++)
         if (tid + j * NT < S) keys[tid + j * NT] = v[j];
     __syncthreads();
+}
+
+// Sort keys[0..S) descending in place (S a power of two, S <= NT*16).
+template <int NT>
+__device__ __forceinline__ void block_sort_desc_regs(uint64_t* keys, int S) {
+    if (S <= NT) block_sort_desc_regs_j<NT, 1>(keys, S);
+    else if (S <= 2 * NT) block_sort_desc_regs_j<NT, 2>(keys, S);
+    else if (S <= 4 * NT) block_sort_desc_regs_j<NT, 4>(keys, S);
+    else if (S <= 8 * NT) block_sort_desc_regs_j<NT, 8>(keys, S);
+    else block_sort_desc_regs_j<NT, 16>(keys, S);
 }
 
 // Chunk tiles per workgroup: as many (2..4) as fit in about 72 KB of LDS
