@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         const int i = 8 * (r / 4) + 4 * half + (r % 4);
         return wq * QPW + na * QPB + (ENC == MQ_E8 ? i : (i >> 4) * 8 + (i & 7));
     };
-    uint32_t live[NA];  // slots whose query exists (score-matrix mode)
+    uint32_t live[NA];  // slots whose query exists
 #pragma unroll
     for (int na = 0; na < NA; na++) {
         live[na] = 0;
@@ -266,13 +266,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 #pragma unroll
             for (int u = 0; u < QPL; u++) {
                 const float p = pre_of(acc[na], v, u, scale, rowc);
-                if (keep_of(v, u, p, rowc)) {
+                if (keep_of(v, u, p, rowc) && ((live[na] >> u) & 1)) {
                     const int lq = slot_lq(na, u);
+                    // (no comparison with the threshold key: the bound test
+                    // is at most an ulp looser, and the select merges with k
+                    // keys above the threshold, which such a key cannot
+                    // displace; live excludes the padding queries)
                     const uint64_t key = make_key(score_of(p, lq, rowc), (uint32_t)row, SMALL);
-                    if (key > tau_s[lq]) {
-                        const int pos = atomicAdd(&cnt_s[lq], 1);
-                        wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = key;
-                    }
+                    const int pos = atomicAdd(&cnt_s[lq], 1);
+                    wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = key;
                 }
             }
         }
@@ -534,6 +536,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     // all of a pass's shadow pairs fit: rank them by pre-score first
     const bool prune = PM == 2 && M > k && M <= LCAP - fill;
 
+    bool compacted = false;  // a compaction left the k-th best key in minkey
     for (int base = 0; base < M;) {
         const int take = (M - base) < (LCAP - fill) ? (M - base) : (LCAP - fill);
         int added = take;  // keys this batch leaves in buf (fewer after pruning)
@@ -650,9 +653,11 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
         }
         fill += added;
         base += take;
-        if (fill > k && (fill == LCAP || base == M)) compact();
+        if (fill > k && (fill == LCAP || base == M)) {
+            compact();
+            compacted = true;
+        }
     }
-    bool compacted = false;
     if (fill > k) {
         compact();
         compacted = true;

@@ -177,9 +177,20 @@ class Runtime:
         return Candidates(self, h, _lib.Q4_BLOCKS, sets, n, d)
 
     # ------------------------------------------------------------ scoring
+    @staticmethod
+    def _query_rows(cands: Candidates, queries: DeviceArray) -> int:
+        """Rows of a query array: f16 values (float16, or uint16 f16 bits),
+        [d] or [nq, d].  The C ABI reads the buffer as f16 bits, so any other
+        dtype would be misread."""
+        if np.dtype(queries.dtype) not in (np.dtype(np.float16), np.dtype(np.uint16)):
+            raise TypeError("queries must be float16 or uint16 f16 bits (got %s)" % np.dtype(queries.dtype))
+        if queries.shape[-1] != cands.d or len(queries.shape) not in (1, 2):
+            raise ValueError("queries must be [d] or [nq, d] with d=%d (got %s)" % (cands.d, tuple(queries.shape)))
+        return queries.shape[0] if len(queries.shape) == 2 else 1
+
     def score(self, cands: Candidates, op: str, queries: DeviceArray,
               out: Optional[DeviceArray] = None) -> DeviceArray:
-        nq = queries.shape[0] if len(queries.shape) == 2 else 1
+        nq = self._query_rows(cands, queries)
         if out is None:
             out = self.empty((nq, cands.n), np.float32)
         call("manta_rocm_score", self.handle, cands.handle, C.c_int(_lib.OPS[op]), queries.ptr,
@@ -189,7 +200,7 @@ class Runtime:
     def score_topk(self, cands: Candidates, op: str, queries: DeviceArray, k: int,
                    smallest: bool = False, with_scores: bool = True, with_acc: bool = False,
                    out=None):
-        nq = queries.shape[0] if len(queries.shape) == 2 else 1
+        nq = self._query_rows(cands, queries)
         if out is None:
             ids = self.empty((nq, k), np.int32)
             sc = self.empty((nq, k), np.float32) if with_scores else None

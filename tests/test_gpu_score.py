@@ -241,6 +241,27 @@ def test_multi_query_topk_bit_exact(rt, op, smallest, nq, n, d, k):
     cands.close()
 
 
+@pytest.mark.parametrize("op,smallest", [("dot", False), ("cosine", False), ("l2_distance", True),
+                                         ("cosine", True), ("l2_distance", False)])
+def test_multi_query_zero_rows_partial_group(rt, op, smallest):
+    """All-zero rows (cosine's zero denominator) among normal ones, with a
+    query count that leaves most of the last query group empty: the empty
+    slots never append keys, and zero rows score like the oracle's."""
+    nq, n, d, k = 19, 6000, 128, 40
+    q, codes, scales = _q8_case(91, nq, n, d, sets=1, normalize=(op != "l2_distance"))
+    codes, scales = codes[0].copy(), scales[0].copy()
+    zero = np.arange(0, n, 7)
+    codes[zero] = 0
+    scales[zero[::2]] = 0.0
+    cands = rt.bind_q8(codes, scales)
+    ids, sc, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    want_s = orc.score_q8(op, q, codes, scales)
+    want_ids = orc.topk(want_s, k, smallest=smallest)
+    np.testing.assert_array_equal(ids.download(), want_ids)
+    np.testing.assert_array_equal(sc.download(), np.take_along_axis(want_s, want_ids, 1))
+    cands.close()
+
+
 def test_multi_query_repeated_calls_are_identical(rt):
     """Thresholds and tickets are reset between calls: a second call with a
     smaller input reproduces the oracle too."""
