@@ -132,6 +132,12 @@ int manta_rocm_stats(const MantaRocm* rt, MantaRocmStats* out);
 int manta_rocm_set_timing(MantaRocm* rt, int on, char** err);
 int manta_rocm_timing(MantaRocm* rt, const char* name, uint64_t* count, double* total_ms, int reset,
                       char** err);
+/* Span timing: end = 0 records a start event on the runtime's stream, end = 1
+ * a stop event; the second call waits for it and reports the milliseconds
+ * between the two.  Times a run of launches with nothing recorded between
+ * them (per-launch events add microseconds to short launches).  No
+ * counterpart in the reference; a measurement aid beside manta_rocm_timing. */
+int manta_rocm_span(MantaRocm* rt, int end, double* elapsed_ms, char** err);
 
 /* ---- packing and candidate binding ------------------------------------ */
 

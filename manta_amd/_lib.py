@@ -54,6 +54,7 @@ SIGNATURES = {
         C.c_int,
         [_p, C.c_char_p, C.POINTER(C.c_uint64), C.POINTER(C.c_double), C.c_int, _err],
     ),
+    "manta_rocm_span": (C.c_int, [_p, C.c_int, C.POINTER(C.c_double), _err]),
     "manta_rocm_pack_q8_rows": (C.c_int, [_p, _i64, _i64, _p, _p, _err]),
     "manta_rocm_pack_q4_blocks": (C.c_int, [_p, _i64, _i64, _p, _p, _err]),
     "manta_rocm_bind_q8_rows": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, C.POINTER(_p), _err]),

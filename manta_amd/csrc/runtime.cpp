@@ -52,6 +52,8 @@ struct MantaRocm {
     std::vector<TimedLaunch> pending;
     std::vector<hipEvent_t> event_pool;
     std::map<std::string, std::pair<uint64_t, double>> totals;
+    // span timing (manta_rocm_span): events around a run of launches
+    hipEvent_t span_ev[2] = {nullptr, nullptr};
 };
 
 struct MantaRocmCandidates {
@@ -320,6 +322,8 @@ void manta_rocm_destroy(MantaRocm* rt) {
         (void)hipEventDestroy(t.stop);
     }
     for (auto e : rt->event_pool) (void)hipEventDestroy(e);
+    for (auto e : rt->span_ev)
+        if (e) (void)hipEventDestroy(e);
     if (rt->ws) (void)hipFree(rt->ws);
     if (rt->err_word) (void)hipFree(rt->err_word);
     if (rt->tickets) (void)hipFree(rt->tickets);
@@ -408,6 +412,20 @@ int manta_rocm_timing(MantaRocm* rt, const char* name, uint64_t* count, double* 
     if (count) *count = c;
     if (total_ms) *total_ms = ms;
     if (reset) rt->totals.clear();
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_span(MantaRocm* rt, int end, double* elapsed_ms, char** err) {
+    RT_CHECK(rt);
+    const int i = end ? 1 : 0;
+    if (!rt->span_ev[i]) HIP_TRY(hipEventCreate(&rt->span_ev[i]), "hipEventCreate");
+    HIP_TRY(hipEventRecord(rt->span_ev[i], rt->stream), "hipEventRecord");
+    if (!end) return MANTA_ROCM_OK;
+    if (!rt->span_ev[0]) return fail(err, MANTA_ROCM_ERROR, "span: no start mark");
+    HIP_TRY(hipEventSynchronize(rt->span_ev[1]), "hipEventSynchronize");
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, rt->span_ev[0], rt->span_ev[1]), "hipEventElapsedTime");
+    if (elapsed_ms) *elapsed_ms = ms;
     return MANTA_ROCM_OK;
 }
 

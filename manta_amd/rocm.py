@@ -138,6 +138,13 @@ class Runtime:
              C.byref(ms), C.c_int(1 if reset else 0))
         return cnt.value, ms.value
 
+    def span(self, end: bool) -> float:
+        """Start (end=False) or stop (end=True) a span timer on the runtime's
+        stream; stopping waits and returns the span's device milliseconds."""
+        ms = C.c_double()
+        call("manta_rocm_span", self.handle, C.c_int(1 if end else 0), C.byref(ms))
+        return ms.value
+
     def stats(self) -> dict:
         s = _lib.Stats()
         load().manta_rocm_stats(self.handle, C.byref(s))
