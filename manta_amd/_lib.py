@@ -20,7 +20,8 @@ PROJ_F16, PROJ_Q8_COL = 0, 1
 
 OPS = {"dot": DOT, "cosine": COSINE, "l2_distance": L2_DISTANCE}
 
-# Every exported symbol of include/manta_rocm.h: name -> (restype, argtypes).
+# Every exported symbol of include/manta_rocm.h and include/manta_mll.h:
+# name -> (restype, argtypes).
 _p = C.c_void_p
 _i64 = C.c_int64
 _err = C.POINTER(C.c_char_p)
@@ -55,6 +56,26 @@ SIGNATURES = {
         [_p, C.c_char_p, C.POINTER(C.c_uint64), C.POINTER(C.c_double), C.c_int, _err],
     ),
     "manta_rocm_span": (C.c_int, [_p, C.c_int, C.POINTER(C.c_double), _err]),
+    # include/manta_mll.h (host only)
+    "manta_mll_open": (C.c_int, [_p, C.c_size_t, C.c_int, C.POINTER(_p), _err]),
+    "manta_mll_close": (None, [_p]),
+    "manta_mll_format_word": (C.c_uint32, [_p]),
+    "manta_mll_section_count": (C.c_int, [_p]),
+    "manta_mll_section_info": (
+        C.c_int,
+        [_p, C.c_int, C.c_char_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint32), _p, _err],
+    ),
+    "manta_mll_section": (C.c_int, [_p, C.c_char_p, C.POINTER(_p), C.POINTER(C.c_uint64), _err]),
+    "manta_mll_string_count": (C.c_int, [_p]),
+    "manta_mll_string": (C.c_char_p, [_p, C.c_uint32]),
+    "manta_mll_head": (
+        C.c_int, [_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_int), _err]),
+    "manta_mll_head_entry": (
+        C.c_int,
+        [_p, C.c_int, C.POINTER(C.c_uint32), C.POINTER(C.c_int), C.POINTER(C.c_int64), C.POINTER(C.c_double),
+         C.POINTER(C.c_uint32), _err],
+    ),
+    "manta_mll_blake3": (None, [_p, C.c_size_t, _p]),
     "manta_rocm_pack_q8_rows": (C.c_int, [_p, _i64, _i64, _p, _p, _err]),
     "manta_rocm_pack_q4_blocks": (C.c_int, [_p, _i64, _i64, _p, _p, _err]),
     "manta_rocm_bind_q8_rows": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, C.POINTER(_p), _err]),

@@ -1,6 +1,7 @@
 """The C-ABI library loads on a CPU-only host and exports every entry point
-include/manta_rocm.h declares (no compute calls without a GPU)."""
+include/*.h declares (no compute calls without a GPU)."""
 import ctypes as C
+import glob
 import os
 import re
 
@@ -9,19 +10,22 @@ import pytest
 from manta_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "manta_rocm.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def declared_symbols():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(manta_rocm_\w+)\s*\(", text)))
+    syms = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        syms |= set(re.findall(r"\b(manta_(?:rocm|mll)_\w+)\s*\(", text))
+    return sorted(syms)
 
 
 def test_header_declares_entry_points():
     syms = declared_symbols()
     assert "manta_rocm_score_topk" in syms and "manta_rocm_embed_pooled" in syms
-    assert len(syms) >= 25
+    assert "manta_mll_open" in syms and "manta_mll_blake3" in syms
+    assert len(syms) >= 35
 
 
 def test_library_exports_every_declared_symbol():
