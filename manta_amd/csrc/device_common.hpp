@@ -40,6 +40,20 @@ __device__ __forceinline__ float round_half_away(float x) {
     return t;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active): DPP
+// row shifts by 1, 2, 4 and 8 sum within each 16-lane row, then lane 15's
+// total is added to rows 1 and 3 and lane 31's to rows 2 and 3.  Lanes whose
+// shift source lies outside their row add 0.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+    return x;
+}
+
 __device__ __forceinline__ float fmul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float fadd_rn(float a, float b) { return __fadd_rn(a, b); }
 __device__ __forceinline__ float fsub_rn(float a, float b) { return __fsub_rn(a, b); }
@@ -198,12 +212,7 @@ __device__ inline void topk_compact(uint64_t* keys, TopKShared* st, int k) {
                 h[j] = ss.hist[255 - 4 * tid - j];
                 sum += h[j];
             }
-            int incl = sum;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                int t = __shfl_up(incl, off);
-                if (tid >= off) incl += t;
-            }
+            const int incl = wave_incl_scan(sum);
             int cum = incl - sum;  // keys with a larger digit
 #pragma unroll
             for (int j = 0; j < 4; j++) {

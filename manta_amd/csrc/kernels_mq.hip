@@ -418,12 +418,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
         const int w = base + tid;
         int c = w < a.R ? a.counts[(int64_t)w * a.nq + q] : 0;
         c = c < a.rc ? c : a.rc;
-        int incl = c;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int t = __shfl_up(incl, off);
-            if (lane >= off) incl += t;
-        }
+        const int incl = wave_incl_scan(c);
         if (lane == 63) wsum[wave] = incl;
         __syncthreads();
         int before = carry;

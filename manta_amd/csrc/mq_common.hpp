@@ -124,12 +124,7 @@ __device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, Ra
                 hist[255 - 4 * tid - j] = 0;  // ready for the round after next
                 sum += h[j];
             }
-            int incl = sum;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int t = __shfl_up(incl, off);
-                if (tid >= off) incl += t;
-            }
+            const int incl = wave_incl_scan(sum);
             int cum = incl - sum;  // keys with a larger digit
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -156,12 +151,7 @@ __device__ inline void block_radix_prefix(const uint64_t* keys, int c, int k, Ra
 // `counter`: a wave prefix sum and one LDS atomic per wave.
 __device__ __forceinline__ int wave_append(int cnt, int* counter) {
     const int lane = threadIdx.x & 63;
-    int incl = cnt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off);
-        if (lane >= off) incl += t;
-    }
+    const int incl = wave_incl_scan(cnt);
     int base = 0;
     if (lane == 63 && incl) base = atomicAdd(counter, incl);
     base = __shfl(base, 63);
