@@ -200,6 +200,35 @@ int manta_rocm_pack_candidates(MantaRocm* rt, const MantaRocmCandidates* cands, 
                                int64_t nq, int64_t k, const int64_t* candidate_ids_dev, int64_t* out_ids_dev,
                                void* out_rows_dev, void* out_scales_dev, char** err);
 
+/* ---- encoder forward (examples/encoder_trainable_q8.manta) -------------- */
+
+/* The weights of the one-layer encoder: q8 token rows ([vocab, d] int8 with
+ * an f32 scale per row) and six q8 matrices with an f32 scale per output
+ * column -- attn_q, attn_k, attn_v, attn_o [d, d], ffn_up [d, h],
+ * projection [h, d].  Device pointers. */
+typedef struct MantaRocmEncoderWeights {
+    const int8_t* token_codes;
+    const float* token_scales;
+    const int8_t* codes[6];       /* attn_q, attn_k, attn_v, attn_o, ffn_up, projection */
+    const float* col_scales[6];
+} MantaRocmEncoderWeights;
+
+/* embed_pooled_batch of examples/encoder_trainable_q8.manta:37-60 on the
+ * device: gather + dequant, q/k/v projections, scores = q @ transpose(k)
+ * per sequence (no scaling, every position attended, as the program
+ * states), softmax, @ v, @ attn_o, layernorm(attended + hidden), ffn_up,
+ * gelu, projection, layernorm(projected + attn_hidden), normalize, masked
+ * mean pool; f16 out [b, d].  The steps are the reference's
+ * gatherTensor / matmulTensor / transposeTensor / softmaxRows /
+ * layerNormRows / geluTensor / normalizeRows / meanPoolMaskedTensor
+ * (tensor_ops.go:751-1344), in f32.  Token ids out of range are reported by
+ * the next synchronizing call, as manta_rocm_embed_pooled.  Replaces the
+ * host execution of these steps (the CUDA backend offers only matmul and
+ * normalize, cuda.go:270-299). */
+int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens_dev, const int32_t* mask_dev, int64_t b,
+                              int64_t t, const MantaRocmEncoderWeights* w, int64_t vocab, int64_t d, int64_t h,
+                              uint16_t* out_dev, char** err);
+
 /* top-k over an f32 score matrix [rows, cols] (rows == 1 is the rank-1
  * form).  Replaces topKTensor (tensor_ops.go:1523-1592). */
 int manta_rocm_topk(MantaRocm* rt, const float* scores_dev, int64_t rows, int64_t cols, int64_t k,

@@ -37,6 +37,16 @@ class Stats(C.Structure):
     ]
 
 
+class EncoderWeights(C.Structure):
+    """MantaRocmEncoderWeights: device pointers of the encoder's q8 weights."""
+    _fields_ = [
+        ("token_codes", C.c_void_p),
+        ("token_scales", C.c_void_p),
+        ("codes", C.c_void_p * 6),
+        ("col_scales", C.c_void_p * 6),
+    ]
+
+
 SIGNATURES = {
     "manta_rocm_abi_version": (C.c_int, []),
     "manta_rocm_device_count": (C.c_int, [C.POINTER(C.c_int), _err]),
@@ -56,6 +66,8 @@ SIGNATURES = {
         [_p, C.c_char_p, C.POINTER(C.c_uint64), C.POINTER(C.c_double), C.c_int, _err],
     ),
     "manta_rocm_span": (C.c_int, [_p, C.c_int, C.POINTER(C.c_double), _err]),
+    "manta_rocm_encoder_pooled": (
+        C.c_int, [_p, _p, _p, _i64, _i64, C.POINTER(EncoderWeights), _i64, _i64, _i64, _p, _err]),
     # include/manta_mll.h (host only)
     "manta_mll_open": (C.c_int, [_p, C.c_size_t, C.c_int, C.POINTER(_p), _err]),
     "manta_mll_close": (None, [_p]),

@@ -1,0 +1,235 @@
+// kernels_encoder.hip -- device steps of the encoder pipeline (gather of q8
+// token rows, f32 GEMMs with fused q8 column dequant, row softmax, residual
+// add + layernorm, gelu), composed by manta_rocm_encoder_pooled.
+//
+// All arithmetic is f32 (f64 where the reference uses it: the softmax sum
+// and exponentials, the layernorm's reciprocal square root, gelu's tanh).
+// Reductions run in tree order, so results match the reference's
+// sequential loops within rounding, not bit for bit.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace manta {
+
+namespace {
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+}  // namespace
+
+// X[i][c] = codes[tok[i]][c] * scale[tok[i]] (f32); an id out of range is
+// recorded in err (flag | id) and its row is zero.
+__global__ __launch_bounds__(256) void enc_gather_q8_kernel(const int32_t* __restrict__ tok, int64_t rows,
+                                                            const int8_t* __restrict__ codes,
+                                                            const float* __restrict__ scales, int64_t vocab, int d,
+                                                            float* __restrict__ x, unsigned long long* err) {
+    const int64_t total = rows * d;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / d;
+        const int c = (int)(i - r * d);
+        const int id = tok[r];
+        const bool ok = id >= 0 && (int64_t)id < vocab;
+        if (!ok && c == 0 && err) atomicCAS(err, 0ull, (1ull << 32) | (unsigned long long)(uint32_t)id);
+        x[i] = ok ? fmul_rn((float)codes[(int64_t)id * d + c], scales[id]) : 0.0f;
+    }
+}
+
+// C[b] = A[b] (M x K, row-major, batch stride sA) times B:
+//   BMODE 0: B[b] f32 [K][N] row-major (batch stride sB)
+//   BMODE 1: int8 [K][N] with an f32 scale per column (shared), dequantized
+//            as code * scale
+//   BMODE 2: the transpose of Bm[b], an f32 [N][K] row-major matrix
+// 64 x 64 output tile per workgroup, 4 x 4 per thread, K in steps of 16
+// through LDS; grid = (tiles of N, tiles of M, batches).
+template <int BMODE>
+__global__ __launch_bounds__(256) void enc_gemm_kernel(const float* __restrict__ A, int64_t sA,
+                                                       const void* __restrict__ Bv, const float* __restrict__ bscale,
+                                                       int64_t sB, float* __restrict__ C, int64_t sC, int M, int N,
+                                                       int K) {
+    __shared__ float As[16][64 + 4];
+    __shared__ float Bs[16][64 + 4];
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int64_t bt = blockIdx.z;
+    const float* a = A + bt * sA;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < K; k0 += 16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i;
+            const int m = e >> 4, kk = e & 15;
+            const int gm = m0 + m, gk = k0 + kk;
+            As[kk][m] = (gm < M && gk < K) ? a[(int64_t)gm * K + gk] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i;
+            float v = 0.0f;
+            if (BMODE == 2) {
+                const int n = e >> 4, kk = e & 15;
+                const int gn = n0 + n, gk = k0 + kk;
+                if (gn < N && gk < K) v = ((const float*)Bv)[bt * sB + (int64_t)gn * K + gk];
+                Bs[kk][n] = v;
+            } else {
+                const int kk = e >> 6, n = e & 63;
+                const int gn = n0 + n, gk = k0 + kk;
+                if (gn < N && gk < K) {
+                    if (BMODE == 0) v = ((const float*)Bv)[bt * sB + (int64_t)gk * N + gn];
+                    else v = fmul_rn((float)((const int8_t*)Bv)[(int64_t)gk * N + gn], bscale[gn]);
+                }
+                Bs[kk][n] = v;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++) {
+            const float4 av = *(const float4*)&As[kk][ty * 4];
+            const float4 bv = *(const float4*)&Bs[kk][tx * 4];
+            const float ar[4] = {av.x, av.y, av.z, av.w};
+            const float br[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __fmaf_rn(ar[i], br[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+    float* c = C + bt * sC;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int gm = m0 + ty * 4 + i;
+        if (gm >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int gn = n0 + tx * 4 + j;
+            if (gn < N) c[(int64_t)gm * N + gn] = acc[i][j];
+        }
+    }
+}
+
+// Row softmax in place (softmaxRows): one wave per row.
+__global__ __launch_bounds__(256) void enc_softmax_rows_kernel(float* __restrict__ x, int64_t rows, int cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    float* row = x + r * cols;
+    float m = -__builtin_inff();
+    for (int c = lane; c < cols; c += 64) m = fmaxf(m, row[c]);
+    m = wave_max_f32(m);
+    double s = 0.0;
+    for (int c = lane; c < cols; c += 64) {
+        const double ev = exp((double)fsub_rn(row[c], m));
+        row[c] = (float)ev;
+        s += ev;
+    }
+    s = wave_sum_f64(s);
+    if (s == 0.0) return;
+    const float inv = (float)(1.0 / s);
+    for (int c = lane; c < cols; c += 64) row[c] = fmul_rn(row[c], inv);
+}
+
+// y = layernorm(a + b) per row (binary_add then layerNormRows): one wave per
+// row; f32 mean and variance, f64 reciprocal square root of variance + 1e-5.
+__global__ __launch_bounds__(256) void enc_add_layernorm_kernel(const float* __restrict__ a,
+                                                                const float* __restrict__ b, float* __restrict__ y,
+                                                                int64_t rows, int cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* ar = a + r * cols;
+    const float* br = b + r * cols;
+    float* yr = y + r * cols;
+    float s = 0.0f;
+    for (int c = lane; c < cols; c += 64) s = fadd_rn(s, fadd_rn(ar[c], br[c]));
+    const float mean = fdiv_rn(wave_sum_f32(s), (float)cols);
+    float v = 0.0f;
+    for (int c = lane; c < cols; c += 64) {
+        const float d = fsub_rn(fadd_rn(ar[c], br[c]), mean);
+        v = __fmaf_rn(d, d, v);
+    }
+    const float var = fdiv_rn(wave_sum_f32(v), (float)cols);
+    const float inv = (float)(1.0 / sqrt((double)var + 1e-5));
+    for (int c = lane; c < cols; c += 64) yr[c] = fmul_rn(fsub_rn(fadd_rn(ar[c], br[c]), mean), inv);
+}
+
+// geluTensor in place: 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))),
+// f32 with the tanh in f64.
+__global__ __launch_bounds__(256) void enc_gelu_kernel(float* __restrict__ x, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const float v = x[i];
+        const float cubic = fmul_rn(fmul_rn(v, v), v);
+        const float inner = fmul_rn(0.7978845608f, fadd_rn(v, fmul_rn(0.044715f, cubic)));
+        x[i] = fmul_rn(fmul_rn(0.5f, v), fadd_rn(1.0f, (float)tanh((double)inner)));
+    }
+}
+
+__global__ __launch_bounds__(256) void enc_to_f16_kernel(const float* __restrict__ x, int64_t n,
+                                                         uint16_t* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        out[i] = f2h(x[i]);
+}
+
+static unsigned grid_for(int64_t n) {
+    const int64_t g = (n + 255) / 256;
+    return (unsigned)(g < 65536 ? (g < 1 ? 1 : g) : 65536);
+}
+
+hipError_t launch_enc_gather_q8(const int32_t* tok, int64_t rows, const int8_t* codes, const float* scales,
+                                int64_t vocab, int d, float* x, unsigned long long* err, hipStream_t s) {
+    hipLaunchKernelGGL(enc_gather_q8_kernel, dim3(grid_for(rows * d)), dim3(256), 0, s, tok, rows, codes, scales,
+                       vocab, d, x, err);
+    return hipGetLastError();
+}
+
+hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B, const float* bscale, int64_t sB,
+                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s) {
+    if (M <= 0 || N <= 0 || K <= 0 || batches <= 0 || batches > 65535 || (M + 63) / 64 > 65535)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)batches);
+    if (bmode == 0)
+        hipLaunchKernelGGL(enc_gemm_kernel<0>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
+    else if (bmode == 1)
+        hipLaunchKernelGGL(enc_gemm_kernel<1>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
+    else
+        hipLaunchKernelGGL(enc_gemm_kernel<2>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_enc_softmax_rows(float* x, int64_t rows, int cols, hipStream_t s) {
+    hipLaunchKernelGGL(enc_softmax_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_enc_add_layernorm(const float* a, const float* b, float* y, int64_t rows, int cols,
+                                    hipStream_t s) {
+    hipLaunchKernelGGL(enc_add_layernorm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a, b, y, rows,
+                       cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_enc_gelu(float* x, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(enc_gelu_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_enc_to_f16(const float* x, int64_t n, uint16_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(enc_to_f16_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, n, out);
+    return hipGetLastError();
+}
+
+}  // namespace manta

@@ -1200,6 +1200,62 @@ int manta_rocm_normalize_rows(MantaRocm* rt, float* x, int64_t rows, int64_t col
     return MANTA_ROCM_OK;
 }
 
+int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t* mask, int64_t b, int64_t t,
+                              const MantaRocmEncoderWeights* w, int64_t vocab, int64_t d, int64_t h,
+                              uint16_t* out, char** err) {
+    RT_CHECK(rt);
+    if (!tokens || !mask || !w || !out) return fail(err, MANTA_ROCM_ERROR, "nil encoder input");
+    if (!w->token_codes || !w->token_scales) return fail(err, MANTA_ROCM_ERROR, "nil encoder token table");
+    for (int i = 0; i < 6; i++)
+        if (!w->codes[i] || !w->col_scales[i]) return fail(err, MANTA_ROCM_ERROR, "nil encoder weight %d", i);
+    if (b <= 0 || t <= 0 || vocab <= 0 || d <= 0 || h <= 0)
+        return fail(err, MANTA_ROCM_ERROR, "encoder: bad shape b=%lld t=%lld vocab=%lld d=%lld h=%lld",
+                    (long long)b, (long long)t, (long long)vocab, (long long)d, (long long)h);
+    const int64_t rows = b * t;
+    if (b > 65535 || rows > 0x7FFFFFFF || d > 0x7FFFFFFF || h > 0x7FFFFFFF || t > 0x7FFFFFFF)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "encoder: shape too large");
+    // x, q, k, v, mixed [rows, d]; scores [b, t, t]; ffn [rows, h]; pooled [b, d]
+    const size_t rd = (size_t)rows * (size_t)d;
+    const size_t need = 5 * (rd * 4 + 256) + (size_t)b * t * t * 4 + 256 + (size_t)rows * h * 4 + 256 +
+                        (size_t)b * d * 4 + 256;
+    int rc = ensure_workspace(rt, need, err);
+    if (rc) return rc;
+    Carver cv(rt->ws);
+    float* x = cv.take<float>(rd);
+    float* q = cv.take<float>(rd);
+    float* k = cv.take<float>(rd);
+    float* v = cv.take<float>(rd);
+    float* mx = cv.take<float>(rd);
+    float* sc = cv.take<float>((size_t)b * t * t);
+    float* ffn = cv.take<float>((size_t)rows * h);
+    float* pooled = cv.take<float>((size_t)b * d);
+    const int R = (int)rows, D = (int)d, H = (int)h, T = (int)t;
+    const int64_t td = (int64_t)t * d, tt = (int64_t)t * t;
+    hipStream_t s = rt->stream;
+    LAUNCH_TRY(manta::launch_enc_gather_q8(tokens, rows, w->token_codes, w->token_scales, vocab, D, x, rt->err_word, s),
+               "encoder_gather");
+    rt->gather_pending = true;
+    LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[0], w->col_scales[0], 0, q, 0, R, D, D, 1, s), "encoder_gemm");
+    LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[1], w->col_scales[1], 0, k, 0, R, D, D, 1, s), "encoder_gemm");
+    LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[2], w->col_scales[2], 0, v, 0, R, D, D, 1, s), "encoder_gemm");
+    // scores[b] = q[b] @ transpose(k[b]); softmax over each row of t
+    LAUNCH_TRY(manta::launch_enc_gemm(2, q, td, k, nullptr, td, sc, tt, T, T, D, (int)b, s), "encoder_attention");
+    LAUNCH_TRY(manta::launch_enc_softmax_rows(sc, rows, T, s), "encoder_softmax");
+    LAUNCH_TRY(manta::launch_enc_gemm(0, sc, tt, v, nullptr, td, mx, td, T, D, T, (int)b, s), "encoder_attention");
+    // attended = mixed @ attn_o (into q); attn_hidden = layernorm(attended + x) (into k)
+    LAUNCH_TRY(manta::launch_enc_gemm(1, mx, 0, w->codes[3], w->col_scales[3], 0, q, 0, R, D, D, 1, s), "encoder_gemm");
+    LAUNCH_TRY(manta::launch_enc_add_layernorm(q, x, k, rows, D, s), "encoder_layernorm");
+    LAUNCH_TRY(manta::launch_enc_gemm(1, k, 0, w->codes[4], w->col_scales[4], 0, ffn, 0, R, H, D, 1, s), "encoder_gemm");
+    LAUNCH_TRY(manta::launch_enc_gelu(ffn, rows * h, s), "encoder_gelu");
+    // projected = gelu @ projection (into v); encoded = layernorm(projected + attn_hidden) (into mx)
+    LAUNCH_TRY(manta::launch_enc_gemm(1, ffn, 0, w->codes[5], w->col_scales[5], 0, v, 0, R, D, H, 1, s), "encoder_gemm");
+    LAUNCH_TRY(manta::launch_enc_add_layernorm(v, k, mx, rows, D, s), "encoder_layernorm");
+    LAUNCH_TRY(manta::launch_normalize_rows(mx, rows, d, s), "normalize");
+    LAUNCH_TRY(manta::launch_mean_pool_masked(mx, mask, b, t, d, pooled, s), "mean_pool");
+    LAUNCH_TRY(manta::launch_enc_to_f16(pooled, b * d, out, s), "encoder_out");
+    return MANTA_ROCM_OK;
+}
+
 int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t* mask, int64_t b,
                             int64_t t, const uint16_t* table, int64_t vocab, int64_t d, const void* proj,
                             int proj_kind, const float* col_scale, int64_t e, uint16_t* out, char** err) {

@@ -292,6 +292,32 @@ class Runtime:
         return out
 
 
+    # ------------------------------------------------------------ encoder
+    def encoder_pooled(self, tokens: DeviceArray, mask: DeviceArray, token_codes: DeviceArray,
+                       token_scales: DeviceArray, weights, out: Optional[DeviceArray] = None) -> DeviceArray:
+        """The one-layer encoder's embed_pooled_batch: f16 [b, d].  weights:
+        six (int8 [k, n] codes, f32 [n] column scales) device pairs in the
+        order attn_q, attn_k, attn_v, attn_o, ffn_up, projection."""
+        b, t = tokens.shape
+        vocab, d = token_codes.shape
+        if len(weights) != 6:
+            raise ValueError("encoder weights: six (codes, scales) pairs")
+        h = weights[4][0].shape[1]
+        shapes = [(d, d), (d, d), (d, d), (d, d), (d, h), (h, d)]
+        for (codes, scales), want in zip(weights, shapes):
+            if tuple(codes.shape) != want or tuple(scales.shape) != (want[1],):
+                raise ValueError("encoder weight shape %s / %s, want %s" % (codes.shape, scales.shape, want))
+        w = _lib.EncoderWeights()
+        w.token_codes, w.token_scales = token_codes.addr, token_scales.addr
+        for i, (codes, scales) in enumerate(weights):
+            w.codes[i], w.col_scales[i] = codes.addr, scales.addr
+        if out is None:
+            out = self.empty((b, d), np.uint16)
+        call("manta_rocm_encoder_pooled", self.handle, tokens.ptr, mask.ptr, C.c_int64(b), C.c_int64(t),
+             C.byref(w), C.c_int64(vocab), C.c_int64(d), C.c_int64(h), out.ptr)
+        return out
+
+
 def pack_q8_rows(x: np.ndarray):
     x = np.ascontiguousarray(x, dtype=np.float32)
     n, d = x.shape

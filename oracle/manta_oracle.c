@@ -541,3 +541,114 @@ void orc_score_q4(int op, const uint16_t* queries, int64_t nq,
     }
     free(c16);
 }
+
+/* ------------------------------------------------------ encoder ops */
+
+/* layerNormRows, tensor_ops.go:1140-1168: f32 sequential mean and variance,
+ * invStd = float32(1 / sqrt(float64(variance) + 1e-5)), no affine terms. */
+void orc_layernorm_rows(float* x, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++) {
+        float* row = x + r * cols;
+        float mean = 0.0f;
+        for (int64_t c = 0; c < cols; c++) mean += row[c];
+        mean /= (float)cols;
+        float variance = 0.0f;
+        for (int64_t c = 0; c < cols; c++) {
+            float centered = row[c] - mean;
+            variance += centered * centered;
+        }
+        variance /= (float)cols;
+        float inv_std = (float)(1.0 / sqrt((double)variance + 1e-5));
+        for (int64_t c = 0; c < cols; c++) row[c] = (row[c] - mean) * inv_std;
+    }
+}
+
+/* softmaxRows, tensor_ops.go:1303-1334: f32 max, exp of the f32 difference
+ * in f64, f64 sum, f32 reciprocal of the sum, f32 products; a zero sum
+ * leaves the exponentials. */
+void orc_softmax_rows(float* x, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++) {
+        float* row = x + r * cols;
+        float max_v = row[0];
+        for (int64_t c = 1; c < cols; c++)
+            if (row[c] > max_v) max_v = row[c];
+        double sum = 0.0;
+        for (int64_t c = 0; c < cols; c++) {
+            double ev = exp((double)(row[c] - max_v));
+            row[c] = (float)ev;
+            sum += ev;
+        }
+        if (sum == 0.0) continue;
+        float inv = (float)(1.0 / sum);
+        for (int64_t c = 0; c < cols; c++) row[c] *= inv;
+    }
+}
+
+/* geluTensor, tensor_ops.go:1336-1344: the tanh approximation in f32 with
+ * the tanh in f64. */
+void orc_gelu(float* x, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        float v = x[i];
+        float cubic = v * v * v;
+        float inner = 0.7978845608f * (v + 0.044715f * cubic);
+        x[i] = 0.5f * v * (1.0f + (float)tanh((double)inner));
+    }
+}
+
+/* Batched [B,M,K] x [B,K,N] (matmulTensor rank 3 x rank 3,
+ * tensor_ops.go:1037-1058): the [M,K]x[K,N] loop per batch. */
+static void orc_matmul_batched(const float* lhs, const float* rhs, int64_t b, int64_t m, int64_t k,
+                               int64_t n, float* out) {
+    for (int64_t bi = 0; bi < b; bi++)
+        orc_matmul(lhs + bi * m * k, rhs + bi * k * n, m, k, n, out + bi * m * n);
+}
+
+/* The encoder pipeline of examples/encoder_trainable_q8.manta:37-60
+ * (embed_pooled_batch) over dequantized f32 values: gather, q/k/v
+ * projections, scores = q @ transpose(k), softmax, @ v, @ attn_o, layernorm
+ * of the residual sum, ffn_up, gelu, projection, layernorm of the residual
+ * sum, normalize, masked mean pool.  out [b, d] f32. */
+int orc_encoder_pooled(const int32_t* tokens, const int32_t* mask, int64_t b, int64_t t,
+                       const float* table, int64_t vocab, int64_t d, const float* wq,
+                       const float* wk, const float* wv, const float* wo, const float* wup,
+                       const float* wproj, int64_t h, float* out, char* msg, int msglen) {
+    const int64_t rows = b * t;
+    float* hid = (float*)malloc((size_t)(rows * d) * sizeof(float));
+    float* q = (float*)malloc((size_t)(rows * d) * sizeof(float));
+    float* k = (float*)malloc((size_t)(rows * d) * sizeof(float));
+    float* v = (float*)malloc((size_t)(rows * d) * sizeof(float));
+    float* kt = (float*)malloc((size_t)(rows * d) * sizeof(float));
+    float* s = (float*)malloc((size_t)(b * t * t) * sizeof(float));
+    float* mixed = (float*)malloc((size_t)(rows * d) * sizeof(float));
+    float* att = (float*)malloc((size_t)(rows * d) * sizeof(float));
+    float* f = (float*)malloc((size_t)(rows * h) * sizeof(float));
+    int rc = 1;
+    if (!hid || !q || !k || !v || !kt || !s || !mixed || !att || !f) {
+        if (msg) snprintf(msg, (size_t)msglen, "out of memory");
+        goto done;
+    }
+    if (orc_gather_rows(table, vocab, d, tokens, rows, hid, msg, msglen)) goto done;
+    orc_matmul(hid, wq, rows, d, d, q);
+    orc_matmul(hid, wk, rows, d, d, k);
+    orc_matmul(hid, wv, rows, d, d, v);
+    for (int64_t bi = 0; bi < b; bi++) /* transpose of each [t, d] block */
+        for (int64_t r = 0; r < t; r++)
+            for (int64_t c = 0; c < d; c++) kt[bi * d * t + c * t + r] = k[bi * t * d + r * d + c];
+    orc_matmul_batched(q, kt, b, t, d, t, s);
+    orc_softmax_rows(s, b * t, t);
+    orc_matmul_batched(s, v, b, t, t, d, mixed);
+    orc_matmul(mixed, wo, rows, d, d, att);
+    for (int64_t i = 0; i < rows * d; i++) att[i] = att[i] + hid[i]; /* attended + hidden */
+    orc_layernorm_rows(att, rows, d);                                /* attn_hidden */
+    orc_matmul(att, wup, rows, d, h, f);
+    orc_gelu(f, rows * h);
+    orc_matmul(f, wproj, rows, h, d, q);                             /* projected */
+    for (int64_t i = 0; i < rows * d; i++) q[i] = q[i] + att[i];     /* + attn_hidden */
+    orc_layernorm_rows(q, rows, d);                                  /* encoded */
+    orc_normalize_rows(q, rows, d);
+    orc_mean_pool_masked(q, mask, b, t, d, out);
+    rc = 0;
+done:
+    free(hid); free(q); free(k); free(v); free(kt); free(s); free(mixed); free(att); free(f);
+    return rc;
+}

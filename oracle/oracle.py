@@ -54,6 +54,10 @@ def lib() -> C.CDLL:
             "orc_query_e16": (None, [p, i64, p, p, p, p]),
             "orc_score_q8": (None, [ci, p, i64, p, p, p, p, i64, i64, i64, p, p]),
             "orc_score_q4": (None, [ci, p, i64, p, p, p, p, i64, i64, i64, p]),
+            "orc_layernorm_rows": (None, [p, i64, i64]),
+            "orc_softmax_rows": (None, [p, i64, i64]),
+            "orc_gelu": (None, [p, i64]),
+            "orc_encoder_pooled": (ci, [p, p, i64, i64, p, i64, i64, p, p, p, p, p, p, i64, p, C.c_char_p, ci]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -196,6 +200,43 @@ def embed(tokens, mask, table_f16, proj_f16=None, proj_codes=None, col_scale=Non
     if rc:
         raise OracleError(msg.value.decode())
     return out16, out32
+
+
+# ------------------------------------------------------------ encoder
+def layernorm_rows(x):
+    x = np.array(x, dtype=np.float32, order="C", copy=True)
+    lib().orc_layernorm_rows(_p(x), int(np.prod(x.shape[:-1])), x.shape[-1])
+    return x
+
+
+def softmax_rows(x):
+    x = np.array(x, dtype=np.float32, order="C", copy=True)
+    lib().orc_softmax_rows(_p(x), int(np.prod(x.shape[:-1])), x.shape[-1])
+    return x
+
+
+def gelu(x):
+    x = np.array(x, dtype=np.float32, order="C", copy=True)
+    lib().orc_gelu(_p(x), x.size)
+    return x
+
+
+def encoder_pooled(tokens, mask, table, wq, wk, wv, wo, wup, wproj):
+    """f32 [b, d] of the encoder pipeline over dequantized f32 weights."""
+    tokens = _c(tokens, np.int32)
+    mask = _c(mask, np.int32)
+    table = _c(table, np.float32)
+    ws = [_c(w, np.float32) for w in (wq, wk, wv, wo, wup, wproj)]
+    b, t = tokens.shape
+    vocab, d = table.shape
+    h = ws[4].shape[1]
+    out = np.empty((b, d), np.float32)
+    msg = C.create_string_buffer(256)
+    rc = lib().orc_encoder_pooled(_p(tokens), _p(mask), b, t, _p(table), vocab, d, *[_p(w) for w in ws], h,
+                                  _p(out), msg, 256)
+    if rc:
+        raise OracleError(msg.value.decode())
+    return out
 
 
 # ------------------------------------------------ packed scoring contract
