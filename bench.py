@@ -96,6 +96,7 @@ def copy_calibration(mib: int) -> int:
 HBM_PEAK = 8000.0          # GB/s
 F16_PEAK = 2517.0          # dense f16 MFMA TFLOP/s
 I8_PEAK = 5033.0           # dense i8 MFMA TOP/s
+F32_PEAK = 157.3           # dense f32 MFMA TFLOP/s
 
 
 def _timed(rt, fn, steps, warmup, families, min_warm_s=0.5):
@@ -308,6 +309,42 @@ def run_c4(rt, steps, warmup) -> dict:
     }
 
 
+def run_enc(rt, steps, warmup) -> dict:
+    """The encoder forward of examples/encoder_trainable_q8.manta
+    (embed_pooled_batch) at C4's embed shape: 1024 sequences of 64 tokens,
+    vocabulary 32000, d = 384, ffn width h = 1536; random q8 weights."""
+    rng = np.random.default_rng(5)
+    b, t, vocab, d, h = 1024, 64, 32000, 384, 1536
+    tokens = rng.integers(0, vocab, size=(b, t), dtype=np.int32)
+    mask = np.ones((b, t), np.int32)
+    tcodes = rng.integers(-127, 128, size=(vocab, d), dtype=np.int8)
+    tscales = np.full(vocab, 0.5 / 127.0, np.float32)
+    dev = []
+    for k, n in [(d, d), (d, d), (d, d), (d, d), (d, h), (h, d)]:
+        dev.append((rt.to_device(rng.integers(-127, 128, size=(k, n), dtype=np.int8)),
+                    rt.to_device(np.full(n, 1.0 / (127.0 * np.sqrt(k)), np.float32))))
+    td, md, tcd, tsd = (rt.to_device(x) for x in (tokens, mask, tcodes, tscales))
+    out = rt.empty((b, d), np.uint16)
+    fams = ["encoder_gather", "encoder_gemm", "encoder_attention", "encoder_softmax", "encoder_layernorm",
+            "encoder_gelu", "normalize", "mean_pool", "encoder_out"]
+    step_s, fam, dev_ms = _timed(rt, lambda: rt.encoder_pooled(td, md, tcd, tsd, dev, out=out), steps, warmup, fams)
+    r = b * t
+    gemm_flops = 2.0 * r * d * d * 4 + 2.0 * r * d * h * 2
+    attn_flops = 2.0 * 2.0 * b * t * t * d
+    gemm_us = fam["encoder_gemm"][2] * 1000.0
+    return {
+        "workload": "enc_encoder_trainable_q8_pooled", "shape": {"b": b, "t": t, "vocab": vocab, "d": d, "h": h},
+        "value": r / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0, "device_ms_per_step": dev_ms,
+        "kernels": _kernels(fam),
+        "roofline": {"bound": "mfma", "kernel": "enc_gemm_kernel (f32, 64x64 tiles, VALU FMA; q/k/v/o, ffn_up, "
+                                                "projection)",
+                     "achieved": gemm_flops / (gemm_us * 1e-6) / 1e12, "peak": F32_PEAK, "unit": "TFLOP/s",
+                     "frac": gemm_flops / (gemm_us * 1e-6) / 1e12 / F32_PEAK, "gemm_us_per_step": gemm_us,
+                     "flops_per_step": gemm_flops, "attention_flops_per_step": attn_flops,
+                     "note": "f32 throughout; priced at the f32 MFMA peak, which this VALU kernel does not use"},
+    }
+
+
 def run_c0(rt, args) -> dict:
     from manta_amd import synth
 
@@ -387,7 +424,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sets", type=int, default=32, help="C0 problems per step")
-    ap.add_argument("--workload", default="c0", choices=["c0", "c1", "c2", "c3", "c4", "all"],
+    ap.add_argument("--workload", default="c0", choices=["c0", "c1", "c2", "c3", "c4", "enc", "all"],
                     help="c0 is the headline line; the others (or all) are added under 'configs'")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -405,7 +442,7 @@ def main() -> int:
     from manta_amd import rocm
 
     rt = rocm.Runtime(0)
-    extra = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4}
+    extra = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "enc": run_enc}
     todo = list(extra) if args.workload == "all" else ([args.workload] if args.workload in extra else [])
     heavy_steps = max(3, min(args.steps, 10))
     configs = {}
