@@ -14,6 +14,8 @@
 // sums the masked rows of its tile per column and writes one partial per
 // (sequence, row tile); a finalize kernel adds the partials in a fixed
 // order, divides by the count and L2-normalizes.
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -1197,7 +1199,50 @@ hipError_t launch_mean_pool_masked(const float* x, const int32_t* mask, int64_t 
     return hipGetLastError();
 }
 
+// normalizeRows with coalesced traffic: a workgroup stages rb rows in LDS
+// (row pitch cols + 1 words, so the summing threads hit distinct banks), one
+// thread per row sums the squares sequentially in f64 in column order -- the
+// same operations in the same order as normalize_rows_kernel -- and all
+// threads divide and write back.
+__global__ __launch_bounds__(256) void normalize_rows_lds_kernel(float* __restrict__ x, int64_t rows, int cols,
+                                                                 int rb) {
+    extern __shared__ float L[];  // [rb][cols + 1], then rb norms
+    const int pitch = cols + 1;
+    float* norms = L + (int64_t)rb * pitch;
+    const int64_t r0 = (int64_t)blockIdx.x * rb;
+    const int nr = (int)(rows - r0 < rb ? rows - r0 : rb);
+    const int n = nr * cols;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const int r = i / cols, c = i - r * cols;
+        L[r * pitch + c] = x[(r0 + r) * cols + c];
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nr) {
+        const float* p = L + threadIdx.x * pitch;
+        double s = 0.0;
+        for (int c = 0; c < cols; c++) {
+            const double v = (double)p[c];
+            s = __dadd_rn(s, __dmul_rn(v, v));
+        }
+        norms[threadIdx.x] = (float)__builtin_sqrt(s);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const int r = i / cols, c = i - r * cols;
+        const float norm = norms[r];
+        if (norm != 0.0f) x[(r0 + r) * cols + c] = fdiv_rn(L[r * pitch + c], norm);
+    }
+}
+
 hipError_t launch_normalize_rows(float* x, int64_t rows, int64_t cols, hipStream_t s) {
+    // rows per workgroup: as many as 64 KB of LDS holds, at most 32
+    const int64_t rb = cols + 1 <= 16384 ? std::min<int64_t>(32, 16384 / (cols + 1)) : 0;
+    if (rb >= 1 && cols <= 0x7FFFFFFF / 32) {
+        const size_t lds = ((size_t)rb * (size_t)(cols + 1) + (size_t)rb) * sizeof(float);
+        hipLaunchKernelGGL(normalize_rows_lds_kernel, dim3((unsigned)((rows + rb - 1) / rb)), dim3(256), lds, s, x,
+                           rows, (int)cols, (int)rb);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(normalize_rows_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, x, rows,
                        cols);
     return hipGetLastError();

@@ -76,8 +76,11 @@ def test_mean_pool_masked_bit_exact(rt):
     assert np.all(got[0] == 0)
 
 
-def test_normalize_rows_bit_exact(rt):
-    x = synth.normal_f32(15, 0, 70, 384)
+@pytest.mark.parametrize("rows,cols", [(70, 384), (1000, 17), (33, 1), (5, 20000), (65, 511)])
+def test_normalize_rows_bit_exact(rt, rows, cols):
+    """Both launch shapes: rows staged in LDS (pitch cols + 1), and one
+    thread per row when a row does not fit."""
+    x = synth.normal_f32(15, 0, rows, cols)
     x[3] = 0.0  # zero row stays unchanged
     d = rt.to_device(x)
     rt.normalize_rows(d)
