@@ -1,6 +1,6 @@
 // kernels_encoder.hip -- device steps of the encoder pipeline (gather of q8
-// token rows, f32 GEMMs with fused q8 column dequant, row softmax, residual
-// add + layernorm, gelu), composed by manta_rocm_encoder_pooled.
+// token rows, f32 MFMA GEMMs with fused q8 column dequant, row softmax,
+// residual add + layernorm, gelu), composed by manta_rocm_encoder_pooled.
 //
 // All arithmetic is f32 (f64 where the reference uses it: the softmax sum
 // and exponentials, the layernorm's reciprocal square root, gelu's tanh).
@@ -51,23 +51,30 @@ __global__ __launch_bounds__(256) void enc_gather_q8_kernel(const int32_t* __res
 // C[b] = A[b] (M x K, row-major, batch stride sA) times B:
 //   BMODE 0: B[b] f32 [K][N] row-major (batch stride sB)
 //   BMODE 1: int8 [K][N] with an f32 scale per column (shared), dequantized
-//            as code * scale
+//            as code * scale while staging
 //   BMODE 2: the transpose of Bm[b], an f32 [N][K] row-major matrix
-// 64 x 64 output tile per workgroup, 4 x 4 per thread, K in steps of 16
-// through LDS; grid = (tiles of N, tiles of M, batches).
+// on the f32 matrix cores: a 64 x 64 output tile per workgroup as four 32 x 32
+// quarters, one per wave, each accumulated by v_mfma_f32_32x32x2f32 (lane l
+// supplies A[m = l%32][k = l/32] and B[k = l/32][n = l%32]; result row
+// 8*(r/4) + 4*(l/32) + r%4, column l%32 of its 16 values).  K moves in steps
+// of 16 through LDS; grid = (tiles of N, tiles of M, batches).
 template <int BMODE>
-__global__ __launch_bounds__(256) void enc_gemm_kernel(const float* __restrict__ A, int64_t sA,
-                                                       const void* __restrict__ Bv, const float* __restrict__ bscale,
-                                                       int64_t sB, float* __restrict__ C, int64_t sC, int M, int N,
-                                                       int K) {
+__global__ __launch_bounds__(256) void enc_gemm_mfma_kernel(const float* __restrict__ A, int64_t sA,
+                                                            const void* __restrict__ Bv,
+                                                            const float* __restrict__ bscale, int64_t sB,
+                                                            float* __restrict__ C, int64_t sC, int M, int N, int K) {
+    typedef float v16f __attribute__((ext_vector_type(16)));
     __shared__ float As[16][64 + 4];
     __shared__ float Bs[16][64 + 4];
     const int tid = threadIdx.x;
-    const int tx = tid & 15, ty = tid >> 4;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
     const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
     const int64_t bt = blockIdx.z;
     const float* a = A + bt * sA;
-    float acc[4][4] = {};
+    v16f acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
     for (int k0 = 0; k0 < K; k0 += 16) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -97,28 +104,19 @@ __global__ __launch_bounds__(256) void enc_gemm_kernel(const float* __restrict__
         }
         __syncthreads();
 #pragma unroll
-        for (int kk = 0; kk < 16; kk++) {
-            const float4 av = *(const float4*)&As[kk][ty * 4];
-            const float4 bv = *(const float4*)&Bs[kk][tx * 4];
-            const float ar[4] = {av.x, av.y, av.z, av.w};
-            const float br[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = __fmaf_rn(ar[i], br[j], acc[i][j]);
+        for (int kk = 0; kk < 16; kk += 2) {
+            const float av = As[kk + (lane >> 5)][wm + (lane & 31)];
+            const float bv = Bs[kk + (lane >> 5)][wn + (lane & 31)];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
         }
         __syncthreads();
     }
     float* c = C + bt * sC;
+    const int gn = n0 + wn + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int gm = m0 + ty * 4 + i;
-        if (gm >= M) continue;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int gn = n0 + tx * 4 + j;
-            if (gn < N) c[(int64_t)gm * N + gn] = acc[i][j];
-        }
+    for (int r = 0; r < 16; r++) {
+        const int gm = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (gm < M && gn < N) c[(int64_t)gm * N + gn] = acc[r];
     }
 }
 
@@ -202,11 +200,11 @@ hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B,
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)batches);
     if (bmode == 0)
-        hipLaunchKernelGGL(enc_gemm_kernel<0>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
+        hipLaunchKernelGGL(enc_gemm_mfma_kernel<0>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
     else if (bmode == 1)
-        hipLaunchKernelGGL(enc_gemm_kernel<1>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
+        hipLaunchKernelGGL(enc_gemm_mfma_kernel<1>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
     else
-        hipLaunchKernelGGL(enc_gemm_kernel<2>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
+        hipLaunchKernelGGL(enc_gemm_mfma_kernel<2>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
     return hipGetLastError();
 }
 
