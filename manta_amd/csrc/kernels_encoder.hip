@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void enc_gather_q8_kernel(const int32_t* __res
 // supplies A[m = l%32][k = l/32] and B[k = l/32][n = l%32]; result row
 // 8*(r/4) + 4*(l/32) + r%4, column l%32 of its 16 values).  K moves in steps
 // of 16 through LDS; grid = (tiles of N, tiles of M, batches).
-template <int BMODE>
+template <int BMODE, bool VEC>
 __global__ __launch_bounds__(256) void enc_gemm_mfma_kernel(const float* __restrict__ A, int64_t sA,
                                                             const void* __restrict__ Bv,
                                                             const float* __restrict__ bscale, int64_t sB,
@@ -76,30 +76,64 @@ __global__ __launch_bounds__(256) void enc_gemm_mfma_kernel(const float* __restr
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
     for (int k0 = 0; k0 < K; k0 += 16) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + 256 * i;
-            const int m = e >> 4, kk = e & 15;
-            const int gm = m0 + m, gk = k0 + kk;
-            As[kk][m] = (gm < M && gk < K) ? a[(int64_t)gm * K + gk] : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + 256 * i;
-            float v = 0.0f;
+        if (VEC) {
+            // one 16-byte load per thread per tile (K % 16 == 0; N % 4 == 0
+            // unless B is transposed): A by 4 consecutive k of a row
+            {
+                const int m = tid >> 2, kq = (tid & 3) * 4;
+                const int gm = m0 + m;
+                const float4 v = gm < M ? *(const float4*)(a + (int64_t)gm * K + k0 + kq) : float4{0, 0, 0, 0};
+                As[kq][m] = v.x, As[kq + 1][m] = v.y, As[kq + 2][m] = v.z, As[kq + 3][m] = v.w;
+            }
             if (BMODE == 2) {
-                const int n = e >> 4, kk = e & 15;
-                const int gn = n0 + n, gk = k0 + kk;
-                if (gn < N && gk < K) v = ((const float*)Bv)[bt * sB + (int64_t)gn * K + gk];
-                Bs[kk][n] = v;
+                const int n = tid >> 2, kq = (tid & 3) * 4;
+                const int gn = n0 + n;
+                const float4 v = gn < N ? *(const float4*)((const float*)Bv + bt * sB + (int64_t)gn * K + k0 + kq)
+                                        : float4{0, 0, 0, 0};
+                Bs[kq][n] = v.x, Bs[kq + 1][n] = v.y, Bs[kq + 2][n] = v.z, Bs[kq + 3][n] = v.w;
             } else {
-                const int kk = e >> 6, n = e & 63;
-                const int gn = n0 + n, gk = k0 + kk;
-                if (gn < N && gk < K) {
-                    if (BMODE == 0) v = ((const float*)Bv)[bt * sB + (int64_t)gk * N + gn];
-                    else v = fmul_rn((float)((const int8_t*)Bv)[(int64_t)gk * N + gn], bscale[gn]);
+                const int kk = tid >> 4, nq = (tid & 15) * 4;
+                const int gn = n0 + nq;
+                float4 v = {0, 0, 0, 0};
+                if (gn < N) {
+                    const int64_t off = (int64_t)(k0 + kk) * N + gn;
+                    if (BMODE == 0) {
+                        v = *(const float4*)((const float*)Bv + bt * sB + off);
+                    } else {
+                        const char4 c = *(const char4*)((const int8_t*)Bv + off);
+                        const float4 sc = *(const float4*)(bscale + gn);
+                        v = float4{fmul_rn((float)c.x, sc.x), fmul_rn((float)c.y, sc.y), fmul_rn((float)c.z, sc.z),
+                                   fmul_rn((float)c.w, sc.w)};
+                    }
                 }
-                Bs[kk][n] = v;
+                *(float4*)&Bs[kk][nq] = v;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int e = tid + 256 * i;
+                const int m = e >> 4, kk = e & 15;
+                const int gm = m0 + m, gk = k0 + kk;
+                As[kk][m] = (gm < M && gk < K) ? a[(int64_t)gm * K + gk] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int e = tid + 256 * i;
+                float v = 0.0f;
+                if (BMODE == 2) {
+                    const int n = e >> 4, kk = e & 15;
+                    const int gn = n0 + n, gk = k0 + kk;
+                    if (gn < N && gk < K) v = ((const float*)Bv)[bt * sB + (int64_t)gn * K + gk];
+                    Bs[kk][n] = v;
+                } else {
+                    const int kk = e >> 6, n = e & 63;
+                    const int gn = n0 + n, gk = k0 + kk;
+                    if (gn < N && gk < K) {
+                        if (BMODE == 0) v = ((const float*)Bv)[bt * sB + (int64_t)gk * N + gn];
+                        else v = fmul_rn((float)((const int8_t*)Bv)[(int64_t)gk * N + gn], bscale[gn]);
+                    }
+                    Bs[kk][n] = v;
+                }
             }
         }
         __syncthreads();
@@ -199,12 +233,23 @@ hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B,
     if (M <= 0 || N <= 0 || K <= 0 || batches <= 0 || batches > 65535 || (M + 63) / 64 > 65535)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)batches);
-    if (bmode == 0)
-        hipLaunchKernelGGL(enc_gemm_mfma_kernel<0>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
-    else if (bmode == 1)
-        hipLaunchKernelGGL(enc_gemm_mfma_kernel<1>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
-    else
-        hipLaunchKernelGGL(enc_gemm_mfma_kernel<2>, grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, sC, M, N, K);
+    // 16-byte staging loads need whole K steps and 16-byte aligned rows (the
+    // batch strides and base pointers are multiples of 4 elements here)
+    const bool vec = K % 16 == 0 && (bmode == 2 || N % 4 == 0) && sA % 4 == 0 && sB % 4 == 0 &&
+                     ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && (bmode != 1 || ((uintptr_t)bscale & 15) == 0);
+#define MANTA_ENC_GEMM(BM)                                                                                      \
+    do {                                                                                                        \
+        if (vec)                                                                                                \
+            hipLaunchKernelGGL((enc_gemm_mfma_kernel<BM, true>), grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, \
+                               sC, M, N, K);                                                                    \
+        else                                                                                                    \
+            hipLaunchKernelGGL((enc_gemm_mfma_kernel<BM, false>), grid, dim3(256), 0, s, A, sA, B, bscale, sB,   \
+                               C, sC, M, N, K);                                                                 \
+    } while (0)
+    if (bmode == 0) MANTA_ENC_GEMM(0);
+    else if (bmode == 1) MANTA_ENC_GEMM(1);
+    else MANTA_ENC_GEMM(2);
+#undef MANTA_ENC_GEMM
     return hipGetLastError();
 }
 
