@@ -73,6 +73,36 @@ int manta_mll_head_entry(const MantaMll* m, int index, uint32_t* key, int* kind,
 /* BLAKE3-256 of a byte string (the section digest). */
 void manta_mll_blake3(const void* data, size_t size, uint8_t out[32]);
 
+/* ---- packed candidate containers ----------------------------------------
+ * Real int8 / nibble candidate rows on disk, in place of the f32-widened q4/q8
+ * tensors the reference stores (runtime/mll_export.go:858-862, decoded back to
+ * f32 by decodeTensorEntry, runtime/weight_file.go:304-367).  The container is
+ * the MLL layout above; HEAD holds manifest_kind "packed_candidates",
+ * manifest_version "manta/packed-candidates/v0", docs_dtype "q8"|"q4" and
+ * rows / dim (i64) / has_ids (bool); the data sections start on 4 KiB pages
+ * (flag bit 4, as the reference's TNSR section) and hold raw little-endian
+ * arrays:
+ *   QCOD  q8: int8 codes [rows][dim]; q4: packed nibbles [rows][dim/2]
+ *         (value 2j in the low nibble, 2j+1 in the high one, 4-bit two's
+ *         complement)
+ *   QSCL  q8: f32 scale per row; q4: f16 scale per 32-value block [rows][dim/32]
+ *   QIDS  optional i64 candidate ids [rows]
+ * These are the layouts manta_rocm_pack_q8_rows / manta_rocm_pack_q4_blocks
+ * produce and manta_rocm_bind_q8_rows / manta_rocm_bind_q4_blocks take, so a
+ * container binds to the device without conversion.  No reference
+ * counterpart: the format is this library's own (the reference's TNSR tensor
+ * entries come from the unvendored codec and hold f32 for q4/q8). */
+
+/* Write a container.  dtype: MANTA_ROCM_Q8_ROWS (8) or MANTA_ROCM_Q4_BLOCKS (4);
+ * ids may be NULL. */
+int manta_mll_write_packed(const char* path, const char* name, int dtype, uint64_t rows, uint32_t dim,
+                           const void* codes, const void* scales, const int64_t* ids, char** err);
+
+/* Check an opened container's metadata and section sizes and return pointers
+ * into its bytes (owned by the handle); *ids is NULL without a QIDS section. */
+int manta_mll_packed_info(const MantaMll* m, int* dtype, uint64_t* rows, uint32_t* dim, const void** codes,
+                          const void** scales, const int64_t** ids, char** err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -161,6 +161,14 @@ int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* sca
 int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16_t* scales,
                               int64_t sets, int64_t n, int64_t d, MantaRocmCandidates** out,
                               char** err);
+/* Bind the candidates of a packed container (manta_mll.h: QCOD / QSCL
+ * sections opened with manta_mll_open) as one set, the bytes going to the
+ * device as stored, with no f32 widening or re-quantisation.  Replaces the
+ * load path ReadWeightFile -> decodeWeightFileFromMLLReader ->
+ * decodeTensorEntry -> NewTensorQ4/Q8 of f32 values
+ * (runtime/weight_file.go:93-104, 247-367) for candidate stores. */
+int manta_rocm_bind_packed(MantaRocm* rt, const struct MantaMll* container, MantaRocmCandidates** out,
+                           char** err);
 void manta_rocm_unbind(MantaRocmCandidates* cands);
 int manta_rocm_candidates_info(const MantaRocmCandidates* cands, int* format, int64_t* sets,
                                int64_t* n, int64_t* d);

@@ -88,10 +88,16 @@ SIGNATURES = {
          C.POINTER(C.c_uint32), _err],
     ),
     "manta_mll_blake3": (None, [_p, C.c_size_t, _p]),
+    "manta_mll_write_packed": (
+        C.c_int, [C.c_char_p, C.c_char_p, C.c_int, C.c_uint64, C.c_uint32, _p, _p, _p, _err]),
+    "manta_mll_packed_info": (
+        C.c_int, [_p, C.POINTER(C.c_int), C.POINTER(C.c_uint64), C.POINTER(C.c_uint32), C.POINTER(_p),
+                  C.POINTER(_p), C.POINTER(_p), _err]),
     "manta_rocm_pack_q8_rows": (C.c_int, [_p, _i64, _i64, _p, _p, _err]),
     "manta_rocm_pack_q4_blocks": (C.c_int, [_p, _i64, _i64, _p, _p, _err]),
     "manta_rocm_bind_q8_rows": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, C.POINTER(_p), _err]),
     "manta_rocm_bind_q4_blocks": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, C.POINTER(_p), _err]),
+    "manta_rocm_bind_packed": (C.c_int, [_p, _p, C.POINTER(_p), _err]),
     "manta_rocm_unbind": (None, [_p]),
     "manta_rocm_candidates_info": (
         C.c_int,

@@ -230,6 +230,38 @@ void parse_head(MantaMll* m, const uint8_t* p, uint64_t n) {
     if (at != n) m->head_error = "malformed HEAD section: " + std::to_string(n - at) + " trailing bytes";
 }
 
+
+// ------------------------------------------------ packed candidate containers
+
+const char kPackedKind[] = "packed_candidates";
+const char kPackedVersion[] = "manta/packed-candidates/v0";
+
+void put32(std::vector<uint8_t>& b, uint32_t v) {
+    for (int i = 0; i < 4; i++) b.push_back((uint8_t)(v >> (8 * i)));
+}
+void put64(std::vector<uint8_t>& b, uint64_t v) {
+    for (int i = 0; i < 8; i++) b.push_back((uint8_t)(v >> (8 * i)));
+}
+
+// Expected byte sizes of the code and scale sections of `rows` rows of `dim`
+// values: q8 = int8 codes + one f32 scale per row, q4 = two values per byte
+// + one f16 scale per 32-value block.
+void packed_sizes(int dtype, uint64_t rows, uint64_t dim, uint64_t* codes, uint64_t* scales) {
+    if (dtype == MANTA_ROCM_Q8_ROWS) {
+        *codes = rows * dim;
+        *scales = rows * 4;
+    } else {
+        *codes = rows * (dim / 2);
+        *scales = rows * (dim / 32) * 2;
+    }
+}
+
+const MantaMll::Entry* head_value(const MantaMll* m, const char* key) {
+    for (const auto& e : m->entries)
+        if (e.key < m->strings.size() && m->strings[e.key] == key) return &e;
+    return nullptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -342,6 +374,147 @@ int manta_mll_head_entry(const MantaMll* m, int index, uint32_t* key, int* kind,
     if (i64) *i64 = e.i64;
     if (f64) *f64 = e.f64;
     if (str) *str = e.str;
+    return MANTA_ROCM_OK;
+}
+
+int manta_mll_write_packed(const char* path, const char* name, int dtype, uint64_t rows, uint32_t dim,
+                           const void* codes, const void* scales, const int64_t* ids, char** err) {
+    if (!path) return mll_fail(err, "nil path");
+    if (dtype != MANTA_ROCM_Q8_ROWS && dtype != MANTA_ROCM_Q4_BLOCKS)
+        return mll_fail(err, "packed candidates: dtype %d is neither q8 (8) nor q4 (4)", dtype);
+    if (rows == 0 || dim == 0 || (dtype == MANTA_ROCM_Q4_BLOCKS && dim % 32 != 0))
+        return mll_fail(err, "packed candidates: bad shape [%llu,%u]", (unsigned long long)rows, dim);
+    if (!codes || !scales) return mll_fail(err, "packed candidates: nil codes or scales");
+    uint64_t ncode = 0, nscale = 0;
+    packed_sizes(dtype, rows, dim, &ncode, &nscale);
+    // string table: 1 name, 2 description, then keys and string values
+    const char* strs[] = {name ? name : "", "Manta packed candidates", "manifest_kind", kPackedKind,
+                          "manifest_version", kPackedVersion, "docs_dtype",
+                          dtype == MANTA_ROCM_Q8_ROWS ? "q8" : "q4", "rows", "dim", "has_ids"};
+    const int nstr = (int)(sizeof(strs) / sizeof(strs[0]));
+    std::vector<uint8_t> strg;
+    put64(strg, (uint64_t)nstr + 1);
+    for (int i = 0; i < nstr; i++) {
+        const uint32_t len = (uint32_t)strlen(strs[i]);
+        put32(strg, len);
+        strg.insert(strg.end(), strs[i], strs[i] + len);
+    }
+    std::vector<uint8_t> head;
+    put32(head, 1);
+    put32(head, 2);
+    head.resize(head.size() + 20, 0);
+    head.push_back(6);
+    head.push_back(0);
+    for (uint32_t k = 3; k <= 7; k += 2) {  // three string-valued entries
+        put32(head, k);
+        head.push_back(MANTA_MLL_STRING);
+        put32(head, k + 1);
+    }
+    put32(head, 9);
+    head.push_back(MANTA_MLL_I64);
+    put64(head, rows);
+    put32(head, 10);
+    head.push_back(MANTA_MLL_I64);
+    put64(head, dim);
+    put32(head, 11);
+    head.push_back(MANTA_MLL_BOOL);
+    head.push_back(ids ? 1 : 0);
+
+    struct Out {
+        const char* tag;
+        const uint8_t* p;
+        uint64_t n;
+        uint32_t flags;
+        uint64_t off;
+    };
+    // flags: bit 0 required, bit 4 page aligned, schema version in bits 16+
+    std::vector<Out> secs = {{"HEAD", head.data(), head.size(), 0x10001u, 0},
+                             {"STRG", strg.data(), strg.size(), 0x10001u, 0},
+                             {"QCOD", (const uint8_t*)codes, ncode, 0x10011u, 0},
+                             {"QSCL", (const uint8_t*)scales, nscale, 0x10011u, 0}};
+    if (ids) secs.push_back({"QIDS", (const uint8_t*)ids, rows * 8, 0x10011u, 0});
+    uint64_t at = 24 + 64 * (uint64_t)secs.size();
+    for (auto& s : secs) {
+        if (s.flags & 0x10u) at = (at + 4095) & ~(uint64_t)4095;
+        s.off = at;
+        at += s.n;
+    }
+    const uint64_t total = at;
+    std::vector<uint8_t> top;
+    top.insert(top.end(), {'M', 'L', 'L', 0});
+    put32(top, 0x00010100u);
+    put64(top, total);
+    put64(top, secs.size());
+    for (const auto& s : secs) {
+        top.insert(top.end(), s.tag, s.tag + 4);
+        put64(top, s.off);
+        put64(top, s.n);
+        uint8_t d[32];
+        blake3(s.p, (size_t)s.n, d);
+        top.insert(top.end(), d, d + 32);
+        put32(top, s.flags);
+        put64(top, 0);
+    }
+    FILE* f = fopen(path, "wb");
+    if (!f) return mll_fail(err, "packed candidates: cannot create %s", path);
+    bool ok = fwrite(top.data(), 1, top.size(), f) == top.size();
+    uint64_t pos = top.size();
+    static const uint8_t zeros[4096] = {0};
+    for (const auto& s : secs) {
+        if (!ok) break;
+        ok = fwrite(zeros, 1, (size_t)(s.off - pos), f) == (size_t)(s.off - pos) &&
+             fwrite(s.p, 1, (size_t)s.n, f) == (size_t)s.n;
+        pos = s.off + s.n;
+    }
+    if (fclose(f) != 0) ok = false;
+    if (!ok) return mll_fail(err, "packed candidates: short write to %s", path);
+    return MANTA_ROCM_OK;
+}
+
+int manta_mll_packed_info(const MantaMll* m, int* dtype, uint64_t* rows, uint32_t* dim, const void** codes,
+                          const void** scales, const int64_t** ids, char** err) {
+    int rc = manta_mll_head(m, nullptr, nullptr, nullptr, err);
+    if (rc) return rc;
+    const MantaMll::Entry* kind = head_value(m, "manifest_kind");
+    const MantaMll::Entry* version = head_value(m, "manifest_version");
+    if (!kind || kind->kind != MANTA_MLL_STRING || m->strings[kind->str] != kPackedKind)
+        return mll_fail(err, "manifest kind \"%s\", want \"%s\"",
+                        kind && kind->kind == MANTA_MLL_STRING ? manta_mll_string(m, kind->str) : "",
+                        kPackedKind);
+    if (!version || version->kind != MANTA_MLL_STRING || m->strings[version->str] != kPackedVersion)
+        return mll_fail(err, "manifest version \"%s\", want \"%s\"",
+                        version && version->kind == MANTA_MLL_STRING ? manta_mll_string(m, version->str) : "",
+                        kPackedVersion);
+    const MantaMll::Entry* dt = head_value(m, "docs_dtype");
+    const MantaMll::Entry* nr = head_value(m, "rows");
+    const MantaMll::Entry* nd = head_value(m, "dim");
+    const MantaMll::Entry* hi = head_value(m, "has_ids");
+    if (!dt || dt->kind != MANTA_MLL_STRING || !nr || nr->kind != MANTA_MLL_I64 || !nd ||
+        nd->kind != MANTA_MLL_I64 || !hi || hi->kind != MANTA_MLL_BOOL)
+        return mll_fail(err, "packed candidates: docs_dtype, rows, dim or has_ids missing or mistyped");
+    const std::string& dts = m->strings[dt->str];
+    const int t = dts == "q8" ? MANTA_ROCM_Q8_ROWS : (dts == "q4" ? MANTA_ROCM_Q4_BLOCKS : 0);
+    if (!t) return mll_fail(err, "packed candidates: docs_dtype \"%s\" is neither q8 nor q4", dts.c_str());
+    if (nr->i64 <= 0 || nd->i64 <= 0 || nd->i64 > 0xFFFFFFFFll || (t == MANTA_ROCM_Q4_BLOCKS && nd->i64 % 32))
+        return mll_fail(err, "packed candidates: bad shape [%lld,%lld]", (long long)nr->i64, (long long)nd->i64);
+    uint64_t want[3] = {0, 0, (uint64_t)nr->i64 * 8};
+    packed_sizes(t, (uint64_t)nr->i64, (uint64_t)nd->i64, &want[0], &want[1]);
+    const char* tags[3] = {"QCOD", "QSCL", "QIDS"};
+    const void* ptr[3] = {nullptr, nullptr, nullptr};
+    for (int i = 0; i < (hi->i64 ? 3 : 2); i++) {
+        const MantaMll::Section* s = find_section(m, tags[i]);
+        if (!s) return mll_fail(err, "manifest missing %s section", tags[i]);
+        if (s->size != want[i])
+            return mll_fail(err, "packed candidates: %s section is %llu bytes, want %llu", tags[i],
+                            (unsigned long long)s->size, (unsigned long long)want[i]);
+        ptr[i] = m->bytes.data() + s->offset;
+    }
+    if (dtype) *dtype = t;
+    if (rows) *rows = (uint64_t)nr->i64;
+    if (dim) *dim = (uint32_t)nd->i64;
+    if (codes) *codes = ptr[0];
+    if (scales) *scales = ptr[1];
+    if (ids) *ids = (const int64_t*)ptr[2];
     return MANTA_ROCM_OK;
 }
 

@@ -8,6 +8,7 @@
 // runtime/backend/tensor_ops.go (scoreLayout :1499-1521, topKTensor
 // :1523-1534, gatherTensor :794-877).
 #include "manta_rocm.h"
+#include "manta_mll.h"
 
 #include <hip/hip_runtime.h>
 
@@ -520,6 +521,23 @@ int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* sca
     rt->stats.candidate_bytes += c->bytes;
     *out = c;
     return MANTA_ROCM_OK;
+}
+
+int manta_rocm_bind_packed(MantaRocm* rt, const MantaMll* container, MantaRocmCandidates** out, char** err) {
+    RT_CHECK(rt);
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil output");
+    *out = nullptr;
+    int dtype = 0;
+    uint64_t rows = 0;
+    uint32_t dim = 0;
+    const void *codes = nullptr, *scales = nullptr;
+    int rc = manta_mll_packed_info(container, &dtype, &rows, &dim, &codes, &scales, nullptr, err);
+    if (rc) return rc;
+    if (dtype == MANTA_ROCM_Q8_ROWS)
+        return manta_rocm_bind_q8_rows(rt, (const int8_t*)codes, (const float*)scales, 1, (int64_t)rows,
+                                       (int64_t)dim, out, err);
+    return manta_rocm_bind_q4_blocks(rt, (const uint8_t*)codes, (const uint16_t*)scales, 1, (int64_t)rows,
+                                     (int64_t)dim, out, err);
 }
 
 int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16_t* scales,

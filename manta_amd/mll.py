@@ -13,6 +13,8 @@ import ctypes as C
 import os
 from typing import Optional, Union
 
+import numpy as np
+
 from . import _lib
 from ._lib import MantaRocmError, call, load
 
@@ -100,6 +102,51 @@ class MllFile:
                      else self.string(sid.value))
             entries.append((self.string(key.value), k, value))
         return self.string(name.value), self.string(desc.value), entries
+
+    def packed(self) -> dict:
+        """Contents of a packed candidate container (manta_mll_packed_info):
+        {"dtype": "q8"|"q4", "rows", "dim", "codes", "scales", "ids"} with
+        numpy copies of the sections (ids None without a QIDS section)."""
+        t, rows, dim = C.c_int(), C.c_uint64(), C.c_uint32()
+        pc, ps, pi = C.c_void_p(), C.c_void_p(), C.c_void_p()
+        call("manta_mll_packed_info", self._h, C.byref(t), C.byref(rows), C.byref(dim), C.byref(pc),
+             C.byref(ps), C.byref(pi))
+        n, d = rows.value, dim.value
+        if t.value == _lib.Q8_ROWS:
+            codes = np.frombuffer(C.string_at(pc, n * d), np.int8).reshape(n, d)
+            scales = np.frombuffer(C.string_at(ps, n * 4), np.float32).copy()
+        else:
+            codes = np.frombuffer(C.string_at(pc, n * d // 2), np.uint8).reshape(n, d // 2)
+            scales = np.frombuffer(C.string_at(ps, n * (d // 32) * 2), np.uint16).reshape(n, d // 32)
+        ids = np.frombuffer(C.string_at(pi, n * 8), np.int64) if pi.value else None
+        return {"dtype": "q8" if t.value == _lib.Q8_ROWS else "q4", "rows": n, "dim": d, "codes": codes,
+                "scales": scales, "ids": ids}
+
+
+def write_packed(path: Union[str, os.PathLike], codes: np.ndarray, scales: np.ndarray,
+                 ids: Optional[np.ndarray] = None, name: str = "") -> None:
+    """Write a packed candidate container.  q8: codes int8 [n,d], scales f32 [n];
+    q4: codes uint8 [n,d/2] (packed nibbles), scales f16 bits uint16 [n,d/32]."""
+    if codes.dtype == np.int8:
+        t, (n, d) = _lib.Q8_ROWS, codes.shape
+        scales = np.ascontiguousarray(scales, np.float32)
+        if scales.shape != (n,):
+            raise ValueError("q8 scales shape %s, want (%d,)" % (scales.shape, n))
+    elif codes.dtype == np.uint8:
+        t, (n, half) = _lib.Q4_BLOCKS, codes.shape
+        d = 2 * half
+        scales = np.ascontiguousarray(scales, np.uint16)
+        if scales.shape != (n, d // 32):
+            raise ValueError("q4 scales shape %s, want (%d, %d)" % (scales.shape, n, d // 32))
+    else:
+        raise ValueError("codes must be int8 (q8) or uint8 packed nibbles (q4), got %s" % codes.dtype)
+    codes = np.ascontiguousarray(codes)
+    if ids is not None:
+        ids = np.ascontiguousarray(ids, np.int64)
+        if ids.shape != (n,):
+            raise ValueError("ids shape %s, want (%d,)" % (ids.shape, n))
+    call("manta_mll_write_packed", os.fsencode(path), name.encode(), t, n, d, codes.ctypes.data_as(C.c_void_p),
+         scales.ctypes.data_as(C.c_void_p), ids.ctypes.data_as(C.c_void_p) if ids is not None else None)
 
 
 def read_authored_manifest(data: Union[bytes, str, os.PathLike], expected_kind: str = "",

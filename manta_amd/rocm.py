@@ -183,6 +183,15 @@ class Runtime:
              C.byref(h))
         return Candidates(self, h, _lib.Q4_BLOCKS, sets, n, d)
 
+    def bind_packed(self, container) -> Candidates:
+        """Bind the candidates of a packed container (an opened mll.MllFile)
+        straight from its QCOD / QSCL bytes."""
+        h = C.c_void_p()
+        call("manta_rocm_bind_packed", self.handle, container._h, C.byref(h))
+        fmt, sets, n, d = C.c_int(), C.c_int64(), C.c_int64(), C.c_int64()
+        load().manta_rocm_candidates_info(h, C.byref(fmt), C.byref(sets), C.byref(n), C.byref(d))
+        return Candidates(self, h, fmt.value, sets.value, n.value, d.value)
+
     # ------------------------------------------------------------ scoring
     @staticmethod
     def _query_rows(cands: Candidates, queries: DeviceArray) -> int:
