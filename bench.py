@@ -326,7 +326,7 @@ def run_enc(rt, steps, warmup) -> dict:
     td, md, tcd, tsd = (rt.to_device(x) for x in (tokens, mask, tcodes, tscales))
     out = rt.empty((b, d), np.uint16)
     fams = ["encoder_gather", "encoder_gemm", "encoder_attention", "encoder_softmax", "encoder_layernorm",
-            "encoder_gelu", "normalize", "mean_pool", "encoder_out"]
+            "normalize", "mean_pool", "encoder_out"]
     step_s, fam, dev_ms = _timed(rt, lambda: rt.encoder_pooled(td, md, tcd, tsd, dev, out=out), steps, warmup, fams)
     r = b * t
     gemm_flops = 2.0 * r * d * d * 4 + 2.0 * r * d * h * 2

@@ -251,11 +251,10 @@ hipError_t launch_normalize_rows(float* x, int64_t rows, int64_t cols, hipStream
 hipError_t launch_enc_gather_q8(const int32_t* tok, int64_t rows, const int8_t* codes, const float* scales,
                                 int64_t vocab, int d, float* x, unsigned long long* err, hipStream_t s);
 hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B, const float* bscale, int64_t sB,
-                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s);
+                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s, bool gelu = false);
 hipError_t launch_enc_softmax_rows(float* x, int64_t rows, int cols, hipStream_t s);
 hipError_t launch_enc_add_layernorm(const float* a, const float* b, float* y, int64_t rows, int cols,
                                     hipStream_t s);
-hipError_t launch_enc_gelu(float* x, int64_t n, hipStream_t s);
 hipError_t launch_enc_to_f16(const float* x, int64_t n, uint16_t* out, hipStream_t s);
 
 hipError_t launch_topk_rows_partial(const float* scores, int64_t rows, int64_t cols, int64_t seg,

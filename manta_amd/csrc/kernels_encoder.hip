@@ -48,6 +48,14 @@ __global__ __launch_bounds__(256) void enc_gather_q8_kernel(const int32_t* __res
     }
 }
 
+// geluTensor: 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))), f32 with the
+// tanh in f64.
+__device__ __forceinline__ float gelu_value(float v) {
+    const float cubic = fmul_rn(fmul_rn(v, v), v);
+    const float inner = fmul_rn(0.7978845608f, fadd_rn(v, fmul_rn(0.044715f, cubic)));
+    return fmul_rn(fmul_rn(0.5f, v), fadd_rn(1.0f, (float)tanh((double)inner)));
+}
+
 // C[b] = A[b] (M x K, row-major, batch stride sA) times B:
 //   BMODE 0: B[b] f32 [K][N] row-major (batch stride sB)
 //   BMODE 1: int8 [K][N] with an f32 scale per column (shared), dequantized
@@ -57,12 +65,15 @@ __global__ __launch_bounds__(256) void enc_gather_q8_kernel(const int32_t* __res
 // quarters, one per wave, each accumulated by v_mfma_f32_32x32x2f32 (lane l
 // supplies A[m = l%32][k = l/32] and B[k = l/32][n = l%32]; result row
 // 8*(r/4) + 4*(l/32) + r%4, column l%32 of its 16 values).  K moves in steps
-// of 16 through LDS; grid = (tiles of N, tiles of M, batches).
+// of 16 through LDS; grid = (tiles of N, tiles of M, batches).  gelu != 0
+// applies geluTensor to each output value before the store (the FFN's
+// up-projection), the same f32 result as a separate pass.
 template <int BMODE, bool VEC>
 __global__ __launch_bounds__(256) void enc_gemm_mfma_kernel(const float* __restrict__ A, int64_t sA,
                                                             const void* __restrict__ Bv,
                                                             const float* __restrict__ bscale, int64_t sB,
-                                                            float* __restrict__ C, int64_t sC, int M, int N, int K) {
+                                                            float* __restrict__ C, int64_t sC, int M, int N, int K,
+                                                            int gelu) {
     typedef float v16f __attribute__((ext_vector_type(16)));
     __shared__ float As[16][64 + 4];
     __shared__ float Bs[16][64 + 4];
@@ -150,7 +161,7 @@ __global__ __launch_bounds__(256) void enc_gemm_mfma_kernel(const float* __restr
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int gm = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (gm < M && gn < N) c[(int64_t)gm * N + gn] = acc[r];
+        if (gm < M && gn < N) c[(int64_t)gm * N + gn] = gelu ? gelu_value(acc[r]) : acc[r];
     }
 }
 
@@ -199,17 +210,6 @@ __global__ __launch_bounds__(256) void enc_add_layernorm_kernel(const float* __r
     for (int c = lane; c < cols; c += 64) yr[c] = fmul_rn(fsub_rn(fadd_rn(ar[c], br[c]), mean), inv);
 }
 
-// geluTensor in place: 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))),
-// f32 with the tanh in f64.
-__global__ __launch_bounds__(256) void enc_gelu_kernel(float* __restrict__ x, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-        const float v = x[i];
-        const float cubic = fmul_rn(fmul_rn(v, v), v);
-        const float inner = fmul_rn(0.7978845608f, fadd_rn(v, fmul_rn(0.044715f, cubic)));
-        x[i] = fmul_rn(fmul_rn(0.5f, v), fadd_rn(1.0f, (float)tanh((double)inner)));
-    }
-}
-
 __global__ __launch_bounds__(256) void enc_to_f16_kernel(const float* __restrict__ x, int64_t n,
                                                          uint16_t* __restrict__ out) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
@@ -229,7 +229,7 @@ hipError_t launch_enc_gather_q8(const int32_t* tok, int64_t rows, const int8_t* 
 }
 
 hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B, const float* bscale, int64_t sB,
-                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s) {
+                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s, bool gelu) {
     if (M <= 0 || N <= 0 || K <= 0 || batches <= 0 || batches > 65535 || (M + 63) / 64 > 65535)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)batches);
@@ -241,10 +241,10 @@ hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B,
     do {                                                                                                        \
         if (vec)                                                                                                \
             hipLaunchKernelGGL((enc_gemm_mfma_kernel<BM, true>), grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, \
-                               sC, M, N, K);                                                                    \
+                               sC, M, N, K, gelu ? 1 : 0);                                                                    \
         else                                                                                                    \
             hipLaunchKernelGGL((enc_gemm_mfma_kernel<BM, false>), grid, dim3(256), 0, s, A, sA, B, bscale, sB,   \
-                               C, sC, M, N, K);                                                                 \
+                               C, sC, M, N, K, gelu ? 1 : 0);                                                                 \
     } while (0)
     if (bmode == 0) MANTA_ENC_GEMM(0);
     else if (bmode == 1) MANTA_ENC_GEMM(1);
@@ -265,10 +265,6 @@ hipError_t launch_enc_add_layernorm(const float* a, const float* b, float* y, in
     return hipGetLastError();
 }
 
-hipError_t launch_enc_gelu(float* x, int64_t n, hipStream_t s) {
-    hipLaunchKernelGGL(enc_gelu_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, n);
-    return hipGetLastError();
-}
 
 hipError_t launch_enc_to_f16(const float* x, int64_t n, uint16_t* out, hipStream_t s) {
     hipLaunchKernelGGL(enc_to_f16_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, n, out);

@@ -1263,8 +1263,8 @@ int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens, const int32_
     // attended = mixed @ attn_o (into q); attn_hidden = layernorm(attended + x) (into k)
     LAUNCH_TRY(manta::launch_enc_gemm(1, mx, 0, w->codes[3], w->col_scales[3], 0, q, 0, R, D, D, 1, s), "encoder_gemm");
     LAUNCH_TRY(manta::launch_enc_add_layernorm(q, x, k, rows, D, s), "encoder_layernorm");
-    LAUNCH_TRY(manta::launch_enc_gemm(1, k, 0, w->codes[4], w->col_scales[4], 0, ffn, 0, R, H, D, 1, s), "encoder_gemm");
-    LAUNCH_TRY(manta::launch_enc_gelu(ffn, rows * h, s), "encoder_gelu");
+    LAUNCH_TRY(manta::launch_enc_gemm(1, k, 0, w->codes[4], w->col_scales[4], 0, ffn, 0, R, H, D, 1, s, true),
+               "encoder_gemm");
     // projected = gelu @ projection (into v); encoded = layernorm(projected + attn_hidden) (into mx)
     LAUNCH_TRY(manta::launch_enc_gemm(1, ffn, 0, w->codes[5], w->col_scales[5], 0, v, 0, R, D, H, 1, s), "encoder_gemm");
     LAUNCH_TRY(manta::launch_enc_add_layernorm(v, k, mx, rows, D, s), "encoder_layernorm");
