@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MANTA_ROCM_ABI_VERSION 1
+#define MANTA_ROCM_ABI_VERSION 2
 
 enum {
     MANTA_ROCM_OK = 0,
@@ -48,11 +48,28 @@ enum {
 };
 
 /* Score builtins: the kernel body op names dot / cosine / l2_distance
- * (compiler/compiler.go:803-842, classified at native_linux.go:1734-1750). */
+ * (compiler/compiler.go:803-842, classified at native_linux.go:1734-1750).
+ *
+ * By default every score is the reference's own arithmetic on the values the
+ * packed candidates stand for, bit for bit: dotRows (f32 sum in column
+ * order), cosineRows (f64 dot and norms, narrowed), l2DistanceRows (f32
+ * difference, f64 square-sum, sqrt, narrowed) of tensor_ops.go:1366-1490,
+ * with a q8 element valued code*scale in f32 and a q4 element code*f16scale
+ * (the f32 values a fake-quantized reference tensor holds,
+ * runtime/embedding_trainer.go:3753-3762) and the f16 query widened to f32.
+ * Top-k ids are topKTensor's (value desc, index asc).
+ *
+ * OR-ing MANTA_ROCM_QUANTIZED_QUERY into the op selects this library's
+ * quantized-query scores instead: q8 dot is BASELINE's formula
+ * (query codes round(q*127/max(1, maxabs q)), int32 accumulation,
+ * score = scale*acc*qmax/127 in f32); the other ops use 16-bit query codes
+ * (round(q*32639/maxabs q)) with exact integer accumulation.  Within a
+ * stated bound of the reference scores, not equal to them. */
 enum {
     MANTA_ROCM_DOT = 0,
     MANTA_ROCM_COSINE = 1,
     MANTA_ROCM_L2_DISTANCE = 2,
+    MANTA_ROCM_QUANTIZED_QUERY = 0x100,
 };
 
 /* Selection order.  LARGEST is topKTensor's order (value desc, index asc;
@@ -176,18 +193,24 @@ int manta_rocm_candidates_info(const MantaRocmCandidates* cands, int* format, in
 /* ---- scoring ------------------------------------------------------------ */
 
 /* Full score matrix.  queries_dev: f16 [nq, d]; out_scores_dev: f32 [nq, n].
- * Replaces runScoreKernel (native_linux.go:1694-1732) and the host
- * dotRows / cosineRows / l2DistanceRows (tensor_ops.go:1366-1490) for packed
- * candidates. */
+ * op: MANTA_ROCM_DOT / COSINE / L2_DISTANCE, optionally with
+ * MANTA_ROCM_QUANTIZED_QUERY.  Replaces runScoreKernel
+ * (native_linux.go:1694-1732) and the host dotRows / cosineRows /
+ * l2DistanceRows (tensor_ops.go:1366-1490) for packed candidates. */
 int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* cands, int op,
                      const uint16_t* queries_dev, int64_t nq, float* out_scores_dev, char** err);
 
 /* Fused scoring + top-k: the score matrix is never written.  out_ids_dev
  * int32 [nq, k]; out_scores_dev f32 [nq, k] (may be NULL); out_acc_dev int64
  * [nq, k] (may be NULL): the exact integer accumulator of each selected row
- * (q8 candidates only).  Replaces launch_kernel(score) followed by the host
- * topk step (tensor_ops.go:119-135, 1523-1592).  Errors like topKTensor when
- * k <= 0 or k > n. */
+ * (q8 candidates with MANTA_ROCM_QUANTIZED_QUERY only).  Replaces
+ * launch_kernel(score) followed by the host topk step
+ * (tensor_ops.go:119-135, 1523-1592).  Errors like topKTensor when k <= 0 or
+ * k > n.  With reference scores the quantized-query scan ranks the rows, its
+ * best few beyond k are rescored with the reference arithmetic, and the
+ * error bounds between the two decide whether any other row could still
+ * enter; a query where they cannot rule that out is rescanned with the
+ * reference arithmetic, so the result is the reference's either way. */
 int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* cands, int op, int order,
                           const uint16_t* queries_dev, int64_t nq, int64_t k,
                           int32_t* out_ids_dev, float* out_scores_dev, int64_t* out_acc_dev,

@@ -14,6 +14,7 @@ SYNTH_PATH = os.path.join(HERE, "libmanta_synth.so")
 
 OK, ERROR, UNSUPPORTED = 0, 1, 2
 DOT, COSINE, L2_DISTANCE = 0, 1, 2
+QUANTIZED_QUERY = 0x100
 LARGEST, SMALLEST = 0, 1
 Q8_ROWS, Q4_BLOCKS = 8, 4
 PROJ_F16, PROJ_Q8_COL = 0, 1

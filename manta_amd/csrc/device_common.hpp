@@ -54,13 +54,48 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
     return x;
 }
 
-__device__ __forceinline__ float fmul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float fadd_rn(float a, float b) { return __fadd_rn(a, b); }
-__device__ __forceinline__ float fsub_rn(float a, float b) { return __fsub_rn(a, b); }
+// Every operation rounded on its own.  Written as plain operators under this
+// file's `fp contract(off)`: HIP's __fmul_rn / __fadd_rn are plain operators
+// in headers compiled with contraction allowed, so a product from them fed
+// into a sum may be fused into one fma (found by the reference l2 parity
+// test: q - code*scale computed exactly instead of after the product's
+// rounding).
+__device__ __forceinline__ float fmul_rn(float a, float b) { return a * b; }
+__device__ __forceinline__ float fadd_rn(float a, float b) { return a + b; }
+__device__ __forceinline__ float fsub_rn(float a, float b) { return a - b; }
+__device__ __forceinline__ double dmul_rn(double a, double b) { return a * b; }
 __device__ __forceinline__ float fdiv_rn(float a, float b) { return __fdiv_rn(a, b); }
 // __fsqrt_rn lowers to the bare v_sqrt_f32 (about 1 ulp); llvm.sqrt.f32 with
 // -fhip-fp32-correctly-rounded-divide-sqrt is the correctly rounded sequence.
 __device__ __forceinline__ float fsqrt_rn(float a) { return __builtin_sqrtf(a); }
+
+// ----------------------------------------------------------- query codes
+
+// E8 (q8 dot): qmax = max(1, maxabs), code = clamp(round((q*127)/qmax)).
+__device__ __forceinline__ int code_e8(float x, float qmax) {
+    float r = round_half_away(fdiv_rn(fmul_rn(x, 127.0f), qmax));
+    return (int)fminf(127.0f, fmaxf(-127.0f, r));
+}
+
+// E16: code = clamp(round(q*(32639/maxabs)), +-32639), split 256*hi + lo
+// with lo the signed low byte.
+__device__ __forceinline__ int code_e16(float x, float inv) {
+    float r = round_half_away(fmul_rn(x, inv));
+    return (int)fminf(32639.0f, fmaxf(-32639.0f, r));
+}
+
+__device__ __forceinline__ QConst e16_consts(float maxabs, long long ss) {
+    QConst k{0.0f, 0.0f, 0.0f, 0.0f};
+    if (maxabs != 0.0f) {
+        const float qs = fdiv_rn(maxabs, 32639.0f);
+        const double dss = (double)ss;
+        k.a = qs;
+        k.b = (float)__dmul_rn(__dsqrt_rn(dss), (double)qs);
+        k.c = (float)__dmul_rn(__dmul_rn(dss, (double)qs), (double)qs);
+    }
+    return k;
+}
+
 
 // Order-preserving map float -> u32 with -0 folded onto +0 (the reference
 // compares with <, >, so -0 and +0 tie and fall through to the index).

@@ -7,7 +7,13 @@
 
 namespace manta {
 
-enum { OP_DOT = 0, OP_COSINE = 1, OP_L2 = 2 };
+// Device score ops.  OP_DOT / OP_COSINE / OP_L2 name the reference's
+// dotRows / cosineRows / l2DistanceRows where a kernel computes those
+// (kernels_ref.hip); in the quantized-query scans they name the scan's own
+// score: q8 OP_DOT with E8 query codes (BASELINE's q8 dot formula), every
+// other q8 op and every q4 op with E16 codes.  OP_DOT16 is the q8 dot with
+// E16 codes (qd), a scan score only.
+enum { OP_DOT = 0, OP_COSINE = 1, OP_L2 = 2, OP_DOT16 = 3 };
 
 struct QConst;
 
@@ -75,6 +81,48 @@ hipError_t launch_q4_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipS
 hipError_t launch_q8_rescore(const int8_t* codes, int pitch, int64_t set_stride, int64_t n, int d,
                              const uint16_t* queries, const int32_t* ids, int k, int nq, int e16,
                              int64_t* out, hipStream_t s);
+
+// ---- reference scores (kernels_ref.hip)
+//
+// A quantized-query scan returns the best kp >= k rows of each query by its
+// own score; ref_finish rescores them with the reference's arithmetic
+// (ref_common.hpp), keeps the best k and proves from the scan score of the
+// kp-th row and the error bounds that no other row can reach them.  A query
+// where the proof fails (ties or near-ties across the kp-th row, or
+// non-finite inputs) is marked for ref_scan, which rescans every row with
+// the reference arithmetic, starting from the k-th best reference score the
+// finish found.
+struct RefArgs {
+    int fmt;                    // 8: q8 rows, 4: q4 blocks
+    const void* codes;          // q8 [sets][n][pitch] int8; q4 [sets][n][d/2] bytes
+    const void* scales;         // q8 f32 [sets][n]; q4 f16 [sets][n][d/32]
+    const double* sqd;          // [sets][n] sqrt of each row's f64 square-sum
+    int64_t n;
+    int pitch;                  // bytes per row
+    int d;
+    int64_t set_stride;         // rows between consecutive queries' sets (0: shared)
+    const uint16_t* queries;    // f16 [nq][d]
+    int nq;
+    int op;                     // OP_DOT, OP_COSINE or OP_L2 (reference semantics)
+    int smallest;
+    int k;
+    int kp;                     // scan rows per query (k <= kp <= n)
+    const int32_t* cand_ids;    // [nq][kp] the scan's best rows, best first
+    const float* cand_scores;   // [nq][kp] their scan scores
+    float e_qd;                 // relative error bound of the scan's q^.d' term
+    float maxdn;                // max over rows of |d'|, as stored
+    float maxdd;                // max over rows of |d'|^2, as stored
+    int32_t* out_ids;           // [nq][k]
+    float* out_scores;          // [nq][k] or nullptr
+    int* redo;                  // [nq] 1: the query goes to ref_scan
+    uint64_t* redo_tau;         // [nq] threshold key ref_scan starts from (0: none)
+};
+hipError_t launch_ref_finish(const RefArgs& a, hipStream_t s);
+// Reference scores of every row (score matrix: a.out_scores) or top-k with
+// the streaming reservoir and last-workgroup merge (ScanArgs as for the
+// streaming scans).  redo / redo_tau (may be null: every query, no bound).
+hipError_t launch_ref_scan(int fmt, int op, const ScanArgs& a, const double* sqd, const int* redo,
+                           const uint64_t* redo_tau, dim3 grid, size_t lds, hipStream_t s);
 
 // Arguments of the multi-query scan kernel (kernels_mq.hip): nq queries
 // against one shared candidate matrix, over rows [row_begin, row_end).

@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     constexpr int SEGS = (CHUNK * P + 1023) / 1024;  // 1 KB LDS segments per chunk tile
     constexpr int DPW = (SEGS + 3) / 4;              // 16-byte direct-to-LDS loads per wave per chunk
     constexpr int TILE = DPW * 4 * 1024;             // LDS bytes per tile
-    constexpr int NARR = OP == OP_DOT ? 1 : 2;       // per-row arrays: scale (+ |d| or |d|^2)
+    constexpr int NARR = (OP == OP_DOT || OP == OP_DOT16) ? 1 : 2;  // per-row arrays: scale (+ |d| or |d|^2)
     constexpr int CSA = (CHUNK + 63) / 64;           // 256-byte segments per array per chunk
     constexpr int CPW = (NARR * CSA + 3) / 4;        // 4-byte direct-to-LDS loads per wave per chunk
     constexpr int CTILE = CPW * 4 * 256;             // LDS bytes of a chunk's per-row constants
@@ -238,6 +238,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     };
     auto score_of = [&](float p, int lq, float rowc) {
         if (OP == OP_DOT) return fdiv_rn(fmul_rn(p, qa_s[lq]), 127.0f);
+        if (OP == OP_DOT16) return p;
         if (OP == OP_COSINE) {
             const float den = fmul_rn(a.qconst[q0 + lq].b, rowc);
             return den == 0.0f ? 0.0f : fdiv_rn(p, den);
@@ -366,7 +367,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         const float* ctile = consts + buf * (CTILE / 4);
         const int64_t row = c0 + wr * 32 + (lane & 31);
         const float scale = ctile[wr * 32 + (lane & 31)];
-        const float rowc = OP == OP_DOT ? 0.0f : ctile[CSA * 64 + wr * 32 + (lane & 31)];
+        const float rowc = NARR == 1 ? 0.0f : ctile[CSA * 64 + wr * 32 + (lane & 31)];
         // MFMAs of this wave's 32-row block, then its filter: one compare per
         // slot without branches, and the exact scores and keys only in a wave
         // that has a survivor
@@ -726,7 +727,7 @@ MqShape mq_shape(int op, int ks, int64_t nq) {
     s.chunk = (4 / s.wq) * 32;
     const int segs = (s.chunk * (ks * 32 + 16) + 1023) / 1024;
     s.tile = ((segs + 3) / 4) * 4 * 1024;
-    const int narr = op == OP_DOT ? 1 : 2;
+    const int narr = (op == OP_DOT || op == OP_DOT16) ? 1 : 2;
     const int ctile = ((narr * ((s.chunk + 63) / 64) + 3) / 4) * 4 * 256;
     const int vpw = s.tile / 4096 + ctile / 1024;
     s.tile_bytes = mq_nbuf(s.tile + ctile, vpw) * (s.tile + ctile);  // chunk tiles + row constants
@@ -774,6 +775,7 @@ static hipError_t launch_mq_op(const MqShape& sh, const MqArgs& a, dim3 grid, si
 
 hipError_t launch_mq_scan(int op, const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     if (op == OP_DOT) return launch_mq_op<OP_DOT, MQ_E8>(sh, a, grid, lds, s);
+    if (op == OP_DOT16) return launch_mq_op<OP_DOT16, MQ_E16>(sh, a, grid, lds, s);
     if (op == OP_COSINE) return launch_mq_op<OP_COSINE, MQ_E16>(sh, a, grid, lds, s);
     return launch_mq_op<OP_L2, MQ_E16>(sh, a, grid, lds, s);
 }

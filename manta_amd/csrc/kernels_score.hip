@@ -1,58 +1,38 @@
 // kernels_score.hip -- packed-candidate scoring for gfx950 (streaming path).
 //
 // One launch per fused score+top-k call.  Each workgroup (256 threads, 4
-// waves) encodes its query into LDS, then scores `rounds` x 256 candidate
-// rows against it.  q8 rows are read with coalesced 16-byte loads: L lanes
-// cover one row (L*16 contiguous bytes per load), C loads per lane per row,
-// so a wave moves 64*16 bytes per load instruction.  The int8 products run
-// on v_dot4 with the query codes held in registers; row sums are reduced
-// across the L lanes with xor shuffles and then transposed so that thread t
-// owns row t of the round.  The epilogue computes the exact f32 score of the
-// packed contract and either stores it (score matrix) or feeds the LDS top-k
-// reservoir.  In top-k mode each workgroup writes its k best keys; the last
-// workgroup of a query (atomic ticket) merges them into the final ids.
+// waves) scores `rounds` x 256 candidate rows against one query.  q8 rows
+// are read with coalesced 16-byte buffer loads: L lanes cover one row (L*16
+// contiguous bytes per load), C loads per lane per row, so a wave moves
+// 64*16 bytes per load instruction.  The int8 products run on v_dot4 with
+// the query codes held in registers (each lane encodes the columns it
+// multiplies); a DPP group sum over the L lanes leaves every lane of a group
+// the row total, and lane g*L + j keeps row g*L + j, so after a round each
+// lane owns one row for the epilogue.  The epilogue computes the f32 score
+// and either stores it (score matrix) or offers its key to per-wave sorted
+// register lists (k <= 64) or the LDS reservoir.  In top-k mode each
+// workgroup publishes its k best keys; the last workgroup of a query (atomic
+// ticket) merges them into the final ids.
 //
-// Score formulas (the CPU oracle restates them; reference semantics they
-// stand in for: dotRows / cosineRows / l2DistanceRows,
-// runtime/backend/tensor_ops.go:1366-1490):
+// Quantized-query scores (the CPU oracle restates them):
 //   q8 dot    (E8 query codes):  t = s_r*acc; t = t*qmax; score = t/127
-//   q8 cosine (E16 hi/lo codes): qd = (s_r*qs)*f32(acc); den = |q|*|d_r|;
-//                                score = den == 0 ? 0 : qd/den
-//   q8 l2     (E16):             score = sqrt(max(0, (qq + dd_r) - 2*qd))
+//             (BASELINE's q8 dot formula, the quantized-query dot);
+//   q8 E16 codes (hi/lo digits): qd = (s_r*qs)*f32(acc); dot16 = qd;
+//             cosine = den == 0 ? 0 : qd/den with den = |q|*|d_r|;
+//             l2 = sqrt(max(0, (qq + dd_r) - 2*qd));
 //   q4        (E16):             qd = qs * fma-chain over blocks of
 //                                f16scale_b * f32(acc_b); then as above.
+// The E16 scores rank rows for the reference-semantics top-k, which
+// rescores the best of them with the reference's arithmetic
+// (kernels_ref.hip).
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "q4_common.hpp"
+#include "scan_common.hpp"
 
 namespace manta {
 
 // ------------------------------------------------------------ query codes
-
-// E8 (q8 dot): qmax = max(1, maxabs), code = clamp(round((q*127)/qmax)).
-__device__ __forceinline__ int code_e8(float x, float qmax) {
-    float r = round_half_away(fdiv_rn(fmul_rn(x, 127.0f), qmax));
-    return (int)fminf(127.0f, fmaxf(-127.0f, r));
-}
-
-// E16: code = clamp(round(q*(32639/maxabs)), +-32639), split 256*hi + lo
-// with lo the signed low byte.
-__device__ __forceinline__ int code_e16(float x, float inv) {
-    float r = round_half_away(fmul_rn(x, inv));
-    return (int)fminf(32639.0f, fmaxf(-32639.0f, r));
-}
-
-__device__ __forceinline__ QConst e16_consts(float maxabs, long long ss) {
-    QConst k{0.0f, 0.0f, 0.0f, 0.0f};
-    if (maxabs != 0.0f) {
-        const float qs = fdiv_rn(maxabs, 32639.0f);
-        const double dss = (double)ss;
-        k.a = qs;
-        k.b = (float)__dmul_rn(__dsqrt_rn(dss), (double)qs);
-        k.c = (float)__dmul_rn(__dmul_rn(dss, (double)qs), (double)qs);
-    }
-    return k;
-}
 
 // q4 digit planes are permuted per 8 columns to [c0 c2 c4 c6 c1 c3 c5 c7]
 // so that the nibble unpack below feeds v_dot4 without shuffling.
@@ -223,6 +203,7 @@ __device__ __forceinline__ float q8_epilogue(int acc_or_hi, int lo, float scale,
     // f32(256*hi + lo) with one rounding: both terms are exact in f32.
     float dotf = __fmaf_rn(256.0f, (float)acc_or_hi, (float)lo);
     float qd = fmul_rn(fmul_rn(scale, k.a), dotf);
+    if (OP == OP_DOT16) return qd;
     if (OP == OP_COSINE) {
         float den = fmul_rn(k.b, dnorm);
         return den == 0.0f ? 0.0f : fdiv_rn(qd, den);
@@ -249,12 +230,6 @@ struct ScanLds {
     int last;
 };
 
-// Kernels that keep the encoded query in registers.
-struct ScanTopkLds {
-    TopKShared st;
-    int last;
-};
-
 // Store the score, or offer it to the reservoir.
 __device__ __forceinline__ void emit_round(float score, bool valid, int64_t row, int64_t n, int qi,
                                            float* __restrict__ out_scores, uint64_t* keys,
@@ -265,61 +240,6 @@ __device__ __forceinline__ void emit_round(float score, bool valid, int64_t row,
     }
     uint64_t key = valid ? make_key(score, (uint32_t)row, smallest) : 0ull;
     topk_offer(key, tau, keys, st);
-}
-
-// End of a top-k scan workgroup: publish its k best keys; the last
-// workgroup of the query (ticket == gridDim.x - 1) merges every part into
-// the final sorted ids / scores and resets the ticket for the next call.
-// Publication avoids device-wide fences (each one writes back and
-// invalidates a whole XCD L2): the keys are stored write-through at agent
-// scope (sc1), every thread waits for its stores to complete before the
-// barrier, the ticket is an agent-scope atomic, and the merging workgroup
-// reads the parts with agent-scope (sc1) loads.
-template <class SL>
-__device__ inline void finish_topk(const ScanArgs& a, uint64_t* keys, SL& S, int qi) {
-    __syncthreads();
-    topk_compact(keys, &S.st, a.k);
-    const int64_t per_q = (int64_t)gridDim.x * a.k;
-    uint64_t* dst = a.partial + (int64_t)qi * per_q + (int64_t)blockIdx.x * a.k;
-    for (int i = threadIdx.x; i < a.k; i += blockDim.x)
-        __hip_atomic_store(dst + i, i < S.st.cnt ? keys[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        S.last = __hip_atomic_fetch_add(&a.tickets[qi], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 gridDim.x - 1;
-    __syncthreads();
-    if (!S.last) return;
-    const uint64_t* src = a.partial + (int64_t)qi * per_q;
-    topk_init(keys, &S.st);
-    if (per_q <= a.lds_keys) {
-        // every part fits in LDS: one batch of loads, empty slots dropped
-        for (int64_t base = 0; base < per_q; base += blockDim.x) {
-            const int64_t i = base + threadIdx.x;
-            const uint64_t key =
-                i < per_q ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-            topk_offer(key, 0ull, keys, &S.st);
-        }
-        __syncthreads();
-    } else {
-        for (int64_t base = 0; base < per_q; base += blockDim.x) {
-            const int64_t i = base + threadIdx.x;
-            const uint64_t key =
-                i < per_q ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-            topk_offer(key, S.st.tau, keys, &S.st);
-            __syncthreads();
-            topk_maybe_compact(keys, &S.st, a.k, a.cap);
-        }
-    }
-    topk_compact(keys, &S.st, a.k);
-    const int kept = S.st.cnt;
-    topk_sort(keys, kept);
-    for (int i = threadIdx.x; i < a.k; i += blockDim.x) {
-        const uint64_t key = i < kept ? keys[i] : 0ull;
-        a.out_ids[(int64_t)qi * a.k + i] = key ? (int32_t)key_index(key) : -1;
-        if (a.out_topk_scores) a.out_topk_scores[(int64_t)qi * a.k + i] = key ? key_score(key, a.smallest) : 0.0f;
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[qi], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // End of a top-k scan workgroup on the wave-list path (k <= 64): the waves'
@@ -749,6 +669,7 @@ static hipError_t launch_q8_op(const ScanArgs& a, dim3 grid, size_t lds, hipStre
 hipError_t launch_q8_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     switch (op) {
         case OP_DOT: return launch_q8_op<OP_DOT>(a, grid, lds, s);
+        case OP_DOT16: return launch_q8_op<OP_DOT16>(a, grid, lds, s);
         case OP_COSINE: return launch_q8_op<OP_COSINE>(a, grid, lds, s);
         default: return launch_q8_op<OP_L2>(a, grid, lds, s);
     }

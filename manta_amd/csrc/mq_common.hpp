@@ -24,7 +24,8 @@ __device__ __forceinline__ float loosen_up(float x) {
 }
 
 // Pre-score bound of one query from its threshold key.  dot compares s*acc
-// against (tau*127)/qmax; l2 compares dist^2 against tau^2; cosine compares
+// against (tau*127)/qmax; dot16 compares qd against tau; l2 compares dist^2
+// against tau^2; cosine compares
 // q.d against (tau*|q|) * |d| (the |d| factor is applied per row).  No
 // threshold lets everything through.
 template <int OP>
@@ -36,6 +37,7 @@ __device__ __forceinline__ float mq_bound(uint64_t tk, const QConst& qc, bool sm
         const float tt = fdiv_rn(fmul_rn(ts, 127.0f), qc.a);
         return smallest ? loosen_up(tt) : loosen_down(tt);
     }
+    if (OP == OP_DOT16) return smallest ? loosen_up(ts) : loosen_down(ts);
     if (OP == OP_L2) {
         const float t2 = fmul_rn(ts, ts);
         return smallest ? loosen_up(t2) : loosen_down(t2);

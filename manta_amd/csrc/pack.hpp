@@ -105,6 +105,28 @@ inline void q8_row_consts(const int8_t* codes, float scale, int64_t d, float* dn
     *dd = (float)((double)ss * s * s);
 }
 
+// The reference's per-row norm term of cosineRows (tensor_ops.go:1411-1421):
+// sqrt of the f64 sum, in column order, of the squared f32 values the row
+// stands for (q8: code*scale in f32; q4: code*f16scale, exact).  Each square
+// is exact in f64.
+inline double q8_row_ref_norm(const int8_t* codes, float scale, int64_t d) {
+    double s = 0.0;
+    for (int64_t c = 0; c < d; c++) {
+        const double v = (double)((float)codes[c] * scale);
+        s = s + v * v;
+    }
+    return std::sqrt(s);
+}
+
+inline double q4_row_ref_norm(const uint8_t* row, const uint16_t* scales, int64_t d) {
+    double s = 0.0;
+    for (int64_t c = 0; c < d; c++) {
+        const double v = (double)((float)q4_nibble(row, c) * half_to_float(scales[c / 32]));
+        s = s + v * v;
+    }
+    return std::sqrt(s);
+}
+
 inline void q4_row_consts(const uint8_t* row, const uint16_t* scales, int64_t d, float* dnorm,
                           float* dd) {
     double acc = 0.0;

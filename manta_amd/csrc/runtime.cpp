@@ -42,6 +42,10 @@ struct MantaRocm {
     hipStream_t stream = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // reference-semantics top-k: the scan's candidates and the finish's
+    // verdicts, kept apart from ws (which the scans and the rescan use)
+    void* ws_ref = nullptr;
+    size_t ws_ref_bytes = 0;
     MantaRocmStats stats{};
     // first out-of-range gather index seen by a device gather (flag | index)
     unsigned long long* err_word = nullptr;
@@ -67,6 +71,13 @@ struct MantaRocmCandidates {
     void* scales = nullptr;
     float* dnorm = nullptr;
     float* dd = nullptr;
+    double* sqd = nullptr;  // [sets][n] sqrt of each row's f64 square-sum (reference cosine)
+    float maxdn = 0.0f;     // max over rows of dnorm
+    float maxdd = 0.0f;     // max over rows of dd
+    // the quantized-query scans may rank rows for reference-semantics
+    // top-k: every scale finite and zero or within [2^-60, 2^60] (the
+    // scans' error bounds hold without underflow or overflow)
+    bool ref_ranked = false;
     mutable size_t bytes = 0;
     bool scales_finite = false;  // every row / block scale is finite (the 512-query kernel needs it)
     // q4: int8 shadow for many-query top-k (built on first use): codes
@@ -152,19 +163,27 @@ hipEvent_t pooled_event(MantaRocm* rt) {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-int ensure_workspace(MantaRocm* rt, size_t bytes, char** err) {
-    if (bytes <= rt->ws_bytes) return MANTA_ROCM_OK;
-    if (rt->ws) {
+int grow_buffer(MantaRocm* rt, void** buf, size_t* have, size_t bytes, char** err) {
+    if (bytes <= *have) return MANTA_ROCM_OK;
+    if (*buf) {
         HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
-        HIP_TRY(hipFree(rt->ws), "hipFree");
-        rt->ws = nullptr;
-        rt->ws_bytes = 0;
+        HIP_TRY(hipFree(*buf), "hipFree");
+        *buf = nullptr;
+        *have = 0;
     }
     size_t want = align_up(bytes, (size_t)1 << 20);
-    HIP_TRY(hipMalloc(&rt->ws, want), "hipMalloc(workspace)");
-    rt->ws_bytes = want;
-    rt->stats.workspace_bytes = want;
+    HIP_TRY(hipMalloc(buf, want), "hipMalloc(workspace)");
+    *have = want;
+    rt->stats.workspace_bytes = rt->ws_bytes + rt->ws_ref_bytes;
     return MANTA_ROCM_OK;
+}
+
+int ensure_workspace(MantaRocm* rt, size_t bytes, char** err) {
+    return grow_buffer(rt, &rt->ws, &rt->ws_bytes, bytes, err);
+}
+
+int ensure_ref_workspace(MantaRocm* rt, size_t bytes, char** err) {
+    return grow_buffer(rt, &rt->ws_ref, &rt->ws_ref_bytes, bytes, err);
 }
 
 // Carve a workspace into aligned slices.
@@ -243,6 +262,8 @@ int free_candidates_memory(MantaRocmCandidates* c) {
     if (c->scales) (void)hipFree(c->scales);
     if (c->dnorm) (void)hipFree(c->dnorm);
     if (c->dd) (void)hipFree(c->dd);
+    if (c->sqd) (void)hipFree(c->sqd);
+    c->sqd = nullptr;
     if (c->shadow_codes) (void)hipFree(c->shadow_codes);
     if (c->shadow_scales) (void)hipFree(c->shadow_scales);
     if (c->shadow_info) (void)hipFree(c->shadow_info);
@@ -252,6 +273,16 @@ int free_candidates_memory(MantaRocmCandidates* c) {
     c->shadow_scales = nullptr;
     c->shadow_info = nullptr;
     return 0;
+}
+
+void set_row_maxima(MantaRocmCandidates* c, const std::vector<float>& dnorm, const std::vector<float>& dd) {
+    float mn = 0.0f, md = 0.0f;
+    for (size_t i = 0; i < dnorm.size(); i++) {
+        mn = std::fmax(mn, dnorm[i]);
+        md = std::fmax(md, dd[i]);
+    }
+    c->maxdn = mn;
+    c->maxdd = md;
 }
 
 }  // namespace
@@ -326,6 +357,7 @@ void manta_rocm_destroy(MantaRocm* rt) {
     for (auto e : rt->span_ev)
         if (e) (void)hipEventDestroy(e);
     if (rt->ws) (void)hipFree(rt->ws);
+    if (rt->ws_ref) (void)hipFree(rt->ws_ref);
     if (rt->err_word) (void)hipFree(rt->err_word);
     if (rt->tickets) (void)hipFree(rt->tickets);
     if (rt->own_stream) (void)hipStreamDestroy(rt->own_stream);
@@ -481,25 +513,35 @@ int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* sca
     const int64_t rows = sets * n;
     const int pitch = (int)align_up((size_t)d, 16);
     std::vector<float> dnorm((size_t)rows), dd((size_t)rows);
+    std::vector<double> sqd((size_t)rows);
     parallel_rows(rows, [&](int64_t a, int64_t b) {
-        for (int64_t r = a; r < b; r++)
+        for (int64_t r = a; r < b; r++) {
             manta::q8_row_consts(codes + r * d, scales[r], d, &dnorm[(size_t)r], &dd[(size_t)r]);
+            sqd[(size_t)r] = manta::q8_row_ref_norm(codes + r * d, scales[r], d);
+        }
     });
     auto* c = new MantaRocmCandidates();
     c->rt = rt;
     c->format = MANTA_ROCM_Q8_ROWS;
-    bool finite = true;
-    for (int64_t r = 0; r < rows && finite; r++) finite = std::isfinite(scales[r]);
+    bool finite = true, ranked = true;
+    for (int64_t r = 0; r < rows; r++) {
+        const float a = std::fabs(scales[r]);
+        finite = finite && std::isfinite(scales[r]);
+        ranked = ranked && (a == 0.0f || (a >= 0x1p-60f && a <= 0x1p60f));
+    }
     c->scales_finite = finite;
+    c->ref_ranked = finite && ranked;
+    set_row_maxima(c, dnorm, dd);
     c->sets = sets;
     c->n = n;
     c->d = d;
     c->pitch = pitch;
-    c->bytes = (size_t)rows * pitch + (size_t)rows * 12;
+    c->bytes = (size_t)rows * pitch + (size_t)rows * 20;
     hipError_t e = hipMalloc(&c->codes, (size_t)rows * pitch);
     if (e == hipSuccess) e = hipMalloc(&c->scales, (size_t)rows * 4);
     if (e == hipSuccess) e = hipMalloc((void**)&c->dnorm, (size_t)rows * 4);
     if (e == hipSuccess) e = hipMalloc((void**)&c->dd, (size_t)rows * 4);
+    if (e == hipSuccess) e = hipMalloc((void**)&c->sqd, (size_t)rows * 8);
     if (e == hipSuccess) {
         if (pitch == d) {
             e = hipMemcpy(c->codes, codes, (size_t)rows * d, hipMemcpyHostToDevice);
@@ -512,6 +554,7 @@ int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* sca
     if (e == hipSuccess) e = hipMemcpy(c->scales, scales, (size_t)rows * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(c->dnorm, dnorm.data(), (size_t)rows * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(c->dd, dd.data(), (size_t)rows * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(c->sqd, sqd.data(), (size_t)rows * 8, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         free_candidates_memory(c);
         delete c;
@@ -562,9 +605,12 @@ int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16
     const int pitch = (int)(d / 2);
     const int nb = (int)(d / 32);
     std::vector<float> dnorm((size_t)rows), dd((size_t)rows);
+    std::vector<double> sqd((size_t)rows);
     parallel_rows(rows, [&](int64_t a, int64_t b) {
-        for (int64_t r = a; r < b; r++)
+        for (int64_t r = a; r < b; r++) {
             manta::q4_row_consts(packed + r * pitch, scales + r * nb, d, &dnorm[(size_t)r], &dd[(size_t)r]);
+            sqd[(size_t)r] = manta::q4_row_ref_norm(packed + r * pitch, scales + r * nb, d);
+        }
     });
     auto* c = new MantaRocmCandidates();
     c->rt = rt;
@@ -572,20 +618,24 @@ int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16
     bool finite = true;  // f16 exponent field below all-ones
     for (int64_t i = 0; i < rows * nb && finite; i++) finite = (scales[i] & 0x7C00u) != 0x7C00u;
     c->scales_finite = finite;
+    c->ref_ranked = finite;  // finite f16 scales are within [2^-24, 2^16]
+    set_row_maxima(c, dnorm, dd);
     c->sets = sets;
     c->n = n;
     c->d = d;
     c->pitch = pitch;
     c->nb = nb;
-    c->bytes = (size_t)rows * (pitch + nb * 2 + 8);
+    c->bytes = (size_t)rows * (pitch + nb * 2 + 16);
     hipError_t e = hipMalloc(&c->codes, (size_t)rows * pitch);
     if (e == hipSuccess) e = hipMalloc(&c->scales, (size_t)rows * nb * 2);
     if (e == hipSuccess) e = hipMalloc((void**)&c->dnorm, (size_t)rows * 4);
     if (e == hipSuccess) e = hipMalloc((void**)&c->dd, (size_t)rows * 4);
+    if (e == hipSuccess) e = hipMalloc((void**)&c->sqd, (size_t)rows * 8);
     if (e == hipSuccess) e = hipMemcpy(c->codes, packed, (size_t)rows * pitch, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(c->scales, scales, (size_t)rows * nb * 2, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(c->dnorm, dnorm.data(), (size_t)rows * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(c->dd, dd.data(), (size_t)rows * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(c->sqd, sqd.data(), (size_t)rows * 8, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         free_candidates_memory(c);
         delete c;
@@ -637,10 +687,32 @@ ScanArgs scan_args(const MantaRocmCandidates* c, const uint16_t* q) {
     return a;
 }
 
-int check_score_args(const MantaRocmCandidates* c, int op, const void* q, int64_t nq, char** err) {
+// A score op as the ABI takes it: the builtin (dot / cosine / l2_distance)
+// and the MANTA_ROCM_QUANTIZED_QUERY flag.  scan: the device op of the
+// quantized-query scans (q8 dot: E8 codes when the caller asked for them,
+// else E16; every other op E16); ref: the reference arithmetic's.
+struct ScoreOp {
+    int op = 0;
+    bool quant = false;
+    int scan = 0;
+    int ref = 0;
+};
+
+ScoreOp parse_op(const MantaRocmCandidates* c, int op_in) {
+    ScoreOp so;
+    so.op = op_in & ~MANTA_ROCM_QUANTIZED_QUERY;
+    so.quant = (op_in & MANTA_ROCM_QUANTIZED_QUERY) != 0;
+    so.ref = so.op == MANTA_ROCM_DOT ? manta::OP_DOT : (so.op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
+    so.scan = so.ref;
+    if (so.op == MANTA_ROCM_DOT && c->format == MANTA_ROCM_Q8_ROWS && !so.quant) so.scan = manta::OP_DOT16;
+    return so;
+}
+
+int check_score_args(const MantaRocmCandidates* c, int op_in, const void* q, int64_t nq, char** err) {
     if (!c) return fail(err, MANTA_ROCM_ERROR, "nil score input");
+    const int op = op_in & ~MANTA_ROCM_QUANTIZED_QUERY;
     if (op < MANTA_ROCM_DOT || op > MANTA_ROCM_L2_DISTANCE)
-        return fail(err, MANTA_ROCM_ERROR, "unknown score op %d", op);
+        return fail(err, MANTA_ROCM_ERROR, "unknown score op %d", op_in);
     if (!q) return fail(err, MANTA_ROCM_ERROR, "nil score input");
     if (nq <= 0) return fail(err, MANTA_ROCM_ERROR, "score expects at least one query");
     if (c->sets != 1 && c->sets != nq)
@@ -660,6 +732,51 @@ int check_score_args(const MantaRocmCandidates* c, int op, const void* q, int64_
 int choose_rounds(int64_t tiles, int64_t nq) {
     int64_t r = (tiles * nq + 511) / 512;
     return (int)std::max<int64_t>(1, std::min<int64_t>(64, r));
+}
+
+// Launch shape of a streaming top-k (one query per blockIdx.y): `parts`
+// workgroups of `rounds` x 256 rows per query, and the LDS reservoir.  A
+// reservoir that holds every row of the workgroup needs no compaction (and
+// no barrier) between rounds.
+struct StreamTopk {
+    int rounds = 1;
+    int64_t parts = 1;
+    int cap = 0;
+    int mid_compact = 1;
+    int lds_keys = 0;
+};
+
+StreamTopk stream_topk_shape(const MantaRocmCandidates* c, int64_t nq, int64_t k, int rounds) {
+    StreamTopk st;
+    const int64_t tiles = (c->n + 255) / 256;
+    st.rounds = rounds;
+    st.parts = (tiles + rounds - 1) / rounds;
+    st.cap = cap_for_k(k);
+    if (k + (int64_t)rounds * 256 <= manta::kMaxCapKeys) {
+        st.cap = cap_for_k(k + (int64_t)(rounds - 1) * 256);
+        st.mid_compact = 0;
+    }
+    // the merge loads all parts at once when they fit in LDS (<= 4096 keys)
+    st.lds_keys = (int)std::max<int64_t>(st.cap, st.parts * k <= manta::kMaxCapKeys ? st.parts * k : 0);
+    (void)nq;
+    return st;
+}
+
+// Streaming top-k arguments; the parts' keys go to the runtime workspace.
+ScanArgs stream_topk_args(MantaRocm* rt, const MantaRocmCandidates* c, const uint16_t* q, const StreamTopk& st,
+                          int64_t k, int order, int32_t* out_ids, float* out_scores) {
+    ScanArgs a = scan_args(c, q);
+    a.mid_compact = st.mid_compact;
+    a.rounds = st.rounds;
+    a.partial = (uint64_t*)rt->ws;
+    a.tickets = rt->tickets;
+    a.out_ids = out_ids;
+    a.out_topk_scores = out_scores;
+    a.k = (int)k;
+    a.cap = st.cap;
+    a.lds_keys = st.lds_keys;
+    a.smallest = order == MANTA_ROCM_SMALLEST;
+    return a;
 }
 
 int launch_scan(MantaRocm* rt, const MantaRocmCandidates* c, int op, const ScanArgs& a, dim3 grid,
@@ -729,8 +846,8 @@ bool mq8_fits(int pitch, int64_t k) {
 
 // q4 cosine / dot top-k with at least 256 queries goes through the int8
 // shadow (built on first use).
-bool q4_shadow_wanted(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k) {
-    return c->format == MANTA_ROCM_Q4_BLOCKS && c->sets == 1 && (op == MANTA_ROCM_COSINE || op == MANTA_ROCM_DOT) &&
+bool q4_shadow_wanted(const MantaRocmCandidates* c, int dop, int64_t nq, int64_t k) {
+    return c->format == MANTA_ROCM_Q4_BLOCKS && c->sets == 1 && (dop == manta::OP_COSINE || dop == manta::OP_DOT) &&
            nq >= 256 && c->d <= 384 && c->scales_finite && mq8_fits((int)align_up((size_t)c->d, 128), k);
 }
 
@@ -769,10 +886,9 @@ void ensure_q4_shadow(MantaRocm* rt, const MantaRocmCandidates* c) {
     rt->stats.candidate_bytes += extra;
 }
 
-MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool topk) {
+MqPlan mq_plan(const MantaRocmCandidates* c, int dop, int64_t nq, int64_t k, bool topk) {
     MqPlan p;
     if (c->sets != 1 || nq < 8) return p;
-    const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
     // the 16x16x64 kernel: 512-query groups, or 256 with the rows of a chunk
     // split over two wave groups
     const int ws8 = nq >= 512 ? 1 : 2;
@@ -785,7 +901,7 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int op, int64_t nq, int64_t k, bool
         }
     } else {
         p.q4 = true;
-        if (topk && c->shadow_state == 1 && q4_shadow_wanted(c, op, nq, k)) {
+        if (topk && c->shadow_state == 1 && q4_shadow_wanted(c, dop, nq, k)) {
             p.shadow = true;
             p.sh = manta::mq8_shape(c->shadow_pitch, ws8, true);
         } else {
@@ -861,7 +977,7 @@ hipError_t launch_mq_pass(const MqPlan& p, int dop, const manta::MqArgs& a, int 
 }
 
 // Encode queries to the global digit planes, then run the multi-query passes.
-int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const uint16_t* q, int64_t nq,
+int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, const uint16_t* q, int64_t nq,
            int64_t k, const MqPlan& p, float* out_scores, int32_t* out_ids, float* out_topk_scores,
            char** err) {
     // query planes: E8 codes or E16 digits, one row per query, as wide as a
@@ -887,13 +1003,12 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const
     uint64_t* reg = cv.take<uint64_t>(regions ? regions : 1);
     int* cnt = cv.take<int>(counts ? counts : 1);
     float* qb = cv.take<float>((size_t)nq * 2);
-    const int dop = op == MANTA_ROCM_DOT ? manta::OP_DOT : (op == MANTA_ROCM_COSINE ? manta::OP_COSINE : manta::OP_L2);
     if (p.shadow) {
         LAUNCH_TRY(manta::launch_query_encode_shadow(q, (int)nq, (int)c->d, width, dop, c->shadow_info, c8, hi, lo,
                                                      qc, qb, rt->stream),
                    "query_encode");
     } else {
-        const int e16 = p.q4 ? 2 : (op != MANTA_ROCM_DOT ? 1 : 0);
+        const int e16 = p.q4 ? 2 : (dop != manta::OP_DOT ? 1 : 0);
         LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, width, e16, c8, hi, lo, qc, rt->stream),
                    "query_encode");
     }
@@ -980,15 +1095,143 @@ int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* c, int op, const 
     int rc = check_score_args(c, op, q, nq, err);
     if (rc) return rc;
     if (!out) return fail(err, MANTA_ROCM_ERROR, "nil score output");
-    const MqPlan plan = mq_plan(c, op, nq, 0, false);
-    if (plan.use) return run_mq(rt, c, op, MANTA_ROCM_LARGEST, q, nq, 0, plan, out, nullptr, nullptr, err);
-    ScanArgs a = scan_args(c, q);
+    const ScoreOp so = parse_op(c, op);
     const int64_t tiles = (c->n + 255) / 256;
+    if (!so.quant) {
+        // the reference arithmetic for every (query, row)
+        ScanArgs a = scan_args(c, q);
+        a.rounds = (int)std::max<int64_t>(1, std::min<int64_t>(16, tiles * nq / 2048));
+        a.out_scores = out;
+        const int64_t parts = (tiles + a.rounds - 1) / a.rounds;
+        LAUNCH_TRY(manta::launch_ref_scan(c->format == MANTA_ROCM_Q8_ROWS ? 8 : 4, so.ref, a, c->sqd, nullptr,
+                                          nullptr, dim3((unsigned)parts, (unsigned)nq), 0, rt->stream),
+                   "ref_scan");
+        return MANTA_ROCM_OK;
+    }
+    const MqPlan plan = mq_plan(c, so.scan, nq, 0, false);
+    if (plan.use) return run_mq(rt, c, so.scan, MANTA_ROCM_LARGEST, q, nq, 0, plan, out, nullptr, nullptr, err);
+    ScanArgs a = scan_args(c, q);
     a.rounds = choose_rounds(tiles, nq);
     a.out_scores = out;
     const int64_t parts = (tiles + a.rounds - 1) / a.rounds;
-    return launch_scan(rt, c, op, a, dim3((unsigned)parts, (unsigned)nq), 0, err);
+    return launch_scan(rt, c, so.scan, a, dim3((unsigned)parts, (unsigned)nq), 0, err);
 }
+
+}  // extern "C"
+
+namespace {
+
+// Top-k of the quantized-query scan scores (device op dop): the
+// multi-query passes, or the streaming scan with its fused top-k.
+int scan_topk(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, const uint16_t* q, int64_t nq,
+              int64_t k, int32_t* out_ids, float* out_scores, int64_t* out_acc, char** err) {
+    if (q4_shadow_wanted(c, dop, nq, k)) ensure_q4_shadow(rt, c);
+    const MqPlan plan = mq_plan(c, dop, nq, k, true);
+    const int e16 = dop != manta::OP_DOT ? 1 : 0;
+    if (plan.use) {
+        int rc = run_mq(rt, c, dop, order, q, nq, k, plan, nullptr, out_ids, out_scores, err);
+        if (rc) return rc;
+        if (out_acc)
+            LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch, 0, c->n, (int)c->d, q, out_ids,
+                                                (int)k, (int)nq, e16, out_acc, rt->stream),
+                       "q8_rescore");
+        return MANTA_ROCM_OK;
+    }
+    StreamTopk st = stream_topk_shape(c, nq, k, choose_rounds((c->n + 255) / 256, nq));
+    int rc = ensure_workspace(rt, (size_t)nq * st.parts * k * 8 + 256, err);
+    if (rc) return rc;
+    ScanArgs a = stream_topk_args(rt, c, q, st, k, order, out_ids, out_scores);
+    // small k on the coalesced q8 kernel: sorted per-wave lists in registers
+    // (LDS only for merging the waves' lists)
+    if (c->format == MANTA_ROCM_Q8_ROWS && manta::q8_scan_coalesced(c->pitch) && k <= manta::kWaveListMaxK) {
+        a.wave_lists = 1;
+        a.lds_keys = 256;
+    }
+    rc = launch_scan(rt, c, dop, a, dim3((unsigned)st.parts, (unsigned)nq), (size_t)a.lds_keys * 8, err);
+    if (rc) return rc;
+    if (out_acc) {
+        LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch, c->sets == 1 ? 0 : c->n, c->n,
+                                            (int)c->d, q, out_ids, (int)k, (int)nq, e16, out_acc, rt->stream),
+                   "q8_rescore");
+    }
+    return MANTA_ROCM_OK;
+}
+
+// Reference-semantics top-k.  The quantized-query scan returns its best kp
+// rows; ref_finish rescores them with the reference arithmetic and proves
+// (or not) that they hold the reference's best k; queries it cannot prove
+// are rescanned in full with the reference arithmetic.  Candidates whose
+// scales lie outside the range the scan's error bounds assume skip the scan
+// and are rescanned in full.
+int ref_topk(MantaRocm* rt, const MantaRocmCandidates* c, const ScoreOp& so, int order, const uint16_t* q,
+             int64_t nq, int64_t k, int32_t* out_ids, float* out_scores, char** err) {
+    const int fmt = c->format == MANTA_ROCM_Q8_ROWS ? 8 : 4;
+    const int smallest = order == MANTA_ROCM_SMALLEST;
+    int* redo = nullptr;
+    uint64_t* redo_tau = nullptr;
+    if (c->ref_ranked) {
+        // a margin of rows past the k-th: ties and near-ties of the scan
+        // scores across the kp-th row are what would send a query to the
+        // full rescan
+        const int64_t kp = std::min<int64_t>(std::min<int64_t>(c->n, kMaxDeviceK),
+                                             k + std::max<int64_t>(16, k / 16));
+        const size_t need = (size_t)nq * kp * 8 + (size_t)nq * 12 + 1024;
+        int rc = ensure_ref_workspace(rt, need, err);
+        if (rc) return rc;
+        Carver cv(rt->ws_ref);
+        int32_t* cand_ids = cv.take<int32_t>((size_t)nq * kp);
+        float* cand_scores = cv.take<float>((size_t)nq * kp);
+        redo = cv.take<int>((size_t)nq);
+        redo_tau = cv.take<uint64_t>((size_t)nq);
+        rc = scan_topk(rt, c, so.scan, order, q, nq, kp, cand_ids, cand_scores, nullptr, err);
+        if (rc) return rc;
+        manta::RefArgs ra{};
+        ra.fmt = fmt;
+        ra.codes = c->codes;
+        ra.scales = c->scales;
+        ra.sqd = c->sqd;
+        ra.n = c->n;
+        ra.pitch = c->pitch;
+        ra.d = (int)c->d;
+        ra.set_stride = c->sets == 1 ? 0 : c->n;
+        ra.queries = q;
+        ra.nq = (int)nq;
+        ra.op = so.ref;
+        ra.smallest = smallest;
+        ra.k = (int)k;
+        ra.kp = (int)kp;
+        ra.cand_ids = cand_ids;
+        ra.cand_scores = cand_scores;
+        // relative error of the scan's q^.d' term: q8 three f32 roundings
+        // (scale*qs, f32(acc), the product); q4 an fma per block plus the
+        // final product
+        ra.e_qd = fmt == 8 ? 3.1f * 0x1p-24f : ((float)c->nb + 1.2f) * 0x1p-24f;
+        ra.maxdn = c->maxdn;
+        ra.maxdd = c->maxdd;
+        ra.out_ids = out_ids;
+        ra.out_scores = out_scores;
+        ra.redo = redo;
+        ra.redo_tau = redo_tau;
+        LAUNCH_TRY(manta::launch_ref_finish(ra, rt->stream), "ref_finish");
+    }
+    // the full rescan (workgroups of proven queries exit at once): about 2048
+    // workgroups in all, at least one per query
+    const int64_t tiles = (c->n + 255) / 256;
+    const int64_t want_parts = std::max<int64_t>(1, std::min<int64_t>(tiles, 2048 / nq));
+    const int rounds = (int)std::max<int64_t>(1, std::min<int64_t>(64, (tiles + want_parts - 1) / want_parts));
+    StreamTopk st = stream_topk_shape(c, nq, k, rounds);
+    int rc = ensure_workspace(rt, (size_t)nq * st.parts * k * 8 + 256, err);
+    if (rc) return rc;
+    ScanArgs a = stream_topk_args(rt, c, q, st, k, order, out_ids, out_scores);
+    LAUNCH_TRY(manta::launch_ref_scan(fmt, so.ref, a, c->sqd, redo, redo_tau,
+                                      dim3((unsigned)st.parts, (unsigned)nq), (size_t)a.lds_keys * 8, rt->stream),
+               "ref_scan");
+    return MANTA_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
 
 int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order,
                           const uint16_t* q, int64_t nq, int64_t k, int32_t* out_ids,
@@ -1005,60 +1248,11 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, i
         return fail(err, MANTA_ROCM_UNSUPPORTED, "topk limit %lld exceeds the device maximum %lld",
                     (long long)k, (long long)kMaxDeviceK);
     if (!out_ids) return fail(err, MANTA_ROCM_ERROR, "nil topk output");
-    if (out_acc && c->format != MANTA_ROCM_Q8_ROWS)
-        return fail(err, MANTA_ROCM_ERROR, "accumulator output needs q8 candidates");
-    if (q4_shadow_wanted(c, op, nq, k)) ensure_q4_shadow(rt, c);
-    const MqPlan plan = mq_plan(c, op, nq, k, true);
-    if (plan.use) {
-        rc = run_mq(rt, c, op, order, q, nq, k, plan, nullptr, out_ids, out_scores, err);
-        if (rc) return rc;
-        if (out_acc)
-            LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch, 0, c->n, (int)c->d, q, out_ids,
-                                                (int)k, (int)nq, op != MANTA_ROCM_DOT ? 1 : 0, out_acc,
-                                                rt->stream),
-                       "q8_rescore");
-        return MANTA_ROCM_OK;
-    }
-    const int64_t tiles = (c->n + 255) / 256;
-    const int rounds = choose_rounds(tiles, nq);
-    const int64_t parts = (tiles + rounds - 1) / rounds;
-    // A reservoir that holds every row of the workgroup needs no compaction
-    // (and no barrier) between rounds.
-    int cap = cap_for_k(k);
-    int mid_compact = 1;
-    if (k + (int64_t)rounds * 256 <= manta::kMaxCapKeys) {
-        cap = cap_for_k(k + (int64_t)(rounds - 1) * 256);
-        mid_compact = 0;
-    }
-    rc = ensure_workspace(rt, (size_t)nq * parts * k * 8 + 256, err);
-    if (rc) return rc;
-    ScanArgs a = scan_args(c, q);
-    a.mid_compact = mid_compact;
-    a.rounds = rounds;
-    a.partial = (uint64_t*)rt->ws;
-    a.tickets = rt->tickets;
-    a.out_ids = out_ids;
-    a.out_topk_scores = out_scores;
-    a.k = (int)k;
-    a.cap = cap;
-    // the merge loads all parts at once when they fit in LDS (<= 4096 keys)
-    a.lds_keys = (int)std::max<int64_t>(cap, parts * k <= manta::kMaxCapKeys ? parts * k : 0);
-    a.smallest = order == MANTA_ROCM_SMALLEST;
-    // small k on the coalesced q8 kernel: sorted per-wave lists in registers
-    // (LDS only for merging the waves' lists)
-    if (c->format == MANTA_ROCM_Q8_ROWS && manta::q8_scan_coalesced(c->pitch) && k <= manta::kWaveListMaxK) {
-        a.wave_lists = 1;
-        a.lds_keys = 256;
-    }
-    rc = launch_scan(rt, c, op, a, dim3((unsigned)parts, (unsigned)nq), (size_t)a.lds_keys * 8, err);
-    if (rc) return rc;
-    if (out_acc) {
-        LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch, c->sets == 1 ? 0 : c->n,
-                                            c->n, (int)c->d, q, out_ids, (int)k, (int)nq,
-                                            op != MANTA_ROCM_DOT ? 1 : 0, out_acc, rt->stream),
-                   "q8_rescore");
-    }
-    return MANTA_ROCM_OK;
+    const ScoreOp so = parse_op(c, op);
+    if (out_acc && (c->format != MANTA_ROCM_Q8_ROWS || !so.quant))
+        return fail(err, MANTA_ROCM_ERROR, "accumulator output needs q8 candidates and quantized-query scores");
+    if (so.quant) return scan_topk(rt, c, so.scan, order, q, nq, k, out_ids, out_scores, out_acc, err);
+    return ref_topk(rt, c, so, order, q, nq, k, out_ids, out_scores, err);
 }
 
 int manta_rocm_pack_candidates(MantaRocm* rt, const MantaRocmCandidates* c, const int32_t* top, int64_t nq,

@@ -204,18 +204,31 @@ class Runtime:
             raise ValueError("queries must be [d] or [nq, d] with d=%d (got %s)" % (cands.d, tuple(queries.shape)))
         return queries.shape[0] if len(queries.shape) == 2 else 1
 
+    @staticmethod
+    def _op(op: str, quantized: bool) -> int:
+        if op not in _lib.OPS:
+            raise ValueError("unknown score op %r (dot, cosine, l2_distance)" % (op,))
+        return _lib.OPS[op] | (_lib.QUANTIZED_QUERY if quantized else 0)
+
     def score(self, cands: Candidates, op: str, queries: DeviceArray,
-              out: Optional[DeviceArray] = None) -> DeviceArray:
+              out: Optional[DeviceArray] = None, quantized: bool = False) -> DeviceArray:
+        """Score matrix [nq, n].  Default: the reference's dotRows /
+        cosineRows / l2DistanceRows on the dequantized candidates, bit for
+        bit; quantized=True: the quantized-query scores."""
         nq = self._query_rows(cands, queries)
         if out is None:
             out = self.empty((nq, cands.n), np.float32)
-        call("manta_rocm_score", self.handle, cands.handle, C.c_int(_lib.OPS[op]), queries.ptr,
+        call("manta_rocm_score", self.handle, cands.handle, C.c_int(self._op(op, quantized)), queries.ptr,
              C.c_int64(nq), out.ptr)
         return out
 
     def score_topk(self, cands: Candidates, op: str, queries: DeviceArray, k: int,
                    smallest: bool = False, with_scores: bool = True, with_acc: bool = False,
-                   out=None):
+                   out=None, quantized: bool = False):
+        """(ids [nq, k] int32, scores [nq, k] f32 or None, accumulators
+        [nq, k] int64 or None); topKTensor's order.  Reference scores by
+        default, quantized-query scores with quantized=True (which the
+        integer accumulators need)."""
         nq = self._query_rows(cands, queries)
         if out is None:
             ids = self.empty((nq, k), np.int32)
@@ -223,7 +236,7 @@ class Runtime:
             acc = self.empty((nq, k), np.int64) if with_acc else None
         else:
             ids, sc, acc = out
-        call("manta_rocm_score_topk", self.handle, cands.handle, C.c_int(_lib.OPS[op]),
+        call("manta_rocm_score_topk", self.handle, cands.handle, C.c_int(self._op(op, quantized)),
              C.c_int(_lib.SMALLEST if smallest else _lib.LARGEST), queries.ptr, C.c_int64(nq),
              C.c_int64(k), ids.ptr, _ptr(sc), _ptr(acc))
         return ids, sc, acc

@@ -78,67 +78,171 @@ static const float* docs_for(const float* docs, int64_t qi, int64_t rows,
     return docs_per_query ? docs + qi * rows * cols : docs;
 }
 
-/* dotRows, tensor_ops.go:1366-1396: f32 sum, sequential over columns. */
+/* One row of dotRows, tensor_ops.go:1366-1396: f32 sum, sequential over
+ * columns (each product and each sum rounded on its own). */
+static float ref_dot_row(const float* q, const float* d, int64_t cols) {
+    float sum = 0.0f;
+    for (int64_t c = 0; c < cols; c++) sum += q[c] * d[c];
+    return sum;
+}
+
+/* The query norm of cosineRows, tensor_ops.go:1404-1408 (f64, sequential). */
+static double ref_query_norm(const float* q, int64_t cols) {
+    double qn = 0.0;
+    for (int64_t c = 0; c < cols; c++) {
+        double v = (double)q[c];
+        qn += v * v;
+    }
+    return qn;
+}
+
+/* One row of cosineRows, tensor_ops.go:1410-1425: f64 dot and row norm, 0
+ * when the denominator is 0, narrowed to f32. */
+static float ref_cosine_row(const float* q, double qn, const float* d, int64_t cols) {
+    double dot = 0.0, dn = 0.0;
+    for (int64_t c = 0; c < cols; c++) {
+        double qq = (double)q[c];
+        double dv = (double)d[c];
+        dot += qq * dv;
+        dn += dv * dv;
+    }
+    double denom = sqrt(qn) * sqrt(dn);
+    return denom == 0.0 ? 0.0f : (float)(dot / denom);
+}
+
+/* One row of l2DistanceRows, tensor_ops.go:1464-1472: difference in f32,
+ * squares and sum in f64, sqrt, narrowed. */
+static float ref_l2_row(const float* q, const float* d, int64_t cols) {
+    double sum = 0.0;
+    for (int64_t c = 0; c < cols; c++) {
+        float diff32 = q[c] - d[c];
+        double diff = (double)diff32;
+        sum += diff * diff;
+    }
+    return (float)sqrt(sum);
+}
+
+/* dotRows, tensor_ops.go:1366-1396. */
 void orc_dot_rows(const float* q, const float* docs, int64_t nq, int64_t rows,
                   int64_t cols, int docs_per_query, float* out) {
     for (int64_t b = 0; b < nq; b++) {
         const float* qb = q + b * cols;
         const float* db = docs_for(docs, b, rows, cols, docs_per_query);
-        for (int64_t r = 0; r < rows; r++) {
-            float sum = 0.0f;
-            const float* d = db + r * cols;
-            for (int64_t c = 0; c < cols; c++) sum += qb[c] * d[c];
-            out[b * rows + r] = sum;
-        }
+        for (int64_t r = 0; r < rows; r++) out[b * rows + r] = ref_dot_row(qb, db + r * cols, cols);
     }
 }
 
-/* cosineRows, tensor_ops.go:1398-1456: f64 dot and norms, 0 when the
- * denominator is 0, narrowed to f32. */
+/* cosineRows, tensor_ops.go:1398-1456. */
 void orc_cosine_rows(const float* q, const float* docs, int64_t nq, int64_t rows,
                      int64_t cols, int docs_per_query, float* out) {
     for (int64_t b = 0; b < nq; b++) {
         const float* qb = q + b * cols;
         const float* db = docs_for(docs, b, rows, cols, docs_per_query);
-        double qn = 0.0;
-        for (int64_t c = 0; c < cols; c++) {
-            double v = (double)qb[c];
-            qn += v * v;
-        }
-        for (int64_t r = 0; r < rows; r++) {
-            double dot = 0.0, dn = 0.0;
-            const float* d = db + r * cols;
-            for (int64_t c = 0; c < cols; c++) {
-                double qq = (double)qb[c];
-                double dv = (double)d[c];
-                dot += qq * dv;
-                dn += dv * dv;
-            }
-            double denom = sqrt(qn) * sqrt(dn);
-            out[b * rows + r] = denom == 0.0 ? 0.0f : (float)(dot / denom);
-        }
+        const double qn = ref_query_norm(qb, cols);
+        for (int64_t r = 0; r < rows; r++) out[b * rows + r] = ref_cosine_row(qb, qn, db + r * cols, cols);
     }
 }
 
-/* l2DistanceRows, tensor_ops.go:1458-1490: difference in f32, squares and
- * sum in f64, sqrt, narrowed. */
+/* l2DistanceRows, tensor_ops.go:1458-1490. */
 void orc_l2_distance_rows(const float* q, const float* docs, int64_t nq,
                           int64_t rows, int64_t cols, int docs_per_query,
                           float* out) {
     for (int64_t b = 0; b < nq; b++) {
         const float* qb = q + b * cols;
         const float* db = docs_for(docs, b, rows, cols, docs_per_query);
-        for (int64_t r = 0; r < rows; r++) {
-            double sum = 0.0;
-            const float* d = db + r * cols;
-            for (int64_t c = 0; c < cols; c++) {
-                float diff32 = qb[c] - d[c];
-                double diff = (double)diff32;
-                sum += diff * diff;
-            }
-            out[b * rows + r] = (float)sqrt(sum);
+        for (int64_t r = 0; r < rows; r++) out[b * rows + r] = ref_l2_row(qb, db + r * cols, cols);
+    }
+}
+
+/* The f32 value a reference q8 / q4 tensor holds for a packed element: the
+ * fake-quantization grid stores q*scale in f32
+ * (runtime/embedding_trainer.go:3753-3762: data[i] = q * scale), so a q8
+ * element is the f32 product code*scale and a q4 element code*f16scale
+ * (exact: a 4-bit code times an 11-bit significand). */
+static float q8_value(int8_t code, float scale) { return (float)code * scale; }
+
+void orc_dequant_q8(const int8_t* codes, const float* scales, int64_t n, int64_t d, float* out) {
+    for (int64_t r = 0; r < n; r++)
+        for (int64_t c = 0; c < d; c++) out[r * d + c] = q8_value(codes[r * d + c], scales[r]);
+}
+
+static int q4_code(const uint8_t* row, int64_t c);
+
+void orc_dequant_q4(const uint8_t* packed, const uint16_t* scales, int64_t n, int64_t d, float* out) {
+    for (int64_t r = 0; r < n; r++)
+        for (int64_t c = 0; c < d; c++)
+            out[r * d + c] = (float)q4_code(packed + r * (d / 2), c) * orc_f16_to_f32(scales[r * (d / 32) + c / 32]);
+}
+
+/* fakeQuantizeDataInPlace, runtime/embedding_trainer.go:3738-3763: one
+ * symmetric grid for the whole tensor, scale = maxAbs/levels (f32),
+ * q = round(v/scale) (f32 division, half away from zero), clamped to
+ * +-levels, value q*scale (f32); an all-zero tensor is left unchanged. */
+void orc_fake_quantize(float* data, int64_t n, int bits) {
+    if (bits <= 0 || n == 0) return;
+    float maxabs = 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        float a = (float)fabs((double)data[i]);
+        if (a > maxabs) maxabs = a;
+    }
+    if (maxabs == 0.0f) return;
+    const float levels = (float)((1 << (bits - 1)) - 1);
+    if (levels <= 0.0f) return;
+    const float scale = maxabs / levels;
+    if (scale == 0.0f) return;
+    for (int64_t i = 0; i < n; i++) {
+        float q = (float)round((double)(data[i] / scale));
+        if (q > levels) q = levels;
+        if (q < -levels) q = -levels;
+        data[i] = q * scale;
+    }
+}
+
+/* dotRows / cosineRows / l2DistanceRows of f16 queries (widened to f32, as
+ * the reference's f16 tensors are f32-backed, tensor.go:11-19) against the
+ * dequantized values of packed candidates, row by row: the per-row loops
+ * above on each dequantized row, so the bits equal those of the functions
+ * above on a dequantized matrix. */
+static void ref_score_rows(int op, const float* q32, const float* row, double qn, int64_t d, float* out) {
+    if (op == ORC_DOT) *out = ref_dot_row(q32, row, d);
+    else if (op == ORC_COSINE) *out = ref_cosine_row(q32, qn, row, d);
+    else *out = ref_l2_row(q32, row, d);
+}
+
+void orc_ref_score_q8(int op, const uint16_t* queries, int64_t nq, const int8_t* codes,
+                      const float* scales, int64_t sets, int64_t n, int64_t d, float* out) {
+    float* q32 = (float*)malloc((size_t)d * sizeof(float));
+    float* row = (float*)malloc((size_t)d * sizeof(float));
+    for (int64_t b = 0; b < nq; b++) {
+        const int64_t set = sets == 1 ? 0 : b;
+        orc_f16_to_f32_array(queries + b * d, d, q32);
+        const double qn = ref_query_norm(q32, d);
+        for (int64_t r = 0; r < n; r++) {
+            const int64_t gr = set * n + r;
+            for (int64_t c = 0; c < d; c++) row[c] = q8_value(codes[gr * d + c], scales[gr]);
+            ref_score_rows(op, q32, row, qn, d, out + b * n + r);
         }
     }
+    free(q32);
+    free(row);
+}
+
+void orc_ref_score_q4(int op, const uint16_t* queries, int64_t nq, const uint8_t* packed,
+                      const uint16_t* scales, int64_t sets, int64_t n, int64_t d, float* out) {
+    float* q32 = (float*)malloc((size_t)d * sizeof(float));
+    float* row = (float*)malloc((size_t)d * sizeof(float));
+    for (int64_t b = 0; b < nq; b++) {
+        const int64_t set = sets == 1 ? 0 : b;
+        orc_f16_to_f32_array(queries + b * d, d, q32);
+        const double qn = ref_query_norm(q32, d);
+        for (int64_t r = 0; r < n; r++) {
+            const int64_t gr = set * n + r;
+            orc_dequant_q4(packed + gr * (d / 2), scales + gr * (d / 32), 1, d, row);
+            ref_score_rows(op, q32, row, qn, d, out + b * n + r);
+        }
+    }
+    free(q32);
+    free(row);
 }
 
 typedef struct {
@@ -459,7 +563,7 @@ void orc_query_e16(const uint16_t* q, int64_t d, int16_t* codes, float* qs,
 
 static float finish_score(int op, float qd, float qnorm, float qq, float dnorm,
                           float dd) {
-    if (op == ORC_DOT) return qd;
+    if (op == ORC_DOT || op == ORC_DOT16) return qd;
     if (op == ORC_COSINE) {
         float den = qnorm * dnorm;
         return den == 0.0f ? 0.0f : qd / den;

@@ -29,7 +29,9 @@
 extern "C" {
 #endif
 
-enum { ORC_DOT = 0, ORC_COSINE = 1, ORC_L2 = 2 };
+/* ORC_DOT16: the q8 dot with E16 query codes (qd below), the scan score the
+ * device ranks reference-semantics dot top-k by. */
+enum { ORC_DOT = 0, ORC_COSINE = 1, ORC_L2 = 2, ORC_DOT16 = 3 };
 
 /* IEEE binary16 <-> binary32 (round to nearest even). */
 float orc_f16_to_f32(uint16_t h);
@@ -86,6 +88,28 @@ int orc_embed(const int32_t* tokens, const int32_t* mask, int64_t b, int64_t t,
               const uint16_t* proj_f16, const int8_t* proj_codes,
               const float* proj_col_scale, int64_t e, uint16_t* out_f16,
               float* out_f32, char* msg, int msglen);
+
+/* The f32 values a reference q8 / q4 tensor carries for packed elements
+ * (code*scale in f32; q4: code*f16scale, exact).  out [n, d]. */
+void orc_dequant_q8(const int8_t* codes, const float* scales, int64_t n,
+                    int64_t d, float* out);
+void orc_dequant_q4(const uint8_t* packed, const uint16_t* scales, int64_t n,
+                    int64_t d, float* out);
+
+/* dotRows / cosineRows / l2DistanceRows (op ORC_*) of f16 queries [nq, d]
+ * (widened to f32) against the dequantized rows of packed candidates
+ * [sets, n, d] (sets 1: shared; sets nq: one set per query).  Bit-identical
+ * to the functions above applied to orc_dequant_* output.  out [nq, n]. */
+void orc_ref_score_q8(int op, const uint16_t* queries, int64_t nq,
+                      const int8_t* codes, const float* scales, int64_t sets,
+                      int64_t n, int64_t d, float* out);
+void orc_ref_score_q4(int op, const uint16_t* queries, int64_t nq,
+                      const uint8_t* packed, const uint16_t* scales,
+                      int64_t sets, int64_t n, int64_t d, float* out);
+
+/* fakeQuantizeDataInPlace (runtime/embedding_trainer.go:3738-3763): the
+ * reference's per-tensor symmetric grid, in place. */
+void orc_fake_quantize(float* data, int64_t n, int bits);
 
 /* ---- 2. packed scoring contract (defined by this repository) ---------- */
 

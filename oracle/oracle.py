@@ -14,8 +14,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-DOT, COSINE, L2 = 0, 1, 2
-OPS = {"dot": DOT, "cosine": COSINE, "l2_distance": L2}
+DOT, COSINE, L2, DOT16 = 0, 1, 2, 3
+OPS = {"dot": DOT, "cosine": COSINE, "l2_distance": L2, "dot16": DOT16}
 
 _L = None
 
@@ -54,6 +54,11 @@ def lib() -> C.CDLL:
             "orc_query_e16": (None, [p, i64, p, p, p, p]),
             "orc_score_q8": (None, [ci, p, i64, p, p, p, p, i64, i64, i64, p, p]),
             "orc_score_q4": (None, [ci, p, i64, p, p, p, p, i64, i64, i64, p]),
+            "orc_dequant_q8": (None, [p, p, i64, i64, p]),
+            "orc_dequant_q4": (None, [p, p, i64, i64, p]),
+            "orc_ref_score_q8": (None, [ci, p, i64, p, p, i64, i64, i64, p]),
+            "orc_ref_score_q4": (None, [ci, p, i64, p, p, i64, i64, i64, p]),
+            "orc_fake_quantize": (None, [p, i64, ci]),
             "orc_layernorm_rows": (None, [p, i64, i64]),
             "orc_softmax_rows": (None, [p, i64, i64]),
             "orc_gelu": (None, [p, i64]),
@@ -327,3 +332,56 @@ def score_q4(op, queries, packed, scales, d):
     lib().orc_score_q4(OPS[op], _p(queries), nq, _p(packed), _p(scales), _p(dn), _p(dd), sets, n,
                        d, _p(out))
     return out
+
+
+# ------------------------------------- reference scores of packed candidates
+def dequant_q8(codes, scales):
+    """The f32 values a reference q8 tensor holds: code*scale (f32)."""
+    codes = _c(codes, np.int8)
+    scales = _c(scales, np.float32)
+    d = codes.shape[-1]
+    n = codes.size // d
+    out = np.empty(codes.shape, np.float32)
+    lib().orc_dequant_q8(_p(codes), _p(scales), n, d, _p(out))
+    return out
+
+
+def dequant_q4(packed, scales, d):
+    """The f32 values of a q4 tensor: nibble code times its block's f16 scale."""
+    packed = _c(packed, np.uint8)
+    scales = _c(scales, np.uint16)
+    n = packed.size // (d // 2)
+    out = np.empty(packed.shape[:-1] + (d,), np.float32)
+    lib().orc_dequant_q4(_p(packed), _p(scales), n, d, _p(out))
+    return out
+
+
+def ref_score_q8(op, queries, codes, scales):
+    """dotRows / cosineRows / l2DistanceRows of f16 queries [nq, d] against
+    the dequantized rows of q8 candidates [n, d] (shared) or [nq, n, d]."""
+    queries = _c(queries, np.uint16)
+    codes = _c(codes, np.int8)
+    scales = _c(scales, np.float32)
+    nq, d = queries.shape
+    sets, n = (1, codes.shape[0]) if codes.ndim == 2 else codes.shape[:2]
+    out = np.empty((nq, n), np.float32)
+    lib().orc_ref_score_q8(OPS[op], _p(queries), nq, _p(codes), _p(scales), sets, n, d, _p(out))
+    return out
+
+
+def ref_score_q4(op, queries, packed, scales, d):
+    queries = _c(queries, np.uint16)
+    packed = _c(packed, np.uint8)
+    scales = _c(scales, np.uint16)
+    nq = queries.shape[0]
+    sets, n = (1, packed.shape[0]) if packed.ndim == 2 else packed.shape[:2]
+    out = np.empty((nq, n), np.float32)
+    lib().orc_ref_score_q4(OPS[op], _p(queries), nq, _p(packed), _p(scales), sets, n, d, _p(out))
+    return out
+
+
+def fake_quantize(x, bits):
+    """fakeQuantizeDataInPlace on a copy of x (one grid for the whole array)."""
+    x = np.array(x, dtype=np.float32, order="C", copy=True)
+    lib().orc_fake_quantize(_p(x), x.size, int(bits))
+    return x

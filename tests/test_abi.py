@@ -40,7 +40,7 @@ def test_python_signatures_cover_header():
 
 def test_abi_version_and_device_count_without_gpu():
     lib = _lib.load()
-    assert lib.manta_rocm_abi_version() == 1
+    assert lib.manta_rocm_abi_version() == 2
     n = C.c_int(-1)
     err = C.c_char_p()
     rc = lib.manta_rocm_device_count(C.byref(n), C.byref(err))

@@ -1,7 +1,7 @@
 """Candidates bound from a packed container (manta_rocm_bind_packed) score
 exactly as candidates bound from the same arrays and as the oracle: the
-container's QCOD / QSCL bytes reach the device unchanged (bit-exact scores and
-ids, the packed contract's bar)."""
+container's QCOD / QSCL bytes reach the device unchanged (bit-exact reference
+scores and ids)."""
 import numpy as np
 import pytest
 
@@ -29,7 +29,7 @@ def test_bind_packed_matches_arrays_and_oracle(rt, tmp_path, dtype, op):
     assert (from_file.n, from_file.d) == (n, d)
     got = rt.score(from_file, op, qd).download()
     np.testing.assert_array_equal(got, rt.score(from_arrays, op, qd).download())
-    want = (orc.score_q8(op, q, codes, scales) if dtype == "q8" else orc.score_q4(op, q, codes, scales, d))
+    want = (orc.ref_score_q8(op, q, codes, scales) if dtype == "q8" else orc.ref_score_q4(op, q, codes, scales, d))
     np.testing.assert_array_equal(got, want)
     ids, sc, _ = rt.score_topk(from_file, op, qd, k, smallest=(op == "l2_distance"))
     oids = orc.topk(want, k, smallest=(op == "l2_distance"))

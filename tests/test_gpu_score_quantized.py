@@ -1,8 +1,11 @@
-"""GPU parity of packed scoring and top-k against the CPU oracle.
+"""GPU parity of the quantized-query scores (MANTA_ROCM_QUANTIZED_QUERY)
+and their top-k against the CPU oracle.
 
-Bar: scores, ids and integer accumulators bit-exact with the oracle's
-restatement of the packed contract on identical seeded inputs; the
-reference's own tiny vectors within its 5e-4.
+These are the scans that rank rows for the reference-semantics top-k (whose
+proof rests on them returning their exact best kp rows), and BASELINE's q8
+dot formula (configs 0 and 4).  Bar: scores, ids and integer accumulators
+bit-exact with the oracle's restatement of the quantized-query formulas on
+identical seeded inputs.
 """
 import json
 import os
@@ -19,6 +22,14 @@ pytestmark = pytest.mark.gpu
 GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_known_answers.json")))
 
 
+def _qscore(rt, *args, **kw):
+    return rt.score(*args, quantized=True, **kw)
+
+
+def _qtopk(rt, *args, **kw):
+    return rt.score_topk(*args, quantized=True, **kw)
+
+
 def _q8_case(seed, nq, n, d, sets, normalize=True):
     q = synth.normal_f16(100 + seed, 0, nq, d, 1.0, normalize=normalize)
     codes = np.empty((sets, n, d), np.int8)
@@ -32,32 +43,13 @@ def _oracle_codes(codes, sets):
     return codes[0] if sets == 1 else codes
 
 
-def test_reference_runtime_vectors_on_device(rt):
-    for case in GOLD["score_runtime"]:
-        q = orc.f32_to_f16(np.asarray(case["q"], np.float32).reshape(1, -1))
-        docs = np.asarray(case["docs"], np.float32)
-        codes, scales = orc.pack_q8_rows(docs)
-        cands = rt.bind_q8(codes, scales)
-        qd = rt.to_device(q)
-        got = rt.score(cands, case["op"], qd).download()[0]
-        want = orc.score_q8(case["op"], q, codes, scales)[0]
-        np.testing.assert_array_equal(got, want)
-        if "want" in case:
-            np.testing.assert_allclose(got, case["want"], rtol=0, atol=5e-4)
-        else:
-            ids, sc, _ = rt.score_topk(cands, case["op"], qd, case["topk"])
-            np.testing.assert_array_equal(ids.download()[0], case["want_ids"])
-            np.testing.assert_allclose(sc.download()[0], case["want_scores"], rtol=0, atol=5e-4)
-        cands.close()
-
-
 @pytest.mark.parametrize("op", ["dot", "cosine", "l2_distance"])
 @pytest.mark.parametrize("d", [64, 128, 256, 384, 100, 48])
 def test_q8_score_matrix_bit_exact(rt, op, d):
     nq, n = 3, 1000
     q, codes, scales = _q8_case(d, nq, n, d, sets=1, normalize=(op != "l2_distance"))
     cands = rt.bind_q8(codes[0], scales[0])
-    got = rt.score(cands, op, rt.to_device(q)).download()
+    got = _qscore(rt, cands, op, rt.to_device(q)).download()
     want = orc.score_q8(op, q, codes[0], scales[0])
     np.testing.assert_array_equal(got, want)
     cands.close()
@@ -71,7 +63,7 @@ def test_q8_score_topk_bit_exact(rt, op, smallest, sets, n, k):
     nq, d = 4, 256
     q, codes, scales = _q8_case(n + k, nq, n, d, sets)
     cands = rt.bind_q8(codes[0] if sets == 1 else codes, scales[0] if sets == 1 else scales)
-    ids, sc, acc = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
+    ids, sc, acc = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
     ids, sc, acc = ids.download(), sc.download(), acc.download()
     want_s, want_acc = orc.score_q8(op, q, _oracle_codes(codes, sets), scales[0] if sets == 1 else scales,
                                     with_acc=True)
@@ -86,7 +78,7 @@ def _check_q8_topk(rt, op, smallest, q, codes, scales, k):
     """score_topk over per-query candidate sets against the oracle: ids,
     scores and integer accumulators bit-exact."""
     cands = rt.bind_q8(codes, scales)
-    ids, sc, acc = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
+    ids, sc, acc = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
     ids, sc, acc = ids.download(), sc.download(), acc.download()
     want_s, want_acc = orc.score_q8(op, q, codes, scales, with_acc=True)
     want_ids = orc.topk(want_s, k, smallest=smallest)
@@ -127,7 +119,7 @@ def test_q8_wave_list_all_ties(rt, op, smallest, k):
     scales[:] = scales[:, :1]
     _check_q8_topk(rt, op, smallest, q, codes, scales, k)
     cands = rt.bind_q8(codes, scales)
-    ids, _, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    ids, _, _ = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=smallest)
     np.testing.assert_array_equal(ids.download(), np.tile(np.arange(k, dtype=np.int32), (2, 1)))
     cands.close()
 
@@ -140,11 +132,11 @@ def test_q4_score_and_topk_bit_exact(rt, op, d):
     packed, s4 = synth.q4_rows(7, 1, n, d, normalize=True)
     cands = rt.bind_q4(packed, s4, d)
     qd = rt.to_device(q)
-    got = rt.score(cands, op, qd).download()
+    got = _qscore(rt, cands, op, qd).download()
     want = orc.score_q4(op, q, packed, s4, d)
     np.testing.assert_array_equal(got, want)
     smallest = op == "l2_distance"
-    ids, sc, _ = rt.score_topk(cands, op, qd, k, smallest=smallest)
+    ids, sc, _ = _qtopk(rt, cands, op, qd, k, smallest=smallest)
     want_ids = orc.topk(want, k, smallest=smallest)
     np.testing.assert_array_equal(ids.download(), want_ids)
     np.testing.assert_array_equal(sc.download(), np.take_along_axis(want, want_ids, 1))
@@ -198,7 +190,7 @@ def test_config0_full_size_bit_exact(rt):
     accumulators bit-exact with the oracle."""
     q, codes, scales = synth.config0()
     cands = rt.bind_q8(codes[0], scales[0])
-    ids, sc, acc = rt.score_topk(cands, "dot", rt.to_device(q), 10, with_acc=True)
+    ids, sc, acc = _qtopk(rt, cands, "dot", rt.to_device(q), 10, with_acc=True)
     want_s, want_acc = orc.score_q8("dot", q, codes[0], scales[0], with_acc=True)
     want_ids = orc.topk(want_s, 10)
     np.testing.assert_array_equal(ids.download(), want_ids)
@@ -218,7 +210,7 @@ def test_multi_query_score_matrix_bit_exact(rt, op, smallest, d):
     nq, n = 37, 3000
     q, codes, scales = _q8_case(d + 1, nq, n, d, sets=1, normalize=(op != "l2_distance"))
     cands = rt.bind_q8(codes[0], scales[0])
-    got = rt.score(cands, op, rt.to_device(q)).download()
+    got = _qscore(rt, cands, op, rt.to_device(q)).download()
     want = orc.score_q8(op, q, codes[0], scales[0])
     np.testing.assert_array_equal(got, want)
     cands.close()
@@ -231,7 +223,7 @@ def test_multi_query_score_matrix_bit_exact(rt, op, smallest, d):
 def test_multi_query_topk_bit_exact(rt, op, smallest, nq, n, d, k):
     q, codes, scales = _q8_case(nq + n + d + k, nq, n, d, sets=1, normalize=(op != "l2_distance"))
     cands = rt.bind_q8(codes[0], scales[0])
-    ids, sc, acc = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
+    ids, sc, acc = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=smallest, with_acc=True)
     ids, sc, acc = ids.download(), sc.download(), acc.download()
     want_s, want_acc = orc.score_q8(op, q, codes[0], scales[0], with_acc=True)
     want_ids = orc.topk(want_s, k, smallest=smallest)
@@ -254,7 +246,7 @@ def test_multi_query_zero_rows_partial_group(rt, op, smallest):
     codes[zero] = 0
     scales[zero[::2]] = 0.0
     cands = rt.bind_q8(codes, scales)
-    ids, sc, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    ids, sc, _ = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=smallest)
     want_s = orc.score_q8(op, q, codes, scales)
     want_ids = orc.topk(want_s, k, smallest=smallest)
     np.testing.assert_array_equal(ids.download(), want_ids)
@@ -268,7 +260,7 @@ def test_multi_query_repeated_calls_are_identical(rt):
     for n, nq in ((20000, 32), (5000, 8)):
         q, codes, scales = _q8_case(n, nq, n, 128, sets=1, normalize=False)
         cands = rt.bind_q8(codes[0], scales[0])
-        ids, _, _ = rt.score_topk(cands, "l2_distance", rt.to_device(q), 100, smallest=True)
+        ids, _, _ = _qtopk(rt, cands, "l2_distance", rt.to_device(q), 100, smallest=True)
         want = orc.topk(orc.score_q8("l2_distance", q, codes[0], scales[0]), 100, smallest=True)
         np.testing.assert_array_equal(ids.download(), want)
         cands.close()
@@ -301,7 +293,7 @@ def test_multi_query_adversarial_row_order(rt, op, smallest, k):
     nq, n, d = 24, 300000, 128
     q, codes, scales = _ordered_case(op, nq, n, d, k)
     cands = rt.bind_q8(codes, scales)
-    ids, sc, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    ids, sc, _ = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=smallest)
     want_s = orc.score_q8(op, q, codes, scales)
     want_ids = orc.topk(want_s, k, smallest=smallest)
     np.testing.assert_array_equal(ids.download(), want_ids)
@@ -318,7 +310,7 @@ def test_multi_query_all_ties(rt, op):
     codes = np.repeat(codes1, n, axis=0)
     scales = np.repeat(scale1, n)
     cands = rt.bind_q8(codes, scales)
-    ids, _, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=(op == "l2_distance"))
+    ids, _, _ = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=(op == "l2_distance"))
     want = orc.topk(orc.score_q8(op, q, codes, scales), k, smallest=(op == "l2_distance"))
     np.testing.assert_array_equal(ids.download(), want)
     np.testing.assert_array_equal(want, np.tile(np.arange(k), (nq, 1)))
@@ -337,7 +329,7 @@ def test_q8_dot_512_queries_bit_exact(rt, smallest, nq, n, d, k):
     scores and accumulators bit-exact."""
     q, codes, scales = _q8_case(nq + n + d + k, nq, n, d, sets=1)
     cands = rt.bind_q8(codes[0], scales[0])
-    ids, sc, acc = rt.score_topk(cands, "dot", rt.to_device(q), k, smallest=smallest, with_acc=True)
+    ids, sc, acc = _qtopk(rt, cands, "dot", rt.to_device(q), k, smallest=smallest, with_acc=True)
     ids, sc, acc = ids.download(), sc.download(), acc.download()
     want_s, want_acc = orc.score_q8("dot", q, codes[0], scales[0], with_acc=True)
     want_ids = orc.topk(want_s, k, smallest=smallest)
@@ -354,7 +346,7 @@ def test_q8_dot_512_queries_adversarial_row_order(rt, k):
     nq, n, d = 512, 60000, 128
     q, codes, scales = _ordered_case("dot", nq, n, d, k)
     cands = rt.bind_q8(codes, scales)
-    ids, sc, _ = rt.score_topk(cands, "dot", rt.to_device(q), k)
+    ids, sc, _ = _qtopk(rt, cands, "dot", rt.to_device(q), k)
     want_s = orc.score_q8("dot", q, codes, scales)
     want_ids = orc.topk(want_s, k)
     np.testing.assert_array_equal(ids.download(), want_ids)
@@ -370,7 +362,7 @@ def test_q8_dot_512_queries_all_ties(rt, smallest):
     codes = np.repeat(codes1, n, axis=0)
     scales = np.repeat(scale1, n)
     cands = rt.bind_q8(codes, scales)
-    ids, _, _ = rt.score_topk(cands, "dot", rt.to_device(q), k, smallest=smallest)
+    ids, _, _ = _qtopk(rt, cands, "dot", rt.to_device(q), k, smallest=smallest)
     want = orc.topk(orc.score_q8("dot", q, codes, scales), k, smallest=smallest)
     np.testing.assert_array_equal(ids.download(), want)
     np.testing.assert_array_equal(want, np.tile(np.arange(k), (nq, 1)))
@@ -385,7 +377,7 @@ def test_q8_dot_512_queries_negative_scales(rt):
     scales = scales.copy()
     scales[0, ::7] *= -1.0
     cands = rt.bind_q8(codes[0], scales[0])
-    ids, sc, _ = rt.score_topk(cands, "dot", rt.to_device(q), k)
+    ids, sc, _ = _qtopk(rt, cands, "dot", rt.to_device(q), k)
     want_s = orc.score_q8("dot", q, codes[0], scales[0])
     want_ids = orc.topk(want_s, k)
     np.testing.assert_array_equal(ids.download(), want_ids)
@@ -408,7 +400,7 @@ def test_q4_multi_query_score_matrix_bit_exact(rt, op, d):
     nq, n = 40, 3000
     q, packed, s4 = _q4_case(d, nq, n, d, normalize=(op != "l2_distance"))
     cands = rt.bind_q4(packed, s4, d)
-    got = rt.score(cands, op, rt.to_device(q)).download()
+    got = _qscore(rt, cands, op, rt.to_device(q)).download()
     np.testing.assert_array_equal(got, orc.score_q4(op, q, packed, s4, d))
     cands.close()
 
@@ -419,7 +411,7 @@ def test_q4_multi_query_score_matrix_bit_exact(rt, op, d):
 def test_q4_multi_query_topk_bit_exact(rt, op, smallest, nq, n, d, k):
     q, packed, s4 = _q4_case(nq + n + d + k, nq, n, d, normalize=(op != "l2_distance"))
     cands = rt.bind_q4(packed, s4, d)
-    ids, sc, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    ids, sc, _ = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=smallest)
     want_s = orc.score_q4(op, q, packed, s4, d)
     want_ids = orc.topk(want_s, k, smallest=smallest)
     np.testing.assert_array_equal(ids.download(), want_ids)
@@ -441,7 +433,7 @@ def test_q4_multi_query_adversarial_row_order(rt, k):
     grow = (1.0 + np.arange(n, dtype=np.float64) / n)[:, None]
     s4 = orc.f32_to_f16((orc.f16_to_f32(s1) * grow).astype(np.float32))
     cands = rt.bind_q4(packed, s4, d)
-    ids, sc, _ = rt.score_topk(cands, "dot", rt.to_device(q), k)
+    ids, sc, _ = _qtopk(rt, cands, "dot", rt.to_device(q), k)
     want_s = orc.score_q4("dot", q, packed, s4, d)
     want_ids = orc.topk(want_s, k)
     np.testing.assert_array_equal(ids.download(), want_ids)
@@ -455,7 +447,7 @@ def test_q4_multi_query_adversarial_row_order(rt, k):
 # score.  Results must equal the q4 contract's, bit for bit.
 
 def _check_q4_topk(rt, cands, op, q, packed, s4, d, k, smallest=False):
-    ids, sc, _ = rt.score_topk(cands, op, rt.to_device(q), k, smallest=smallest)
+    ids, sc, _ = _qtopk(rt, cands, op, rt.to_device(q), k, smallest=smallest)
     want_s = orc.score_q4(op, q, packed, s4, d)
     want_ids = orc.topk(want_s, k, smallest=smallest)
     np.testing.assert_array_equal(ids.download(), want_ids)
