@@ -1,18 +1,24 @@
 #!/usr/bin/env python3
-"""Headline benchmark of the retrieval hot path on one MI355X.
+"""Benchmark of the retrieval hot path on one MI355X, every BASELINE config.
 
-Workload (BASELINE.json configs[0] shape): q8 packed-candidate dot + top-10,
-N = 65,536 candidates x D = 256 per query, one query per candidate set.  A
-step scores `--sets` independent (query, candidate set) problems in one
-fused launch sequence -- the reference's batched score layout
-[Q,D] x [Q,N,D] (runtime/backend/tensor_ops.go:1511-1519) -- over distinct
-candidate copies whose total (32 x 17 MB) exceeds the 256 MB MALL, so the
-candidates stream from HBM.  Inputs are resident in HBM before timing.
+Headline (BASELINE.json configs[0] shape): q8 packed-candidate dot + top-10,
+N = 65,536 candidates x D = 256 per query, one query per candidate set, with
+BASELINE's quantized-query dot formula.  A step scores `--sets` independent
+(query, candidate set) problems in one fused launch -- the reference's batched
+score layout [Q,D] x [Q,N,D] (runtime/backend/tensor_ops.go:1511-1519) --
+over distinct candidate copies whose total (32 x 17 MB) exceeds the 256 MB
+MALL, so the candidates stream from HBM.  Inputs are resident in HBM before
+timing.  The default run adds configs 1-4 under "configs": C1 the f16 embed,
+C2 q4 cosine and C3 q8 l2 with the reference's own arithmetic (cosineRows /
+l2DistanceRows, bit for bit), C4 the q8-projection embed then BASELINE's
+quantized-query q8 dot.
 
-Prints one JSON line.  `roofline` is measured live with HIP events around
-every launch of the dominant kernel (q8_scan); `cpu_baseline` times the
-CPU oracle's restatement of the reference host path (f32 dotRows +
-full-sort topKTensor, one thread) on a bounded sample of the same problems.
+Prints one JSON line.  Each `roofline` is measured live with HIP events around
+every launch of the dominant kernel; each `cpu_baseline` times the CPU
+oracle's restatement of the reference host path (f32-backed values, the
+reference's score loops, full-sort topKTensor; one thread) on a bounded
+sample of the same work, and `fair_cpu` the same work's quantized-query
+scores on packed data with heap top-k on all host cores.
 """
 from __future__ import annotations
 
@@ -35,24 +41,48 @@ def c0_bytes_per_problem(n=N, d=D, k=K) -> int:
     return n * (d + 4) + 2 * d + k * 8
 
 
+def host_info() -> dict:
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "threads_used_fair": _fair_threads()}
+
+
+def _fair_threads() -> int:
+    # the GPU box grants 16 host cores to a one-GPU job
+    return max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16)))
+
+
+def _budget_loop(budget_s, fn, max_iter=10**6):
+    done = 0
+    t0 = time.perf_counter()
+    while True:
+        fn(done)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or done >= max_iter:
+            return done, el
+
+
 def cpu_baseline(codes, scales, queries, budget_s: float) -> dict:
-    """Reference host path, restated by the CPU oracle (1 thread): the q8
+    """C0 reference host path, restated by the CPU oracle (1 thread): the q8
     tensor's f32-backed values, f32 dotRows, full-sort topKTensor."""
     from oracle import oracle as orc
 
     sets = codes.shape[0]
-    docs = [codes[s].astype(np.float32) * scales[s][:, None] for s in range(min(sets, 2))]
+    docs = [orc.dequant_q8(codes[s], scales[s]) for s in range(min(sets, 2))]
     qf = orc.f16_to_f32(queries)
-    done = 0
-    t0 = time.perf_counter()
-    while True:
-        s = done % len(docs)
-        scores = orc.dot_rows(qf[s], docs[s])
-        orc.topk(scores, K)
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or done >= 4000:
-            break
+
+    def one(i):
+        s = i % len(docs)
+        orc.topk(orc.dot_rows(qf[s], docs[s]), K)
+
+    done, el = _budget_loop(budget_s, one, 4000)
     return {
         "value": done * N / el,
         "unit": "candidates/s",
@@ -63,6 +93,23 @@ def cpu_baseline(codes, scales, queries, budget_s: float) -> dict:
     }
 
 
+def fair_c0(codes, scales, queries, budget_s: float) -> dict:
+    from oracle import oracle as orc
+
+    nt = _fair_threads()
+    done, el = _budget_loop(budget_s, lambda i: orc.fair_q8_topk("dot", queries[i % 2:i % 2 + 1], codes[i % 2],
+                                                                  scales[i % 2], K, threads=nt), 20000)
+    return {"value": done * N / el, "unit": "candidates/s", "cores": nt, "kind": "fair",
+            "sample": "%d C0 problems, BASELINE's q8 dot on the int8 data, heap top-k, %d threads, %.1f s"
+                      % (done, nt, el)}
+
+
+def _ref_cpu(unit, per_item, budget_s, fn, label, total):
+    """Time `fn(i)` (one item of the reference host path) for about budget_s
+    and report the rate scaled to the config's unit."""
+    done, el = _budget_loop(budget_s, fn, total)
+    return {"value": done * per_item / el, "unit": unit, "cores": 1, "kind": "port",
+            "sample": "%d of %d %s, %.1f s; reference host path restated in C, one thread" % (done, total, label, el)}
 def profiled_traffic(name: str, key: str = "traffic_bytes_per_launch"):
     """HBM bytes per launch (or per step) measured by rocprofv3 PMC
     (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated) and recorded in the
@@ -145,7 +192,7 @@ def _kernels(fam) -> dict:
     return {f: {"launches_per_step": v[0], "us_per_step": v[2] * 1000.0} for f, v in fam.items() if v[0]}
 
 
-def run_c1(rt, steps, warmup) -> dict:
+def run_c1(rt, steps, warmup, cpu_s) -> dict:
     """Config 1: embed pipeline, f16, B=64, T=128, V=32000, D=E=384."""
     from manta_amd import synth
 
@@ -176,11 +223,33 @@ def run_c1(rt, steps, warmup) -> dict:
                      "note": "flops counted over all B*T positions (masked ones included), as the reference computes them"},
         "finalize_us": fam["embed_finalize"][1] * 1000.0,
         "transpose_us": fam["embed_transpose"][1] * 1000.0,
+        **c1_cpu(tokens, mask, table, proj, cpu_s),
     }
 
 
-def run_c2(rt, steps, warmup) -> dict:
-    """Config 2: batched q4 cosine + top-100, Q=256, N=1,048,576, D=384."""
+def c1_cpu(tokens, mask, table, proj, cpu_s) -> dict:
+    if cpu_s <= 0:
+        return {"cpu_baseline": None, "fair_cpu": None}
+    from oracle import oracle as orc
+
+    b, t = tokens.shape
+    nt = _fair_threads()
+
+    def one(i):
+        j = (i * 4) % b
+        orc.embed(tokens[j:j + 4], mask[j:j + 4], table, proj_f16=proj)
+
+    cpu = _ref_cpu("tokens/s", 4 * t, cpu_s, one,
+                   "batches of 4 sequences (gather, f32 sequential matmul, masked mean_pool, normalize)", b // 4)
+    done, el = _budget_loop(cpu_s / 2, lambda i: orc.fair_embed(tokens, mask, table, proj_f16=proj, threads=nt), 200)
+    fair = {"value": done * b * t / el, "unit": "tokens/s", "cores": nt, "kind": "fair",
+            "sample": "%d full C1 batches, f32 embed pipeline over %d threads, %.1f s" % (done, nt, el)}
+    return {"cpu_baseline": cpu, "fair_cpu": fair}
+
+
+def run_c2(rt, steps, warmup, cpu_s) -> dict:
+    """Config 2: batched q4 cosine + top-100, Q=256, N=1,048,576, D=384, with
+    the reference's cosineRows on the dequantized candidates."""
     from manta_amd import synth
 
     queries, packed, scales = synth.config2()
@@ -191,7 +260,7 @@ def run_c2(rt, steps, warmup) -> dict:
     qd = rt.to_device(queries)
     ids = rt.empty((nq, k), np.int32)
     sc = rt.empty((nq, k), np.float32)
-    fams = ["mq_scan", "mq_select", "q4_scan", "topk_merge", "query_encode", "mq_clear"]
+    fams = ["mq_scan", "mq_select", "q4_scan", "topk_merge", "query_encode", "mq_clear", "ref_rescore", "ref_finish", "ref_scan"]
     step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "cosine", qd, k, out=(ids, sc, None)),
                                  steps, warmup, fams)
     # the presets' step after top-k: candidate ids, packed rows and scales of
@@ -210,6 +279,7 @@ def run_c2(rt, steps, warmup) -> dict:
     cands.close()
     return {
         "workload": "c2_q4_cosine_top100", "shape": {"q": nq, "n": n, "d": d, "k": k},
+        "semantics": "reference cosineRows on the dequantized q4 values (ids and scores bit-exact)",
         "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0,
         "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         # The contraction is Q x N x D against f16 queries: priced at the f16
@@ -225,16 +295,41 @@ def run_c2(rt, steps, warmup) -> dict:
                      "executed_i8_frac": ops / (fam[dom][2] / 1000.0) / 1e12 / I8_PEAK,
                      "hbm_GB_s": achieved, "hbm_frac": achieved / HBM_PEAK, "shadow_bytes_per_step": nbytes,
                      "note": "all threshold passes of the scan together cover the N rows once; survivors are "
-                             "rescored with the exact q4 contract in mq_select; step_frac prices the whole "
-                             "step (scan, select, encoding)"},
+                             "rescored with the exact 16-bit-query q4 score in mq_select, and the best "
+                             "k + k/16 with the reference arithmetic in ref_finish; step_frac prices the whole "
+                             "step (scan, select, finish, encoding)"},
         "pack_candidates": {"us_per_call": pfam["pack_candidates"][1] * 1000.0, "rows": nq * k,
                             "bytes_per_call": pack_bytes,
                             "GB_s": pack_bytes / (pfam["pack_candidates"][1] / 1000.0) / 1e9},
+        **c2_cpu(queries, packed, scales, k, cpu_s),
     }
 
 
-def run_c3(rt, steps, warmup) -> dict:
-    """Config 3: q8 l2_distance rerank, smallest-1000, Q=32, N=8,388,608, D=128."""
+def c2_cpu(queries, packed, scales, k, cpu_s) -> dict:
+    if cpu_s <= 0:
+        return {"cpu_baseline": None, "fair_cpu": None}
+    from oracle import oracle as orc
+
+    nq, d = queries.shape
+    n = packed.shape[0]
+    nt = _fair_threads()
+
+    def one(i):
+        orc.topk(orc.ref_score_q4("cosine", queries[i:i + 1], packed, scales, d), k)
+
+    cpu = _ref_cpu("candidates/s", n, cpu_s, one, "queries (cosineRows over the dequantized q4 rows + "
+                   "full-sort topKTensor)", nq)
+    done, el = _budget_loop(cpu_s / 2, lambda i: orc.fair_q4_topk("cosine", queries[(8 * i) % nq:(8 * i) % nq + 8],
+                                                                   packed, scales, d, k, threads=nt), nq // 8)
+    fair = {"value": done * 8 * n / el, "unit": "candidates/s", "cores": nt, "kind": "fair",
+            "sample": "%d batches of 8 queries, 16-bit-query q4 cosine on the nibbles, heap top-k, %d threads, "
+                      "%.1f s" % (done, nt, el)}
+    return {"cpu_baseline": cpu, "fair_cpu": fair}
+
+
+def run_c3(rt, steps, warmup, cpu_s) -> dict:
+    """Config 3: q8 l2_distance rerank, smallest-1000, Q=32, N=8,388,608,
+    D=128, with the reference's l2DistanceRows on the dequantized rows."""
     from manta_amd import synth
 
     queries, codes, scales = synth.config3()
@@ -242,11 +337,10 @@ def run_c3(rt, steps, warmup) -> dict:
     n = codes.shape[0]
     k = 1000
     cands = rt.bind_q8(codes, scales)
-    del codes
     qd = rt.to_device(queries)
     ids = rt.empty((nq, k), np.int32)
     sc = rt.empty((nq, k), np.float32)
-    fams = ["mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
+    fams = ["mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear", "ref_rescore", "ref_finish", "ref_scan"]
     step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "l2_distance", qd, k, smallest=True,
                                                            out=(ids, sc, None)), steps, warmup, fams)
     dom = "mq_scan" if fam["mq_scan"][0] else "q8_scan"
@@ -255,6 +349,7 @@ def run_c3(rt, steps, warmup) -> dict:
     cands.close()
     return {
         "workload": "c3_q8_l2_smallest1000", "shape": {"q": nq, "n": n, "d": d, "k": k},
+        "semantics": "reference l2DistanceRows on the dequantized q8 values (ids and scores bit-exact)",
         "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0,
         "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK, "unit": "GB/s",
@@ -262,13 +357,39 @@ def run_c3(rt, steps, warmup) -> dict:
                      "bytes_per_step": nbytes,
                      "traffic": profiled_traffic("mq_scan_c3_l2_smallest1000.md", "traffic_bytes_per_step"),
                      "traffic_source": "profiles/mq_scan_c3_l2_smallest1000.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
-                     "note": "all threshold passes of the scan together cover the N rows once"},
+                     "step_frac": nbytes / (dev_ms / 1000.0) / 1e9 / HBM_PEAK,
+                     "note": "all threshold passes of the scan together cover the N rows once; step_frac "
+                             "prices the whole step (scan, select, finish)"},
+        **c3_cpu(queries, codes, scales, k, cpu_s),
     }
 
 
-def run_c4(rt, steps, warmup) -> dict:
+def c3_cpu(queries, codes, scales, k, cpu_s) -> dict:
+    if cpu_s <= 0:
+        return {"cpu_baseline": None, "fair_cpu": None}
+    from oracle import oracle as orc
+
+    nq, d = queries.shape
+    n = codes.shape[0]
+    nt = _fair_threads()
+
+    def one(i):
+        orc.topk(orc.ref_score_q8("l2_distance", queries[i:i + 1], codes, scales), k, smallest=True)
+
+    cpu = _ref_cpu("candidates/s", n, cpu_s, one, "queries (l2DistanceRows over the dequantized q8 rows + "
+                   "full-sort smallest-k)", nq)
+    done, el = _budget_loop(cpu_s / 2, lambda i: orc.fair_q8_topk("l2_distance", queries[(4 * i) % nq:(4 * i) % nq + 4],
+                                                                   codes, scales, k, smallest=True, threads=nt), nq // 4)
+    fair = {"value": done * 4 * n / el, "unit": "candidates/s", "cores": nt, "kind": "fair",
+            "sample": "%d batches of 4 queries, 16-bit-query q8 l2 on the int8 rows, heap top-k, %d threads, "
+                      "%.1f s" % (done, nt, el)}
+    return {"cpu_baseline": cpu, "fair_cpu": fair}
+
+
+def run_c4(rt, steps, warmup, cpu_s) -> dict:
     """Config 4: embed 1024x64 tokens with a q8 projection, then q8 dot
-    top-50 of the 1024 embedded queries over 4,194,304 x 384 candidates."""
+    top-50 of the 1024 embedded queries over 4,194,304 x 384 candidates, with
+    BASELINE's quantized-query dot formula."""
     from manta_amd import synth
 
     tokens, mask, table, pcodes, cs, codes, scales = synth.config4()
@@ -278,7 +399,6 @@ def run_c4(rt, steps, warmup) -> dict:
     n = codes.shape[0]
     k = 50
     cands = rt.bind_q8(codes, scales)
-    del codes
     td, md, tbd, pd, csd = (rt.to_device(x) for x in (tokens, mask, table, pcodes, cs))
     emb = rt.empty((b, e), np.uint16)
     ids = rt.empty((b, k), np.int32)
@@ -286,7 +406,7 @@ def run_c4(rt, steps, warmup) -> dict:
 
     def step():
         rt.embed_pooled(td, md, tbd, pd, csd, out=emb)
-        rt.score_topk(cands, "dot", emb, k, out=(ids, sc, None))
+        rt.score_topk(cands, "dot", emb, k, out=(ids, sc, None), quantized=True)
 
     fams = ["embed", "embed_transpose", "embed_finalize", "mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
     step_s, fam, dev_ms = _timed(rt, step, steps, warmup, fams)
@@ -298,6 +418,7 @@ def run_c4(rt, steps, warmup) -> dict:
     cands.close()
     return {
         "workload": "c4_embed_q8proj_then_q8dot_top50", "shape": {"q": b, "t": t, "d": d, "n": n, "k": k},
+        "semantics": "BASELINE's q8 dot formula (query codes round(q*127), int32 accumulation)",
         "value": b * n / step_s, "unit": "candidates/s (end to end, embed included)",
         "ms_per_step": step_s * 1000.0, "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         "embed": {"tokens_per_s_kernel": b * t / (fam["embed"][1] / 1000.0),
@@ -306,10 +427,44 @@ def run_c4(rt, steps, warmup) -> dict:
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": sc_t, "peak": I8_PEAK, "unit": "TOP/s",
                      "frac": sc_t / I8_PEAK, "scan_us_per_step": fam[dom][2] * 1000.0, "ops_per_step": ops_b,
                      "note": "all threshold passes of the scan together cover the N rows once"},
+        **c4_cpu(tokens, mask, table, pcodes, cs, codes, scales, k, cpu_s),
     }
 
 
-def run_enc(rt, steps, warmup) -> dict:
+def c4_cpu(tokens, mask, table, pcodes, cs, codes, scales, k, cpu_s) -> dict:
+    if cpu_s <= 0:
+        return {"cpu_baseline": None, "fair_cpu": None}
+    from oracle import oracle as orc
+
+    b, t = tokens.shape
+    n = codes.shape[0]
+    nt = _fair_threads()
+
+    def one(i):
+        # one query end to end: its sequence's embedding, dotRows over the
+        # dequantized rows, full-sort top-k
+        j = i % b
+        q16, _ = orc.embed(tokens[j:j + 1], mask[j:j + 1], table, proj_codes=pcodes, col_scale=cs)
+        qf = orc.f16_to_f32(q16)[0]
+        orc.topk(orc.ref_score_q8("dot", q16, codes, scales)[0], k)
+        del qf
+
+    cpu = _ref_cpu("candidates/s", n, cpu_s, one, "queries end to end (embed of one sequence, dotRows over the "
+                   "dequantized q8 rows, full-sort topKTensor)", b)
+
+    def fair_one(i):
+        q = orc.fair_embed(tokens[(16 * i) % b:(16 * i) % b + 16], mask[(16 * i) % b:(16 * i) % b + 16], table,
+                           proj_codes=pcodes, col_scale=cs, threads=nt)
+        orc.fair_q8_topk("dot", orc.f32_to_f16(q), codes, scales, k, threads=nt)
+
+    done, el = _budget_loop(cpu_s / 2, fair_one, b // 16)
+    fair = {"value": done * 16 * n / el, "unit": "candidates/s", "cores": nt, "kind": "fair",
+            "sample": "%d batches of 16 queries end to end (f32 embed, BASELINE's q8 dot on the int8 rows, heap "
+                      "top-k), %d threads, %.1f s" % (done, nt, el)}
+    return {"cpu_baseline": cpu, "fair_cpu": fair}
+
+
+def run_enc(rt, steps, warmup, cpu_s) -> dict:
     """The encoder forward of examples/encoder_trainable_q8.manta
     (embed_pooled_batch) at C4's embed shape: 1024 sequences of 64 tokens,
     vocabulary 32000, d = 384, ffn width h = 1536; random q8 weights."""
@@ -356,7 +511,8 @@ def run_c0(rt, args) -> dict:
     ids = rt.empty((args.sets, K), np.int32)
     sc = rt.empty((args.sets, K), np.float32)
     # the headline: exactly W untimed warmup steps, then K timed ones
-    step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "dot", q_dev, K, out=(ids, sc, None)),
+    step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "dot", q_dev, K, out=(ids, sc, None),
+                                                           quantized=True),
                                  args.steps, args.warmup, ["q8_scan"], min_warm_s=0.0)
     # one fused launch per step: the uninstrumented run's device time per
     # step (two HIP events around the K timed steps) bounds the kernel's
@@ -371,7 +527,8 @@ def run_c0(rt, args) -> dict:
     q1 = rt.to_device(queries[:1])
     one = rt.bind_q8(codes[0], scales[0])
     ids1 = rt.empty((1, K), np.int32)
-    single_s, _, _ = _timed(rt, lambda: rt.score_topk(one, "dot", q1, K, out=(ids1, None, None)), 200, 5, [])
+    single_s, _, _ = _timed(rt, lambda: rt.score_topk(one, "dot", q1, K, out=(ids1, None, None), quantized=True),
+                            200, 5, [])
     line = {
         "metric": "candidates scored/sec (q8 dot + top-k, BASELINE config 0 shape)",
         "value": args.sets * N / step_s,
@@ -390,6 +547,7 @@ def run_c0(rt, args) -> dict:
             "n": N, "d": D, "k": K,
             "problems_per_step": args.sets,
             "layout": "[Q,D] x [Q,N,D]: one query per distinct 65536x256 q8 candidate set",
+            "semantics": "BASELINE config 0's q8 dot formula (query codes round(q*127), int32 accumulation)",
         },
         "roofline": {
             "bound": "hbm",
@@ -411,8 +569,11 @@ def run_c0(rt, args) -> dict:
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(codes, scales, queries, args.cpu_seconds)
+        line["fair_cpu"] = fair_c0(codes, scales, queries, args.cpu_seconds / 2)
     else:
         line["cpu_baseline"] = None
+        line["fair_cpu"] = None
+    line["host"] = host_info()
     cands.close()
     one.close()
     return line
@@ -424,8 +585,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sets", type=int, default=32, help="C0 problems per step")
-    ap.add_argument("--workload", default="c0", choices=["c0", "c1", "c2", "c3", "c4", "enc", "all"],
-                    help="c0 is the headline line; the others (or all) are added under 'configs'")
+    ap.add_argument("--workload", default="all", choices=["c0", "c1", "c2", "c3", "c4", "enc", "all", "full"],
+                    help="c0 is the headline line; the others are added under 'configs' (all: c1-c4; "
+                         "full: c1-c4 and the encoder)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -443,13 +605,19 @@ def main() -> int:
 
     rt = rocm.Runtime(0)
     extra = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "enc": run_enc}
-    todo = list(extra) if args.workload == "all" else ([args.workload] if args.workload in extra else [])
+    if args.workload == "all":
+        todo = ["c1", "c2", "c3", "c4"]
+    elif args.workload == "full":
+        todo = list(extra)
+    else:
+        todo = [args.workload] if args.workload in extra else []
     heavy_steps = max(3, min(args.steps, 10))
     configs = {}
     for w in todo:
         print("bench: %s" % w, file=sys.stderr, flush=True)
         steps = args.steps if w == "c1" else heavy_steps
-        configs[w] = extra[w](rt, steps, min(args.warmup, 2) if w != "c1" else args.warmup)
+        cpu_s = 0.0 if args.no_cpu else args.cpu_seconds
+        configs[w] = extra[w](rt, steps, min(args.warmup, 2) if w != "c1" else args.warmup, cpu_s)
     print("bench: c0", file=sys.stderr, flush=True)
     line = run_c0(rt, args)
     if configs:

@@ -117,11 +117,16 @@ struct RefArgs {
     int* redo;                  // [nq] 1: the query goes to ref_scan
     uint64_t* redo_tau;         // [nq] threshold key ref_scan starts from (0: none)
 };
-hipError_t launch_ref_finish(const RefArgs& a, hipStream_t s);
-// Reference scores of every row (score matrix: a.out_scores) or top-k with
-// the streaming reservoir and last-workgroup merge (ScanArgs as for the
-// streaming scans).  redo / redo_tau (may be null: every query, no bound).
-hipError_t launch_ref_scan(int fmt, int op, const ScanArgs& a, const double* sqd, const int* redo,
+// keys [nq][kp]: the reference key of each candidate (ref_rescore), then
+// the finish over them.
+hipError_t launch_ref_rescore(const RefArgs& a, uint64_t* keys, hipStream_t s);
+hipError_t launch_ref_finish(const RefArgs& a, const uint64_t* keys, hipStream_t s);
+// Reference scores of every row (score matrix: a.out_scores, grid
+// (parts, nq)) or top-k with the streaming reservoir and last-workgroup merge
+// (ScanArgs as for the streaming scans; grid (parts, R), each blockIdx.y
+// taking every R-th query).  redo / redo_tau (may be null: every query, no
+// bound).
+hipError_t launch_ref_scan(int fmt, int op, const ScanArgs& a, int nq, const double* sqd, const int* redo,
                            const uint64_t* redo_tau, dim3 grid, size_t lds, hipStream_t s);
 
 // Arguments of the multi-query scan kernel (kernels_mq.hip): nq queries

@@ -2,9 +2,10 @@
 // cosineRows, l2DistanceRows; runtime/backend/tensor_ops.go:1366-1490) on the
 // values packed q8 / q4 rows stand for.
 //
-// ref_finish_kernel (one workgroup per query): the quantized-query scans
-// return their best kp rows; this kernel rescores them with the reference
-// arithmetic, sorts them by (score, index) as topKTensor does
+// ref_rescore_kernel (one candidate per thread): the quantized-query scans
+// return their best kp rows; each is rescored with the reference arithmetic.
+// ref_finish_kernel (one workgroup per query) sorts them by (score, index)
+// as topKTensor does
 // (tensor_ops.go:1539-1551), and keeps the best k if the bounds of
 // ref_common.hpp prove that no row outside the kp can reach the k-th: for
 // largest-first, every outside row has a scan score of at most that of the
@@ -37,40 +38,67 @@ __device__ __forceinline__ float ref_row_score(const void* codes, const void* sc
 // Keys of the finish: next_pow2(kp) <= kRefMaxKeys in LDS.
 constexpr int kRefMaxKeys = 4096;
 
+// Reference keys of the scan's kp candidates of each query: one candidate per
+// thread, grid (ceil(kp / 256), nq).  keys [nq][kp] (0 for an invalid id).
 template <int FMT, int OP>
-__global__ __launch_bounds__(256) void ref_finish_kernel(RefArgs a) {
-    extern __shared__ uint64_t keys[];
+__global__ __launch_bounds__(256) void ref_rescore_kernel(RefArgs a, uint64_t* __restrict__ keys) {
     __shared__ float qf[kMaxQueryDim];
-    __shared__ float red_m[4];
-    __shared__ double red_g[4], red_n[4];
-    __shared__ long long red_s[4];
     __shared__ double sqn_s;
+    const int q = blockIdx.y;
+    const int d = a.d;
+    const uint16_t* qrow = a.queries + (int64_t)q * d;
+    for (int c = threadIdx.x; c < d; c += 256) qf[c] = h2f(qrow[c]);
+    __syncthreads();
+    if (OP == OP_COSINE && threadIdx.x == 0) sqn_s = ref_sqrt_norm(qf, d);
+    __syncthreads();
+    const double sqn = OP == OP_COSINE ? sqn_s : 0.0;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.kp) return;
+    const int32_t id = a.cand_ids[(int64_t)q * a.kp + i];
+    uint64_t key = 0;
+    if (id >= 0 && (int64_t)id < a.n) {
+        const float s = ref_row_score<FMT, OP>(a.codes, a.scales, a.sqd, (int64_t)q * a.set_stride + id, a.pitch, d,
+                                               qf, sqn);
+        key = make_key(s, (uint32_t)id, a.smallest);
+    }
+    keys[(int64_t)q * a.kp + i] = key;
+}
+
+// One workgroup per query: sort the candidates' reference keys, take the
+// k-th, and prove (or not) from the scan score of the kp-th candidate that
+// no other row reaches it.
+template <int OP, int NT>
+__global__ __launch_bounds__(NT) void ref_finish_kernel(RefArgs a, const uint64_t* __restrict__ cand_keys) {
+    constexpr int NW = NT / 64;
+    extern __shared__ uint64_t keys[];
+    __shared__ float red_m[NW];
+    __shared__ double red_g[NW], red_n[NW];
+    __shared__ long long red_s[NW];
     __shared__ int ok_s;
     const int q = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int d = a.d;
     const uint16_t* qrow = a.queries + (int64_t)q * d;
+    const int kp = a.kp;
+    const int S = next_pow2(kp < 2 ? 2 : kp);
+    for (int i = tid; i < S; i += NT) keys[i] = i < kp ? cand_keys[(int64_t)q * kp + i] : 0ull;
 
-    // the query as f32, and the quantities of the bounds: the scans' E16
-    // codes of it (same arithmetic as encode_query_block), G = |q - qs*code|,
-    // |q| and sum code^2
+    // the quantities of the bounds: the scans' E16 codes of the query (same
+    // arithmetic as encode_query_block), G = |q - qs*code|, |q|, sum code^2
     float m = 0.0f;
-    for (int c = tid; c < d; c += 256) {
-        const float x = h2f(qrow[c]);
-        qf[c] = x;
-        m = fmaxf(m, __builtin_fabsf(x));
-    }
+    for (int c = tid; c < d; c += NT) m = fmaxf(m, __builtin_fabsf(h2f(qrow[c])));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if (lane == 0) red_m[wave] = m;
     __syncthreads();
-    const float maxabs = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    float maxabs = 0.0f;
+    for (int w = 0; w < NW; w++) maxabs = fmaxf(maxabs, red_m[w]);
     const float inv = maxabs == 0.0f ? 0.0f : fdiv_rn(32639.0f, maxabs);
     const float qs = maxabs == 0.0f ? 0.0f : fdiv_rn(maxabs, 32639.0f);
     double g2 = 0.0, n2 = 0.0;
     long long ss = 0;
-    for (int c = tid; c < d; c += 256) {
-        const float x = qf[c];
+    for (int c = tid; c < d; c += NT) {
+        const float x = h2f(qrow[c]);
         const int code = maxabs != 0.0f ? code_e16(x, inv) : 0;
         const double diff = (double)x - (double)code * (double)qs;
         g2 += diff * diff;
@@ -88,27 +116,8 @@ __global__ __launch_bounds__(256) void ref_finish_kernel(RefArgs a) {
         red_n[wave] = n2;
         red_s[wave] = ss;
     }
-    if (OP == OP_COSINE && tid == 0) sqn_s = ref_sqrt_norm(qf, d);
     __syncthreads();
-    const double sqn = OP == OP_COSINE ? sqn_s : 0.0;
-
-    // reference keys of the kp candidates, then the sort
-    const int kp = a.kp;
-    const int S = next_pow2(kp < 2 ? 2 : kp);
-    const int64_t set0 = (int64_t)q * a.set_stride;
-    for (int i = tid; i < S; i += 256) {
-        uint64_t key = 0;
-        if (i < kp) {
-            const int32_t id = a.cand_ids[(int64_t)q * kp + i];
-            if (id >= 0 && (int64_t)id < a.n) {
-                const float s = ref_row_score<FMT, OP>(a.codes, a.scales, a.sqd, set0 + id, a.pitch, d, qf, sqn);
-                key = make_key(s, (uint32_t)id, a.smallest);
-            }
-        }
-        keys[i] = key;
-    }
-    __syncthreads();
-    block_sort_desc_regs<256>(keys, S);
+    block_sort_desc_regs<NT>(keys, S);
 
     if (tid == 0) {
         const uint64_t kth = keys[a.k - 1];
@@ -121,10 +130,16 @@ __global__ __launch_bounds__(256) void ref_finish_kernel(RefArgs a) {
                 ok = true;
             } else {
                 const double up = 1.0 + 9.094947017729282e-13;
-                const double G = __builtin_sqrt(red_g[0] + red_g[1] + red_g[2] + red_g[3]) * up;
-                const double qn = __builtin_sqrt(red_n[0] + red_n[1] + red_n[2] + red_n[3]) * up;
-                const double qh =
-                    __builtin_sqrt((double)(red_s[0] + red_s[1] + red_s[2] + red_s[3])) * (double)qs * up;
+                double sg = 0.0, sn = 0.0;
+                long long sc = 0;
+                for (int w = 0; w < NW; w++) {
+                    sg += red_g[w];
+                    sn += red_n[w];
+                    sc += red_s[w];
+                }
+                const double G = __builtin_sqrt(sg) * up;
+                const double qn = __builtin_sqrt(sn) * up;
+                const double qh = __builtin_sqrt((double)sc) * (double)qs * up;
                 const double wide = 1.0 + 2.384185791015625e-07;  // 1 + 2^-22
                 const RefBounds b = ref_bounds(OP, G, qn, qh, (double)a.e_qd, (double)a.maxdn * wide,
                                                (double)a.maxdd * wide, d);
@@ -140,52 +155,78 @@ __global__ __launch_bounds__(256) void ref_finish_kernel(RefArgs a) {
     }
     __syncthreads();
     if (!ok_s) return;
-    for (int i = tid; i < a.k; i += 256) {
+    for (int i = tid; i < a.k; i += NT) {
         const uint64_t key = keys[i];
         a.out_ids[(int64_t)q * a.k + i] = key ? (int32_t)key_index(key) : -1;
         if (a.out_scores) a.out_scores[(int64_t)q * a.k + i] = key ? key_score(key, a.smallest) : 0.0f;
     }
 }
 
+// Reference scores of every row, lane = row.  Score matrix (a.out_scores):
+// grid (parts, nq), one query per blockIdx.y.  Top-k: grid (parts, R); the
+// workgroups of blockIdx.y = r take the queries r, r + R, ... the finish
+// marked (redo == nullptr: all of them), each with the streaming reservoir
+// from the threshold key redo_tau and the last-workgroup merge over the
+// gridDim.x parts.  A query nobody marked costs its workgroups one flag read.
 template <int FMT, int OP>
-__global__ __launch_bounds__(256) void ref_scan_kernel(ScanArgs a, const double* __restrict__ sqd,
+__global__ __launch_bounds__(256) void ref_scan_kernel(ScanArgs a, int nq, const double* __restrict__ sqd,
                                                        const int* __restrict__ redo,
                                                        const uint64_t* __restrict__ redo_tau) {
     extern __shared__ uint64_t topk_keys[];
     __shared__ ScanTopkLds S;
     __shared__ float qf[kMaxQueryDim];
     __shared__ double sqn_s;
-    const int qi = blockIdx.y;
+    __shared__ int marked[256];
+    __shared__ int nmarked;
     const bool topk = a.out_scores == nullptr;
-    if (topk && redo && !redo[qi]) return;  // whole workgroup: the finish proved this query
-    const uint64_t tau0 = (topk && redo_tau) ? redo_tau[qi] : 0ull;
-    const uint16_t* qrow = a.queries + (int64_t)qi * a.d;
-    for (int c = threadIdx.x; c < a.d; c += 256) qf[c] = h2f(qrow[c]);
-    __syncthreads();
-    if (OP == OP_COSINE && threadIdx.x == 0) sqn_s = ref_sqrt_norm(qf, a.d);
-    if (topk) topk_init(topk_keys, &S.st);  // (its barrier publishes sqn_s)
-    else __syncthreads();
-    const double sqn = OP == OP_COSINE ? sqn_s : 0.0;
-    const int64_t set_row0 = (int64_t)qi * a.set_stride;
-    const int64_t wg_row0 = (int64_t)blockIdx.x * a.rounds * 256;
-    for (int r = 0; r < a.rounds; r++) {
-        const int64_t row = wg_row0 + (int64_t)r * 256 + threadIdx.x;
-        const bool valid = row < a.n;
-        float s = 0.0f;
-        if (valid) s = ref_row_score<FMT, OP>(a.codes, a.scales, sqd, set_row0 + row, a.pitch, a.d, qf, sqn);
-        if (!topk) {
-            if (valid) a.out_scores[(int64_t)qi * a.n + row] = s;
-            continue;
+    // this slot's queries, 256 at a time: the marks are read in parallel and
+    // the marked queries listed in LDS (the list is usually empty)
+    const int per_slot = (nq - (int)blockIdx.y + (int)gridDim.y - 1) / (int)gridDim.y;
+    for (int base = 0; base < per_slot; base += 256) {
+        __syncthreads();  // the previous batch's list is consumed
+        if (threadIdx.x == 0) nmarked = 0;
+        __syncthreads();
+        {
+            const int j = base + (int)threadIdx.x;
+            const int qj = (int)blockIdx.y + j * (int)gridDim.y;
+            if (j < per_slot && (!topk || !redo || redo[qj])) marked[atomicAdd(&nmarked, 1)] = qj;
         }
-        const uint64_t key = valid ? make_key(s, (uint32_t)row, a.smallest) : 0ull;
-        const uint64_t tau = S.st.tau > tau0 ? S.st.tau : tau0;
-        topk_offer(key, tau, topk_keys, &S.st);
-        if (a.mid_compact) {
+        __syncthreads();
+        const int nm = nmarked;
+        for (int mi = 0; mi < nm; mi++) {
+            const int qi = marked[mi];
+            const uint64_t tau0 = (topk && redo_tau) ? redo_tau[qi] : 0ull;
+            __syncthreads();  // the previous query's readers of qf and the reservoir are done
+            const uint16_t* qrow = a.queries + (int64_t)qi * a.d;
+            for (int c = threadIdx.x; c < a.d; c += 256) qf[c] = h2f(qrow[c]);
             __syncthreads();
-            topk_maybe_compact(topk_keys, &S.st, a.k, a.cap);
+            if (OP == OP_COSINE && threadIdx.x == 0) sqn_s = ref_sqrt_norm(qf, a.d);
+            if (topk) topk_init(topk_keys, &S.st);  // (its barrier publishes sqn_s)
+            else __syncthreads();
+            const double sqn = OP == OP_COSINE ? sqn_s : 0.0;
+            const int64_t set_row0 = (int64_t)qi * a.set_stride;
+            const int64_t wg_row0 = (int64_t)blockIdx.x * a.rounds * 256;
+            for (int r = 0; r < a.rounds; r++) {
+                const int64_t row = wg_row0 + (int64_t)r * 256 + threadIdx.x;
+                const bool valid = row < a.n;
+                float s = 0.0f;
+                if (valid)
+                    s = ref_row_score<FMT, OP>(a.codes, a.scales, sqd, set_row0 + row, a.pitch, a.d, qf, sqn);
+                if (!topk) {
+                    if (valid) a.out_scores[(int64_t)qi * a.n + row] = s;
+                    continue;
+                }
+                const uint64_t key = valid ? make_key(s, (uint32_t)row, a.smallest) : 0ull;
+                const uint64_t tau = S.st.tau > tau0 ? S.st.tau : tau0;
+                topk_offer(key, tau, topk_keys, &S.st);
+                if (a.mid_compact) {
+                    __syncthreads();
+                    topk_maybe_compact(topk_keys, &S.st, a.k, a.cap);
+                }
+            }
+            if (topk) finish_topk(a, topk_keys, S, qi);
         }
     }
-    if (topk) finish_topk(a, topk_keys, S, qi);
 }
 
 // ----------------------------------------------------------------- hosts
@@ -196,50 +237,81 @@ static int next_pow2_host(int x) {
     return p;
 }
 
+template <int FMT, int OP>
+static void launch_ref_rescore_op(const RefArgs& a, uint64_t* keys, hipStream_t s) {
+    const dim3 grid((unsigned)((a.kp + 255) / 256), (unsigned)a.nq);
+    hipLaunchKernelGGL((ref_rescore_kernel<FMT, OP>), grid, dim3(256), 0, s, a, keys);
+}
+
 template <int FMT>
-static hipError_t launch_ref_finish_fmt(const RefArgs& a, size_t lds, hipStream_t s) {
-    const dim3 grid((unsigned)a.nq), block(256);
+static void launch_ref_rescore_fmt(const RefArgs& a, uint64_t* keys, hipStream_t s) {
     switch (a.op) {
-        case OP_DOT: hipLaunchKernelGGL((ref_finish_kernel<FMT, OP_DOT>), grid, block, lds, s, a); break;
-        case OP_COSINE: hipLaunchKernelGGL((ref_finish_kernel<FMT, OP_COSINE>), grid, block, lds, s, a); break;
-        default: hipLaunchKernelGGL((ref_finish_kernel<FMT, OP_L2>), grid, block, lds, s, a); break;
+        case OP_DOT: launch_ref_rescore_op<FMT, OP_DOT>(a, keys, s); break;
+        case OP_COSINE: launch_ref_rescore_op<FMT, OP_COSINE>(a, keys, s); break;
+        default: launch_ref_rescore_op<FMT, OP_L2>(a, keys, s); break;
+    }
+}
+
+hipError_t launch_ref_rescore(const RefArgs& a, uint64_t* keys, hipStream_t s) {
+    if (a.d <= 0 || a.d > kMaxQueryDim || a.kp <= 0 || a.nq <= 0 || a.nq > 65535) return hipErrorInvalidValue;
+    if (a.fmt == 4 && a.d % 32 != 0) return hipErrorInvalidValue;
+    if (a.fmt == 8) launch_ref_rescore_fmt<8>(a, keys, s);
+    else launch_ref_rescore_fmt<4>(a, keys, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_ref_finish(const RefArgs& a, const uint64_t* keys, hipStream_t s) {
+    if (a.d <= 0 || a.d > kMaxQueryDim || a.k <= 0 || a.kp < a.k || a.nq <= 0) return hipErrorInvalidValue;
+    const int S = next_pow2_host(a.kp);
+    if (S > kRefMaxKeys) return hipErrorInvalidValue;
+    const size_t lds = (size_t)S * 8;
+    const dim3 grid((unsigned)a.nq);
+    // 1024 threads sort the larger candidate sets (fewer register slots and
+    // network steps per thread)
+    if (S > 512) {
+        switch (a.op) {
+            case OP_DOT: hipLaunchKernelGGL((ref_finish_kernel<OP_DOT, 1024>), grid, dim3(1024), lds, s, a, keys); break;
+            case OP_COSINE:
+                hipLaunchKernelGGL((ref_finish_kernel<OP_COSINE, 1024>), grid, dim3(1024), lds, s, a, keys);
+                break;
+            default: hipLaunchKernelGGL((ref_finish_kernel<OP_L2, 1024>), grid, dim3(1024), lds, s, a, keys); break;
+        }
+    } else {
+        switch (a.op) {
+            case OP_DOT: hipLaunchKernelGGL((ref_finish_kernel<OP_DOT, 256>), grid, dim3(256), lds, s, a, keys); break;
+            case OP_COSINE:
+                hipLaunchKernelGGL((ref_finish_kernel<OP_COSINE, 256>), grid, dim3(256), lds, s, a, keys);
+                break;
+            default: hipLaunchKernelGGL((ref_finish_kernel<OP_L2, 256>), grid, dim3(256), lds, s, a, keys); break;
+        }
     }
     return hipGetLastError();
 }
 
-hipError_t launch_ref_finish(const RefArgs& a, hipStream_t s) {
-    if (a.d <= 0 || a.d > kMaxQueryDim || a.k <= 0 || a.kp < a.k || a.nq <= 0) return hipErrorInvalidValue;
-    if (a.fmt == 4 && a.d % 32 != 0) return hipErrorInvalidValue;
-    const int S = next_pow2_host(a.kp);
-    if (S > kRefMaxKeys) return hipErrorInvalidValue;
-    const size_t lds = (size_t)S * 8;
-    return a.fmt == 8 ? launch_ref_finish_fmt<8>(a, lds, s) : launch_ref_finish_fmt<4>(a, lds, s);
-}
-
 template <int FMT>
-static hipError_t launch_ref_scan_fmt(int op, const ScanArgs& a, const double* sqd, const int* redo,
+static hipError_t launch_ref_scan_fmt(int op, const ScanArgs& a, int nq, const double* sqd, const int* redo,
                                       const uint64_t* redo_tau, dim3 grid, size_t lds, hipStream_t s) {
     const dim3 block(256);
     switch (op) {
         case OP_DOT:
-            hipLaunchKernelGGL((ref_scan_kernel<FMT, OP_DOT>), grid, block, lds, s, a, sqd, redo, redo_tau);
+            hipLaunchKernelGGL((ref_scan_kernel<FMT, OP_DOT>), grid, block, lds, s, a, nq, sqd, redo, redo_tau);
             break;
         case OP_COSINE:
-            hipLaunchKernelGGL((ref_scan_kernel<FMT, OP_COSINE>), grid, block, lds, s, a, sqd, redo, redo_tau);
+            hipLaunchKernelGGL((ref_scan_kernel<FMT, OP_COSINE>), grid, block, lds, s, a, nq, sqd, redo, redo_tau);
             break;
         default:
-            hipLaunchKernelGGL((ref_scan_kernel<FMT, OP_L2>), grid, block, lds, s, a, sqd, redo, redo_tau);
+            hipLaunchKernelGGL((ref_scan_kernel<FMT, OP_L2>), grid, block, lds, s, a, nq, sqd, redo, redo_tau);
             break;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_ref_scan(int fmt, int op, const ScanArgs& a, const double* sqd, const int* redo,
+hipError_t launch_ref_scan(int fmt, int op, const ScanArgs& a, int nq, const double* sqd, const int* redo,
                            const uint64_t* redo_tau, dim3 grid, size_t lds, hipStream_t s) {
-    if (a.d <= 0 || a.d > kMaxQueryDim) return hipErrorInvalidValue;
+    if (a.d <= 0 || a.d > kMaxQueryDim || nq <= 0) return hipErrorInvalidValue;
     if (fmt == 4 && a.d % 32 != 0) return hipErrorInvalidValue;
-    return fmt == 8 ? launch_ref_scan_fmt<8>(op, a, sqd, redo, redo_tau, grid, lds, s)
-                    : launch_ref_scan_fmt<4>(op, a, sqd, redo, redo_tau, grid, lds, s);
+    return fmt == 8 ? launch_ref_scan_fmt<8>(op, a, nq, sqd, redo, redo_tau, grid, lds, s)
+                    : launch_ref_scan_fmt<4>(op, a, nq, sqd, redo, redo_tau, grid, lds, s);
 }
 
 }  // namespace manta

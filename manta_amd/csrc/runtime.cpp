@@ -1103,8 +1103,8 @@ int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* c, int op, const 
         a.rounds = (int)std::max<int64_t>(1, std::min<int64_t>(16, tiles * nq / 2048));
         a.out_scores = out;
         const int64_t parts = (tiles + a.rounds - 1) / a.rounds;
-        LAUNCH_TRY(manta::launch_ref_scan(c->format == MANTA_ROCM_Q8_ROWS ? 8 : 4, so.ref, a, c->sqd, nullptr,
-                                          nullptr, dim3((unsigned)parts, (unsigned)nq), 0, rt->stream),
+        LAUNCH_TRY(manta::launch_ref_scan(c->format == MANTA_ROCM_Q8_ROWS ? 8 : 4, so.ref, a, (int)nq, c->sqd,
+                                          nullptr, nullptr, dim3((unsigned)parts, (unsigned)nq), 0, rt->stream),
                    "ref_scan");
         return MANTA_ROCM_OK;
     }
@@ -1174,13 +1174,14 @@ int ref_topk(MantaRocm* rt, const MantaRocmCandidates* c, const ScoreOp& so, int
         // scores across the kp-th row are what would send a query to the
         // full rescan
         const int64_t kp = std::min<int64_t>(std::min<int64_t>(c->n, kMaxDeviceK),
-                                             k + std::max<int64_t>(16, k / 16));
-        const size_t need = (size_t)nq * kp * 8 + (size_t)nq * 12 + 1024;
+                                             k + std::max<int64_t>(8, k / 32));
+        const size_t need = (size_t)nq * kp * 16 + (size_t)nq * 12 + 2048;
         int rc = ensure_ref_workspace(rt, need, err);
         if (rc) return rc;
         Carver cv(rt->ws_ref);
         int32_t* cand_ids = cv.take<int32_t>((size_t)nq * kp);
         float* cand_scores = cv.take<float>((size_t)nq * kp);
+        uint64_t* cand_keys = cv.take<uint64_t>((size_t)nq * kp);
         redo = cv.take<int>((size_t)nq);
         redo_tau = cv.take<uint64_t>((size_t)nq);
         rc = scan_topk(rt, c, so.scan, order, q, nq, kp, cand_ids, cand_scores, nullptr, err);
@@ -1212,19 +1213,23 @@ int ref_topk(MantaRocm* rt, const MantaRocmCandidates* c, const ScoreOp& so, int
         ra.out_scores = out_scores;
         ra.redo = redo;
         ra.redo_tau = redo_tau;
-        LAUNCH_TRY(manta::launch_ref_finish(ra, rt->stream), "ref_finish");
+        LAUNCH_TRY(manta::launch_ref_rescore(ra, cand_keys, rt->stream), "ref_rescore");
+        LAUNCH_TRY(manta::launch_ref_finish(ra, cand_keys, rt->stream), "ref_finish");
     }
-    // the full rescan (workgroups of proven queries exit at once): about 2048
-    // workgroups in all, at least one per query
+    // The full rescan of the queries the finish marked: parts of up to 64
+    // rounds per query, and R query slots, each taking every R-th query, so
+    // that about 256 workgroups check the marks when nothing is marked (all
+    // queries when the scans were skipped).
     const int64_t tiles = (c->n + 255) / 256;
-    const int64_t want_parts = std::max<int64_t>(1, std::min<int64_t>(tiles, 2048 / nq));
-    const int rounds = (int)std::max<int64_t>(1, std::min<int64_t>(64, (tiles + want_parts - 1) / want_parts));
+    const int rounds = (int)std::max<int64_t>(1, std::min<int64_t>(64, (tiles + 63) / 64));
     StreamTopk st = stream_topk_shape(c, nq, k, rounds);
+    const int64_t R = redo ? std::max<int64_t>(1, std::min<int64_t>(nq, 256 / std::max<int64_t>(1, st.parts)))
+                           : std::min<int64_t>(nq, 65535);
     int rc = ensure_workspace(rt, (size_t)nq * st.parts * k * 8 + 256, err);
     if (rc) return rc;
     ScanArgs a = stream_topk_args(rt, c, q, st, k, order, out_ids, out_scores);
-    LAUNCH_TRY(manta::launch_ref_scan(fmt, so.ref, a, c->sqd, redo, redo_tau,
-                                      dim3((unsigned)st.parts, (unsigned)nq), (size_t)a.lds_keys * 8, rt->stream),
+    LAUNCH_TRY(manta::launch_ref_scan(fmt, so.ref, a, (int)nq, c->sqd, redo, redo_tau,
+                                      dim3((unsigned)st.parts, (unsigned)R), (size_t)a.lds_keys * 8, rt->stream),
                "ref_scan");
     return MANTA_ROCM_OK;
 }

@@ -154,6 +154,27 @@ void orc_score_q4(int op, const uint16_t* queries, int64_t nq,
                   const float* dnorm, const float* dd, int64_t sets, int64_t n,
                   int64_t d, float* out);
 
+/* ---- 3. bench.py's all-core CPU baseline (fair_cpu.c) ---------------- */
+
+/* Quantized-query scores on the packed data (same formulas as above),
+ * bounded heaps, rows split over `threads` OpenMP threads; candidates shared
+ * by every query.  out_vals may be NULL. */
+void orc_fair_q8_topk(int op, const uint16_t* queries, int64_t nq,
+                      const int8_t* codes, const float* scales,
+                      const float* dnorm, const float* dd, int64_t n, int64_t d,
+                      int64_t k, int smallest, int threads, int32_t* out_ids,
+                      float* out_vals);
+void orc_fair_q4_topk(int op, const uint16_t* queries, int64_t nq,
+                      const uint8_t* packed, const uint16_t* scales,
+                      const float* dnorm, const float* dd, int64_t n, int64_t d,
+                      int64_t k, int smallest, int threads, int32_t* out_ids,
+                      float* out_vals);
+/* The embed pipeline in f32 with sequences over threads; out f32 [b, e]. */
+void orc_fair_embed(const int32_t* tokens, const int32_t* mask, int64_t b,
+                    int64_t t, const uint16_t* table, int64_t vocab, int64_t d,
+                    const uint16_t* proj_f16, const int8_t* proj_codes,
+                    const float* col_scale, int64_t e, int threads, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,9 @@ def lib() -> C.CDLL:
             "orc_ref_score_q8": (None, [ci, p, i64, p, p, i64, i64, i64, p]),
             "orc_ref_score_q4": (None, [ci, p, i64, p, p, i64, i64, i64, p]),
             "orc_fake_quantize": (None, [p, i64, ci]),
+            "orc_fair_q8_topk": (None, [ci, p, i64, p, p, p, p, i64, i64, i64, ci, ci, p, p]),
+            "orc_fair_q4_topk": (None, [ci, p, i64, p, p, p, p, i64, i64, i64, ci, ci, p, p]),
+            "orc_fair_embed": (None, [p, p, i64, i64, p, i64, i64, p, p, p, i64, ci, p]),
             "orc_layernorm_rows": (None, [p, i64, i64]),
             "orc_softmax_rows": (None, [p, i64, i64]),
             "orc_gelu": (None, [p, i64]),
@@ -385,3 +388,52 @@ def fake_quantize(x, bits):
     x = np.array(x, dtype=np.float32, order="C", copy=True)
     lib().orc_fake_quantize(_p(x), x.size, int(bits))
     return x
+
+
+# --------------------------------------------- bench.py's fair CPU baseline
+def fair_q8_topk(op, queries, codes, scales, k, smallest=False, threads=None):
+    """Quantized-query q8 top-k on all cores (fair_cpu.c)."""
+    queries = _c(queries, np.uint16)
+    codes = _c(codes, np.int8)
+    scales = _c(scales, np.float32)
+    nq, d = queries.shape
+    n = codes.shape[0]
+    dn, dd = q8_row_consts(codes, scales) if op != "dot" else (None, None)
+    ids = np.empty((nq, k), np.int32)
+    vals = np.empty((nq, k), np.float32)
+    lib().orc_fair_q8_topk(OPS[op], _p(queries), nq, _p(codes), _p(scales), _p(dn), _p(dd), n, d, k,
+                           1 if smallest else 0, int(threads or os.cpu_count() or 1), _p(ids), _p(vals))
+    return ids, vals
+
+
+def fair_q4_topk(op, queries, packed, scales, d, k, smallest=False, threads=None):
+    queries = _c(queries, np.uint16)
+    packed = _c(packed, np.uint8)
+    scales = _c(scales, np.uint16)
+    nq = queries.shape[0]
+    n = packed.shape[0]
+    dn, dd = q4_row_consts(packed, scales, d)
+    ids = np.empty((nq, k), np.int32)
+    vals = np.empty((nq, k), np.float32)
+    lib().orc_fair_q4_topk(OPS[op], _p(queries), nq, _p(packed), _p(scales), _p(dn), _p(dd), n, d, k,
+                           1 if smallest else 0, int(threads or os.cpu_count() or 1), _p(ids), _p(vals))
+    return ids, vals
+
+
+def fair_embed(tokens, mask, table_f16, proj_f16=None, proj_codes=None, col_scale=None, threads=None):
+    tokens = _c(tokens, np.int32)
+    mask = _c(mask, np.int32)
+    table = _c(table_f16, np.uint16)
+    b, t = tokens.shape
+    vocab, d = table.shape
+    if proj_codes is not None:
+        proj_codes = _c(proj_codes, np.int8)
+        col_scale = _c(col_scale, np.float32)
+        e = proj_codes.shape[1]
+    else:
+        proj_f16 = _c(proj_f16, np.uint16)
+        e = proj_f16.shape[1]
+    out = np.empty((b, e), np.float32)
+    lib().orc_fair_embed(_p(tokens), _p(mask), b, t, _p(table), vocab, d, _p(proj_f16), _p(proj_codes),
+                         _p(col_scale), e, int(threads or os.cpu_count() or 1), _p(out))
+    return out
