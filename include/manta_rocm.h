@@ -166,6 +166,21 @@ int manta_rocm_pack_q8_rows(const float* x, int64_t n, int64_t d, int8_t* codes,
 int manta_rocm_pack_q4_blocks(const float* x, int64_t n, int64_t d, uint8_t* packed,
                               uint16_t* scales, char** err);
 
+/* Exact repacking of the f32 values a reference q8 / q4 tensor carries
+ * (bits 8 or 4) into q8 rows -- int8 codes + an f32 scale per row, bound with
+ * manta_rocm_bind_q8_rows -- so that every value is the f32 product
+ * code*scale.  *grid reports what was found: 2, the values lie on one
+ * per-tensor symmetric grid, the reference's fakeQuantizeDataInPlace
+ * (runtime/embedding_trainer.go:3738-3763; every row gets the tensor's
+ * scale, codes in [-2^(bits-1)+1, 2^(bits-1)-1]); 1, each row lies on its own
+ * grid of step maxabs_row/levels; 0, on neither, and the rows were
+ * re-quantized per row to int8 (lossy, as manta_rocm_pack_q8_rows).  With
+ * 2 or 1 the device scores equal the reference's on the original tensor.
+ * No reference counterpart: replaces the per-tensor re-quantization at load
+ * (cuda quantizeBufferInPlace, native_linux.go:2588-2619). */
+int manta_rocm_pack_grid(const float* x, int64_t n, int64_t d, int bits, int8_t* codes, float* scales, int* grid,
+                         char** err);
+
 /* Make a device-resident candidate matrix from packed host arrays:
  * `sets` independent [n, d] matrices (sets == 1: one matrix shared by every
  * query, the [Q,D] x [N,D] form; sets == Q: one per query, the reference's

@@ -96,6 +96,7 @@ SIGNATURES = {
                   C.POINTER(_p), C.POINTER(_p), _err]),
     "manta_rocm_pack_q8_rows": (C.c_int, [_p, _i64, _i64, _p, _p, _err]),
     "manta_rocm_pack_q4_blocks": (C.c_int, [_p, _i64, _i64, _p, _p, _err]),
+    "manta_rocm_pack_grid": (C.c_int, [_p, _i64, _i64, C.c_int, _p, _p, C.POINTER(C.c_int), _err]),
     "manta_rocm_bind_q8_rows": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, C.POINTER(_p), _err]),
     "manta_rocm_bind_q4_blocks": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, C.POINTER(_p), _err]),
     "manta_rocm_bind_packed": (C.c_int, [_p, _p, C.POINTER(_p), _err]),

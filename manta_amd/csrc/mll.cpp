@@ -224,6 +224,12 @@ void parse_head(MantaMll* m, const uint8_t* p, uint64_t n) {
             memcpy(&e.f64, &bits, 8);
         }
         if (e.kind == MANTA_MLL_STRING) e.str = rd32(p + at);
+        if (e.key >= m->strings.size() || (e.kind == MANTA_MLL_STRING && e.str >= m->strings.size())) {
+            m->head_error = "malformed HEAD section: entry " + std::to_string(i) + " names string " +
+                            std::to_string(e.key >= m->strings.size() ? e.key : e.str) + " of " +
+                            std::to_string(m->strings.size());
+            return;
+        }
         at += width;
         m->entries.push_back(e);
     }
@@ -246,6 +252,7 @@ void put64(std::vector<uint8_t>& b, uint64_t v) {
 // Expected byte sizes of the code and scale sections of `rows` rows of `dim`
 // values: q8 = int8 codes + one f32 scale per row, q4 = two values per byte
 // + one f16 scale per 32-value block.
+// (rows < 2^31 and dim < 2^32, so no product overflows.)
 void packed_sizes(int dtype, uint64_t rows, uint64_t dim, uint64_t* codes, uint64_t* scales) {
     if (dtype == MANTA_ROCM_Q8_ROWS) {
         *codes = rows * dim;
@@ -495,7 +502,9 @@ int manta_mll_packed_info(const MantaMll* m, int* dtype, uint64_t* rows, uint32_
     const std::string& dts = m->strings[dt->str];
     const int t = dts == "q8" ? MANTA_ROCM_Q8_ROWS : (dts == "q4" ? MANTA_ROCM_Q4_BLOCKS : 0);
     if (!t) return mll_fail(err, "packed candidates: docs_dtype \"%s\" is neither q8 nor q4", dts.c_str());
-    if (nr->i64 <= 0 || nd->i64 <= 0 || nd->i64 > 0xFFFFFFFFll || (t == MANTA_ROCM_Q4_BLOCKS && nd->i64 % 32))
+    // rows index with int32 ids and every section size must fit 64 bits
+    if (nr->i64 <= 0 || nr->i64 >= (1ll << 31) || nd->i64 <= 0 || nd->i64 > 0xFFFFFFFFll ||
+        (t == MANTA_ROCM_Q4_BLOCKS && nd->i64 % 32))
         return mll_fail(err, "packed candidates: bad shape [%lld,%lld]", (long long)nr->i64, (long long)nd->i64);
     uint64_t want[3] = {0, 0, (uint64_t)nr->i64 * 8};
     packed_sizes(t, (uint64_t)nr->i64, (uint64_t)nd->i64, &want[0], &want[1]);

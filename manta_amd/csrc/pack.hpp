@@ -90,6 +90,57 @@ inline void pack_q4_row(const float* x, int64_t d, uint8_t* dst, uint16_t* scale
     }
 }
 
+// ---- exact repacking of symmetric grids
+//
+// The reference's fake quantization stores v' = fl32(q * scale) with q an
+// integer in [-levels, levels] and scale = fl32(maxabs / levels)
+// (fakeQuantizeDataInPlace, runtime/embedding_trainer.go:3738-3763).  Values
+// on such a grid repack exactly: codes q with f32 scale `scale` reproduce
+// every value as the f32 product code*scale (-0 becomes code 0, whose
+// product +0 compares equal and adds identically in every score).
+
+// Codes of x[0..count) on the grid of step s, or false if some value is not
+// fl32(q*s) for an integer |q| <= levels.
+inline bool grid_codes(const float* x, int64_t count, float s, int levels, int8_t* codes) {
+    if (!(s >= 0.0f) || !std::isfinite(s)) return false;
+    for (int64_t i = 0; i < count; i++) {
+        const float v = x[i];
+        if (s == 0.0f) {
+            if (v != 0.0f) return false;
+            codes[i] = 0;
+            continue;
+        }
+        const float q = std::round(v / s);
+        if (!(std::fabs(q) <= (float)levels)) return false;
+        if ((float)q * s != v) return false;
+        codes[i] = (int8_t)q;
+    }
+    return true;
+}
+
+// The grid of x[0..count) as the reference would have built it: the step
+// fl32(maxabs / levels) of the grid's own maximum, or (when rounding moved
+// the maximum by an ulp) one of its neighbouring f32 values.  Returns the
+// step, or -1 if no candidate reproduces every value.
+inline float grid_scale(const float* x, int64_t count, int levels, int8_t* codes) {
+    float maxabs = 0.0f;
+    for (int64_t i = 0; i < count; i++) {
+        if (!std::isfinite(x[i])) return -1.0f;
+        maxabs = std::fmax(maxabs, std::fabs(x[i]));
+    }
+    if (maxabs == 0.0f) {
+        std::memset(codes, 0, (size_t)count);
+        return 0.0f;
+    }
+    const float s0 = maxabs / (float)levels;
+    const float cand[5] = {s0, std::nextafter(s0, 0.0f), std::nextafter(s0, 2.0f * s0),
+                           std::nextafter(std::nextafter(s0, 0.0f), 0.0f),
+                           std::nextafter(std::nextafter(s0, 2.0f * s0), 2.0f * s0)};
+    for (float s : cand)
+        if (s > 0.0f && grid_codes(x, count, s, levels, codes)) return s;
+    return -1.0f;
+}
+
 inline int q4_nibble(const uint8_t* row, int64_t c) {
     int v = (c & 1) ? (row[c >> 1] >> 4) : (row[c >> 1] & 0xF);
     return v >= 8 ? v - 16 : v;

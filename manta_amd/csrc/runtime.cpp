@@ -494,6 +494,41 @@ int manta_rocm_pack_q4_blocks(const float* x, int64_t n, int64_t d, uint8_t* pac
     return MANTA_ROCM_OK;
 }
 
+int manta_rocm_pack_grid(const float* x, int64_t n, int64_t d, int bits, int8_t* codes, float* scales, int* grid,
+                         char** err) {
+    if (n < 0 || d <= 0) return fail(err, MANTA_ROCM_ERROR, "pack_grid: bad shape [%lld,%lld]", (long long)n,
+                                     (long long)d);
+    if (bits != 8 && bits != 4) return fail(err, MANTA_ROCM_ERROR, "pack_grid: bits must be 8 or 4 (got %d)", bits);
+    if (!x || !codes || !scales || !grid) return fail(err, MANTA_ROCM_ERROR, "pack_grid: nil pointer");
+    const int levels = (1 << (bits - 1)) - 1;
+    // one grid for the whole tensor (the reference's own)
+    const float s = manta::grid_scale(x, n * d, levels, codes);
+    if (s >= 0.0f) {
+        for (int64_t r = 0; r < n; r++) scales[r] = s;
+        *grid = 2;
+        return MANTA_ROCM_OK;
+    }
+    // a grid per row (e.g. rows packed per row and dequantized)
+    bool rows_ok = true;
+    parallel_rows(n, [&](int64_t a, int64_t b) {
+        for (int64_t r = a; r < b && rows_ok; r++) {
+            const float sr = manta::grid_scale(x + r * d, d, levels, codes + r * d);
+            if (sr < 0.0f) rows_ok = false;
+            scales[r] = sr;
+        }
+    });
+    if (rows_ok) {
+        *grid = 1;
+        return MANTA_ROCM_OK;
+    }
+    // on no grid: re-quantized per row to int8 (lossy)
+    parallel_rows(n, [&](int64_t a, int64_t b) {
+        for (int64_t r = a; r < b; r++) scales[r] = manta::pack_q8_row(x + r * d, d, codes + r * d);
+    });
+    *grid = 0;
+    return MANTA_ROCM_OK;
+}
+
 // ------------------------------------------------------------- binding
 
 int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* scales, int64_t sets,
@@ -1429,7 +1464,10 @@ int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens, const int32_
         return fail(err, MANTA_ROCM_ERROR, "encoder: bad shape b=%lld t=%lld vocab=%lld d=%lld h=%lld",
                     (long long)b, (long long)t, (long long)vocab, (long long)d, (long long)h);
     const int64_t rows = b * t;
-    if (b > 65535 || rows > 0x7FFFFFFF || d > 0x7FFFFFFF || h > 0x7FFFFFFF || t > 0x7FFFFFFF)
+    // the GEMM grids: 64-row tiles of the b*t rows (and of each sequence's t
+    // rows for the attention products) in at most 65535 workgroup rows
+    if (b > 65535 || rows > 0x7FFFFFFF || d > 0x7FFFFFFF || h > 0x7FFFFFFF || t > 0x7FFFFFFF ||
+        (rows + 63) / 64 > 65535)
         return fail(err, MANTA_ROCM_UNSUPPORTED, "encoder: shape too large");
     // x, q, k, v, mixed [rows, d]; scores [b, t, t]; ffn [rows, h]; pooled [b, d]
     const size_t rd = (size_t)rows * (size_t)d;

@@ -320,8 +320,17 @@ class Runtime:
         """The one-layer encoder's embed_pooled_batch: f16 [b, d].  weights:
         six (int8 [k, n] codes, f32 [n] column scales) device pairs in the
         order attn_q, attn_k, attn_v, attn_o, ffn_up, projection."""
+        if len(tokens.shape) != 2 or np.dtype(tokens.dtype) != np.dtype(np.int32):
+            raise ValueError("encoder tokens must be int32 [b, t] (got %s %s)" % (tokens.dtype, tokens.shape))
+        if tuple(mask.shape) != tuple(tokens.shape) or np.dtype(mask.dtype) != np.dtype(np.int32):
+            raise ValueError("encoder mask must be int32 %s (got %s %s)" % (tokens.shape, mask.dtype, mask.shape))
         b, t = tokens.shape
+        if len(token_codes.shape) != 2 or np.dtype(token_codes.dtype) != np.dtype(np.int8):
+            raise ValueError("encoder token codes must be int8 [vocab, d]")
         vocab, d = token_codes.shape
+        if tuple(token_scales.shape) != (vocab,) or np.dtype(token_scales.dtype) != np.dtype(np.float32):
+            raise ValueError("encoder token scales must be f32 [%d] (got %s %s)" % (vocab, token_scales.dtype,
+                                                                                   token_scales.shape))
         if len(weights) != 6:
             raise ValueError("encoder weights: six (codes, scales) pairs")
         h = weights[4][0].shape[1]
@@ -329,6 +338,8 @@ class Runtime:
         for (codes, scales), want in zip(weights, shapes):
             if tuple(codes.shape) != want or tuple(scales.shape) != (want[1],):
                 raise ValueError("encoder weight shape %s / %s, want %s" % (codes.shape, scales.shape, want))
+            if np.dtype(codes.dtype) != np.dtype(np.int8) or np.dtype(scales.dtype) != np.dtype(np.float32):
+                raise ValueError("encoder weights must be int8 codes with f32 column scales")
         w = _lib.EncoderWeights()
         w.token_codes, w.token_scales = token_codes.addr, token_scales.addr
         for i, (codes, scales) in enumerate(weights):
@@ -358,3 +369,21 @@ def pack_q4_blocks(x: np.ndarray):
     call("manta_rocm_pack_q4_blocks", x.ctypes.data_as(C.c_void_p), C.c_int64(n), C.c_int64(d),
          packed.ctypes.data_as(C.c_void_p), scales.ctypes.data_as(C.c_void_p))
     return packed, scales
+
+
+GRID_NONE, GRID_ROWS, GRID_TENSOR = 0, 1, 2
+
+
+def pack_grid(x: np.ndarray, bits: int):
+    """Exact q8-row repack of the f32 values of a reference q8 / q4 tensor:
+    (codes int8 [n, d], scales f32 [n], grid) with grid 2 for one
+    per-tensor grid (fakeQuantizeDataInPlace), 1 for a grid per row, 0 when
+    the rows had to be re-quantized (lossy)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = x.shape
+    codes = np.empty((n, d), np.int8)
+    scales = np.empty((n,), np.float32)
+    grid = C.c_int(-1)
+    call("manta_rocm_pack_grid", x.ctypes.data_as(C.c_void_p), C.c_int64(n), C.c_int64(d), C.c_int(bits),
+         codes.ctypes.data_as(C.c_void_p), scales.ctypes.data_as(C.c_void_p), C.byref(grid))
+    return codes, scales, grid.value

@@ -5,6 +5,7 @@ import glob
 import os
 import re
 
+import numpy as np
 import pytest
 
 from manta_amd import _lib
@@ -74,3 +75,34 @@ def test_create_without_device_reports_unsupported():
         pytest.skip("a device is present")
     with pytest.raises(_lib.Unsupported, match="no ROCm device"):
         rocm.Runtime(0)
+
+
+def test_encoder_wrapper_validates_before_the_abi():
+    """encoder_pooled hands raw device pointers to the C ABI, which cannot
+    check them: the wrapper rejects mistyped or mis-shaped tokens, mask and
+    token scales first (stand-ins carry only shape and dtype; no device)."""
+    from types import SimpleNamespace as A
+
+    from manta_amd import rocm
+
+    def arr(shape, dtype):
+        return A(shape=shape, dtype=np.dtype(dtype), addr=0, ptr=None)
+
+    b, t, vocab, d, h = 2, 4, 10, 32, 64
+    good = dict(tokens=arr((b, t), np.int32), mask=arr((b, t), np.int32), token_codes=arr((vocab, d), np.int8),
+                token_scales=arr((vocab,), np.float32),
+                weights=[(arr(s, np.int8), arr((s[1],), np.float32))
+                         for s in [(d, d), (d, d), (d, d), (d, d), (d, h), (h, d)]])
+    bad_cases = [
+        ("tokens", arr((b, t), np.int64), "tokens must be int32"),
+        ("mask", arr((b, t - 1), np.int32), "mask must be int32"),
+        ("mask", arr((b, t), np.int8), "mask must be int32"),
+        ("token_scales", arr((vocab - 1,), np.float32), "token scales must be f32"),
+        ("token_codes", arr((vocab, d), np.uint8), "token codes must be int8"),
+    ]
+    for key, value, msg in bad_cases:
+        kw = dict(good)
+        kw[key] = value
+        with pytest.raises(ValueError, match=msg):
+            rocm.Runtime.encoder_pooled(None, kw["tokens"], kw["mask"], kw["token_codes"], kw["token_scales"],
+                                        kw["weights"])

@@ -49,7 +49,10 @@ def _want(tokens, mask, tcodes, tscales, packed):
 
 
 @pytest.mark.parametrize("b,t,vocab,d,h", [(6, 16, 50, 64, 128), (5, 24, 70, 96, 160), (3, 1, 9, 32, 64),
-                                           (8, 64, 300, 384, 1536)])
+                                           (8, 64, 300, 384, 1536),
+                                           # d, h and t not multiples of 16: the scalar staging path of the
+                                           # q8-weight and transposed-K GEMMs, with their bounds-checked K tails
+                                           (4, 24, 40, 40, 72)])
 def test_encoder_matches_oracle(rt, b, t, vocab, d, h):
     case = _case(b * 100 + t, b, t, vocab, d, h)
     got = _run(rt, *case)

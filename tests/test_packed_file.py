@@ -70,6 +70,11 @@ def test_manifest_read_as_authored_manifest(tmp_path):
     assert doc["values"]["has_ids"] == (mll.BOOL, False)
 
 
+def at_rows(body):
+    """Offset of the rows value (the i64 40) in a HEAD section body."""
+    return body.index((40).to_bytes(8, "little"))
+
+
 def test_errors(tmp_path):
     x = _rows(4, 40, 64)
     c, s = orc.pack_q8_rows(x)
@@ -89,6 +94,26 @@ def test_errors(tmp_path):
     bad[head[1] + at] = 41
     with mll.MllFile(bytes(bad), verify=False) as m:
         with pytest.raises(MantaRocmError, match="QCOD section is 2560 bytes, want 2624"):
+            m.packed()
+    # a HEAD string value naming a string id past the string table, and a
+    # row count whose section sizes would wrap 64 bits (opened without
+    # verification: a crafted file can carry matching digests)
+    entries, at = [], 30
+    for _ in range(body[28] | body[29] << 8):
+        kind = body[at + 4]
+        width = {1: 1, 2: 8, 3: 8, 4: 4}[kind]
+        entries.append((at + 5, kind, width))
+        at += 5 + width
+    s_at = [e for e in entries if e[1] == 4][0][0]
+    bad = bytearray(data)
+    bad[head[1] + s_at:head[1] + s_at + 4] = (100000).to_bytes(4, "little")
+    with mll.MllFile(bytes(bad), verify=False) as m:
+        with pytest.raises(MantaRocmError, match="names string 100000"):
+            m.packed()
+    bad = bytearray(data)
+    bad[head[1] + at_rows(body):head[1] + at_rows(body) + 8] = (2 ** 62 + 40).to_bytes(8, "little")
+    with mll.MllFile(bytes(bad), verify=False) as m:
+        with pytest.raises(MantaRocmError, match="bad shape"):
             m.packed()
     # a manifest of another kind
     with mll.MllFile(os.path.join(GOLD, "score_bundle.score.mll")) as m:
