@@ -231,6 +231,22 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* cands, int o
                           int32_t* out_ids_dev, float* out_scores_dev, int64_t* out_acc_dev,
                           char** err);
 
+/* manta_rocm_score_topk for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, semantics
+ * and results as manta_rocm_score_topk (the same kernels), but the call makes
+ * no device allocation and records no timing events: every scratch buffer
+ * comes from a fixed device array of 32 MiB per GPU (minus 256 KiB of
+ * tickets) that the library holds from the first runtime on that GPU until
+ * the process ends.  Only the streaming scan (one query per workgroup) runs,
+ * never the multi-query passes; a call that would need more scratch than the
+ * array holds (about nq * (n / 16384 + 1) * k * 8 bytes, twice that and
+ * nq * k * 16 more for reference scores) returns MANTA_ROCM_UNSUPPORTED.  The
+ * array keeps the last call's contents; calls that overlap on one GPU race. */
+int manta_rocm_score_topk_noalloc(MantaRocm* rt, const MantaRocmCandidates* cands, int op, int order,
+                                  const uint16_t* queries_dev, int64_t nq, int64_t k, int32_t* out_ids_dev,
+                                  float* out_scores_dev, int64_t* out_acc_dev, char** err);
+
 /* The retrieval presets' last steps after top-k (compiler/compiler.go:539-570):
  * gather(candidate_ids, top), gather(docs, top) and pack_candidates
  * (tensor_ops.go:66-82, the pack holding ids, scores and docs, tensor.go:27-31),

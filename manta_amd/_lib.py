@@ -110,6 +110,10 @@ SIGNATURES = {
         C.c_int,
         [_p, _p, C.c_int, C.c_int, _p, _i64, _i64, _p, _p, _p, _err],
     ),
+    "manta_rocm_score_topk_noalloc": (
+        C.c_int,
+        [_p, _p, C.c_int, C.c_int, _p, _i64, _i64, _p, _p, _p, _err],
+    ),
     "manta_rocm_topk": (C.c_int, [_p, _p, _i64, _i64, _i64, C.c_int, _p, _p, _err]),
     "manta_rocm_gather_rows_f16": (C.c_int, [_p, _p, _i64, _i64, _p, _i64, _p, _err]),
     "manta_rocm_pack_candidates": (C.c_int, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p, _err]),

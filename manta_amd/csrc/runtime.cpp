@@ -26,6 +26,7 @@
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "pack.hpp"
+#include "runtime_internal.hpp"
 
 using manta::QConst;
 using manta::ScanArgs;
@@ -186,6 +187,26 @@ int ensure_ref_workspace(MantaRocm* rt, size_t bytes, char** err) {
     return grow_buffer(rt, &rt->ws_ref, &rt->ws_ref_bytes, bytes, err);
 }
 
+// `bytes` of device memory: from the caller's scratch when there is one
+// (an error if it is exhausted), else the runtime workspace (grown on demand;
+// one buffer per call path, so callers take it once).
+int take_buffer(MantaRocm* rt, manta_rt::Scratch* sc, size_t bytes, void** out, char** err) {
+    if (!sc) {
+        int rc = ensure_workspace(rt, bytes + 256, err);
+        if (rc) return rc;
+        *out = rt->ws;
+        return MANTA_ROCM_OK;
+    }
+    const size_t at = align_up(sc->used, 256);
+    if (at + bytes > sc->bytes)
+        return fail(err, MANTA_ROCM_UNSUPPORTED,
+                    "score_topk_noalloc: the call needs more than the %zu bytes of scratch the allocation-free "
+                    "path holds", sc->bytes);
+    *out = sc->base + at;
+    sc->used = at + bytes;
+    return MANTA_ROCM_OK;
+}
+
 // Carve a workspace into aligned slices.
 struct Carver {
     char* base;
@@ -332,6 +353,8 @@ int manta_rocm_create(int device, MantaRocm** out, char** err) {
         return hip_fail(err, "hipStreamCreate", e);
     }
     rt->stream = rt->own_stream;
+    // the allocation-free entry point's scratch address on this device
+    manta_rt::noalloc_init(device);
     e = hipMalloc((void**)&rt->err_word, sizeof(unsigned long long));
     if (e == hipSuccess) e = hipMemset(rt->err_word, 0, sizeof(unsigned long long));
     if (e == hipSuccess) e = hipMalloc((void**)&rt->tickets, kTickets * sizeof(uint32_t));
@@ -797,14 +820,14 @@ StreamTopk stream_topk_shape(const MantaRocmCandidates* c, int64_t nq, int64_t k
     return st;
 }
 
-// Streaming top-k arguments; the parts' keys go to the runtime workspace.
-ScanArgs stream_topk_args(MantaRocm* rt, const MantaRocmCandidates* c, const uint16_t* q, const StreamTopk& st,
-                          int64_t k, int order, int32_t* out_ids, float* out_scores) {
+// Streaming top-k arguments; the parts' keys go to `partial` ([nq][parts][k]).
+ScanArgs stream_topk_args(const MantaRocmCandidates* c, const uint16_t* q, const StreamTopk& st, int64_t k,
+                          int order, int32_t* out_ids, float* out_scores, uint64_t* partial, uint32_t* tickets) {
     ScanArgs a = scan_args(c, q);
     a.mid_compact = st.mid_compact;
     a.rounds = st.rounds;
-    a.partial = (uint64_t*)rt->ws;
-    a.tickets = rt->tickets;
+    a.partial = partial;
+    a.tickets = tickets;
     a.out_ids = out_ids;
     a.out_topk_scores = out_scores;
     a.k = (int)k;
@@ -1157,11 +1180,13 @@ int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* c, int op, const 
 namespace {
 
 // Top-k of the quantized-query scan scores (device op dop): the
-// multi-query passes, or the streaming scan with its fused top-k.
+// multi-query passes, or the streaming scan with its fused top-k.  With a
+// caller's scratch (sc) the call allocates nothing: the streaming scan only,
+// its keys and tickets in sc.
 int scan_topk(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, const uint16_t* q, int64_t nq,
-              int64_t k, int32_t* out_ids, float* out_scores, int64_t* out_acc, char** err) {
-    if (q4_shadow_wanted(c, dop, nq, k)) ensure_q4_shadow(rt, c);
-    const MqPlan plan = mq_plan(c, dop, nq, k, true);
+              int64_t k, int32_t* out_ids, float* out_scores, int64_t* out_acc, manta_rt::Scratch* sc, char** err) {
+    if (!sc && q4_shadow_wanted(c, dop, nq, k)) ensure_q4_shadow(rt, c);
+    const MqPlan plan = sc ? MqPlan() : mq_plan(c, dop, nq, k, true);
     const int e16 = dop != manta::OP_DOT ? 1 : 0;
     if (plan.use) {
         int rc = run_mq(rt, c, dop, order, q, nq, k, plan, nullptr, out_ids, out_scores, err);
@@ -1173,9 +1198,10 @@ int scan_topk(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, c
         return MANTA_ROCM_OK;
     }
     StreamTopk st = stream_topk_shape(c, nq, k, choose_rounds((c->n + 255) / 256, nq));
-    int rc = ensure_workspace(rt, (size_t)nq * st.parts * k * 8 + 256, err);
+    uint64_t* partial = nullptr;
+    int rc = take_buffer(rt, sc, (size_t)nq * st.parts * k * 8, (void**)&partial, err);
     if (rc) return rc;
-    ScanArgs a = stream_topk_args(rt, c, q, st, k, order, out_ids, out_scores);
+    ScanArgs a = stream_topk_args(c, q, st, k, order, out_ids, out_scores, partial, sc ? sc->tickets : rt->tickets);
     // small k on the coalesced q8 kernel: sorted per-wave lists in registers
     // (LDS only for merging the waves' lists)
     if (c->format == MANTA_ROCM_Q8_ROWS && manta::q8_scan_coalesced(c->pitch) && k <= manta::kWaveListMaxK) {
@@ -1199,7 +1225,7 @@ int scan_topk(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, c
 // scales lie outside the range the scan's error bounds assume skip the scan
 // and are rescanned in full.
 int ref_topk(MantaRocm* rt, const MantaRocmCandidates* c, const ScoreOp& so, int order, const uint16_t* q,
-             int64_t nq, int64_t k, int32_t* out_ids, float* out_scores, char** err) {
+             int64_t nq, int64_t k, int32_t* out_ids, float* out_scores, manta_rt::Scratch* sc, char** err) {
     const int fmt = c->format == MANTA_ROCM_Q8_ROWS ? 8 : 4;
     const int smallest = order == MANTA_ROCM_SMALLEST;
     int* redo = nullptr;
@@ -1211,15 +1237,16 @@ int ref_topk(MantaRocm* rt, const MantaRocmCandidates* c, const ScoreOp& so, int
         const int64_t kp = std::min<int64_t>(std::min<int64_t>(c->n, kMaxDeviceK),
                                              k + std::max<int64_t>(8, k / 32));
         const size_t need = (size_t)nq * kp * 16 + (size_t)nq * 12 + 2048;
-        int rc = ensure_ref_workspace(rt, need, err);
+        char* base = nullptr;
+        int rc = sc ? take_buffer(rt, sc, need, (void**)&base, err) : ensure_ref_workspace(rt, need, err);
         if (rc) return rc;
-        Carver cv(rt->ws_ref);
+        Carver cv(sc ? (void*)base : rt->ws_ref);
         int32_t* cand_ids = cv.take<int32_t>((size_t)nq * kp);
         float* cand_scores = cv.take<float>((size_t)nq * kp);
         uint64_t* cand_keys = cv.take<uint64_t>((size_t)nq * kp);
         redo = cv.take<int>((size_t)nq);
         redo_tau = cv.take<uint64_t>((size_t)nq);
-        rc = scan_topk(rt, c, so.scan, order, q, nq, kp, cand_ids, cand_scores, nullptr, err);
+        rc = scan_topk(rt, c, so.scan, order, q, nq, kp, cand_ids, cand_scores, nullptr, sc, err);
         if (rc) return rc;
         manta::RefArgs ra{};
         ra.fmt = fmt;
@@ -1260,9 +1287,10 @@ int ref_topk(MantaRocm* rt, const MantaRocmCandidates* c, const ScoreOp& so, int
     StreamTopk st = stream_topk_shape(c, nq, k, rounds);
     const int64_t R = redo ? std::max<int64_t>(1, std::min<int64_t>(nq, 256 / std::max<int64_t>(1, st.parts)))
                            : std::min<int64_t>(nq, 65535);
-    int rc = ensure_workspace(rt, (size_t)nq * st.parts * k * 8 + 256, err);
+    uint64_t* partial = nullptr;
+    int rc = take_buffer(rt, sc, (size_t)nq * st.parts * k * 8, (void**)&partial, err);
     if (rc) return rc;
-    ScanArgs a = stream_topk_args(rt, c, q, st, k, order, out_ids, out_scores);
+    ScanArgs a = stream_topk_args(c, q, st, k, order, out_ids, out_scores, partial, sc ? sc->tickets : rt->tickets);
     LAUNCH_TRY(manta::launch_ref_scan(fmt, so.ref, a, (int)nq, c->sqd, redo, redo_tau,
                                       dim3((unsigned)st.parts, (unsigned)R), (size_t)a.lds_keys * 8, rt->stream),
                "ref_scan");
@@ -1276,6 +1304,14 @@ extern "C" {
 int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order,
                           const uint16_t* q, int64_t nq, int64_t k, int32_t* out_ids,
                           float* out_scores, int64_t* out_acc, char** err) {
+    return manta_rt::score_topk_impl(rt, c, op, order, q, nq, k, out_ids, out_scores, out_acc, nullptr, err);
+}
+
+}  // extern "C"
+
+int manta_rt::score_topk_impl(MantaRocm* rt, const MantaRocmCandidates* c, int op, int order, const uint16_t* q,
+                              int64_t nq, int64_t k, int32_t* out_ids, float* out_scores, int64_t* out_acc,
+                              Scratch* sc, char** err) {
     RT_CHECK(rt);
     int rc = check_score_args(c, op, q, nq, err);
     if (rc) return rc;
@@ -1291,9 +1327,22 @@ int manta_rocm_score_topk(MantaRocm* rt, const MantaRocmCandidates* c, int op, i
     const ScoreOp so = parse_op(c, op);
     if (out_acc && (c->format != MANTA_ROCM_Q8_ROWS || !so.quant))
         return fail(err, MANTA_ROCM_ERROR, "accumulator output needs q8 candidates and quantized-query scores");
-    if (so.quant) return scan_topk(rt, c, so.scan, order, q, nq, k, out_ids, out_scores, out_acc, err);
-    return ref_topk(rt, c, so, order, q, nq, k, out_ids, out_scores, err);
+    if (!sc) {
+        if (so.quant) return scan_topk(rt, c, so.scan, order, q, nq, k, out_ids, out_scores, out_acc, nullptr, err);
+        return ref_topk(rt, c, so, order, q, nq, k, out_ids, out_scores, nullptr, err);
+    }
+    // the allocation-free path: no per-launch timing events either
+    const bool timing = rt->timing;
+    rt->timing = false;
+    rc = so.quant ? scan_topk(rt, c, so.scan, order, q, nq, k, out_ids, out_scores, out_acc, sc, err)
+                  : ref_topk(rt, c, so, order, q, nq, k, out_ids, out_scores, sc, err);
+    rt->timing = timing;
+    return rc;
 }
+
+int manta_rt::runtime_device(const MantaRocm* rt) { return rt ? rt->device : -1; }
+
+extern "C" {
 
 int manta_rocm_pack_candidates(MantaRocm* rt, const MantaRocmCandidates* c, const int32_t* top, int64_t nq,
                                int64_t k, const int64_t* candidate_ids, int64_t* out_ids, void* out_rows,

@@ -241,6 +241,17 @@ class Runtime:
              C.c_int64(k), ids.ptr, _ptr(sc), _ptr(acc))
         return ids, sc, acc
 
+    def score_topk_noalloc(self, cands: Candidates, op: str, queries: DeviceArray, k: int, out,
+                           smallest: bool = False, quantized: bool = False):
+        """score_topk through the allocation-free entry point into the given
+        (ids, scores or None, accumulators or None) device arrays."""
+        nq = self._query_rows(cands, queries)
+        ids, sc, acc = out
+        call("manta_rocm_score_topk_noalloc", self.handle, cands.handle, C.c_int(self._op(op, quantized)),
+             C.c_int(_lib.SMALLEST if smallest else _lib.LARGEST), queries.ptr, C.c_int64(nq), C.c_int64(k),
+             ids.ptr, _ptr(sc), _ptr(acc))
+        return ids, sc, acc
+
     def pack_candidates(self, cands: Candidates, top: DeviceArray,
                         candidate_ids: Optional[DeviceArray] = None):
         """Candidate ids (int64, when given), packed rows and row scales of
