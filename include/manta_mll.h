@@ -7,7 +7,8 @@
  * github.com/odvcencio/mll v0.0.1 (go.mod:6), which the reference does not
  * vendor; its layout is restated here from the reference's call sites
  * (artifact/manta/mll.go:90-96, runtime/authored_manifest_mll.go:47-270) and
- * from the bytes of the reference's example containers (examples/*.mll), all
+ * from the bytes of the reference's example containers (the .mll files in
+ * examples/), all
  * of whose section digests this reader reproduces:
  *
  *   header   "MLL\0", u32 format word, u64 file size, u64 section count

@@ -318,6 +318,12 @@ int manta_rocm_matmul_f16(MantaRocm* rt, const uint16_t* lhs_dev, int64_t m, int
 int manta_rocm_mean_pool_masked(MantaRocm* rt, const float* x_dev, const int32_t* mask_dev,
                                 int64_t b, int64_t t, int64_t c, float* out_dev, char** err);
 
+/* meanPoolTensor: f32 [b,t,c] -> f32 [b,c], every position counted, the f32
+ * sum in position order divided by float32(t) (tensor_ops.go:1170-1208;
+ * b == 1 is the rank-2 form). */
+int manta_rocm_mean_pool(MantaRocm* rt, const float* x_dev, int64_t b, int64_t t, int64_t c, float* out_dev,
+                         char** err);
+
 /* normalizeRows: f32 [rows, cols] in place (tensor_ops.go:1114-1138, the
  * CUDA row-wise kernel at compiler/compiler.go:731-745). */
 int manta_rocm_normalize_rows(MantaRocm* rt, float* x_dev, int64_t rows, int64_t cols,

@@ -21,7 +21,8 @@ PROJ_F16, PROJ_Q8_COL = 0, 1
 
 OPS = {"dot": DOT, "cosine": COSINE, "l2_distance": L2_DISTANCE}
 
-# Every exported symbol of include/manta_rocm.h and include/manta_mll.h:
+# Every exported symbol of include/manta_rocm.h, include/manta_mll.h and
+# include/manta_module.h:
 # name -> (restype, argtypes).
 _p = C.c_void_p
 _i64 = C.c_int64
@@ -45,6 +46,24 @@ class EncoderWeights(C.Structure):
         ("token_scales", C.c_void_p),
         ("codes", C.c_void_p * 6),
         ("col_scales", C.c_void_p * 6),
+    ]
+
+
+class Value(C.Structure):
+    """MantaRocmValue (include/manta_module.h)."""
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("kind", C.c_int),
+        ("dtype", C.c_int),
+        ("storage", C.c_int),
+        ("rank", C.c_int),
+        ("shape", C.c_int64 * 4),
+        ("data", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("ids", C.c_void_p),
+        ("scores", C.c_void_p),
+        ("ids_dtype", C.c_int),
+        ("candidates", C.c_void_p),
     ]
 
 
@@ -120,6 +139,35 @@ SIGNATURES = {
     "manta_rocm_matmul_f16": (C.c_int, [_p, _p, _i64, _i64, _p, C.c_int, _p, _i64, _p, _err]),
     "manta_rocm_mean_pool_masked": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, _p, _err]),
     "manta_rocm_normalize_rows": (C.c_int, [_p, _p, _i64, _i64, _err]),
+    "manta_rocm_mean_pool": (C.c_int, [_p, _p, _i64, _i64, _i64, _p, _err]),
+    # include/manta_module.h
+    "manta_module_decode_json": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(_p), _err]),
+    "manta_module_decode_mll": (C.c_int, [_p, C.POINTER(_p), _err]),
+    "manta_module_free": (None, [_p]),
+    "manta_module_validate": (C.c_int, [_p, _err]),
+    "manta_module_name": (C.c_char_p, [_p]),
+    "manta_module_encode_json": (C.c_int, [_p, C.POINTER(_p), C.POINTER(C.c_size_t), _err]),
+    "manta_module_encode_mll": (C.c_int, [_p, C.POINTER(_p), C.POINTER(C.c_size_t), _err]),
+    "manta_module_free_buffer": (None, [_p]),
+    "manta_module_validate_score_entry": (
+        C.c_int, [_p, C.c_char_p, C.c_char_p, C.c_int, C.c_char_p, C.c_int, C.c_char_p, C.c_char_p, C.c_char_p,
+                  C.c_int, C.c_char_p, _err]),
+    "manta_module_validate_retrieval_entry": (
+        C.c_int, [_p, C.c_char_p, C.c_char_p, C.c_int, C.c_char_p, C.c_int, C.c_char_p, C.c_int, C.c_char_p,
+                  C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, _err]),
+    "manta_module_validate_embedding_entry": (
+        C.c_int, [_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.c_char_p, _err]),
+    "manta_module_validate_embedding_param": (C.c_int, [_p, C.c_char_p, _err]),
+    "manta_manifest_validate_module": (C.c_int, [_p, _p, _err]),
+    "manta_rocm_program_load": (C.c_int, [_p, _p, C.POINTER(_p), _err]),
+    "manta_rocm_program_destroy": (None, [_p]),
+    "manta_rocm_program_bind": (C.c_int, [_p, C.POINTER(Value), _err]),
+    "manta_rocm_program_supports": (C.c_int, [_p, C.c_char_p, _err]),
+    "manta_rocm_program_run": (
+        C.c_int, [_p, C.c_char_p, C.POINTER(Value), _i64, C.POINTER(Value), _i64, C.POINTER(_i64), _err]),
+    "manta_rocm_program_trace_count": (_i64, [_p]),
+    "manta_rocm_program_trace_step": (
+        C.c_int, [_p, _i64, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.POINTER(C.c_char_p)]),
     "manta_rocm_embed_pooled": (
         C.c_int,
         [_p, _p, _p, _i64, _i64, _p, _i64, _i64, _p, C.c_int, _p, _i64, _p, _err],

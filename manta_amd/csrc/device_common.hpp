@@ -69,6 +69,15 @@ __device__ __forceinline__ float fdiv_rn(float a, float b) { return __fdiv_rn(a,
 // -fhip-fp32-correctly-rounded-divide-sqrt is the correctly rounded sequence.
 __device__ __forceinline__ float fsqrt_rn(float a) { return __builtin_sqrtf(a); }
 
+// Records an out-of-range gather index.  The reference's gather loops stop
+// at the first bad index in position order (tensor_ops.go:751-979), so the
+// lowest position must win however the threads race: the word holds
+// ~(pos << 32 | index) and keeps the largest such value (0 = none; pos <
+// 2^31 keeps every recorded word non-zero).  gather_error_index decodes it.
+__device__ __forceinline__ void report_gather_error(unsigned long long* err, int64_t pos, int idx) {
+    if (err) atomicMax(err, ~(((unsigned long long)pos << 32) | (unsigned long long)(uint32_t)idx));
+}
+
 // ----------------------------------------------------------- query codes
 
 // E8 (q8 dot): qmax = max(1, maxabs), code = clamp(round((q*127)/qmax)).

@@ -316,4 +316,11 @@ hipError_t launch_topk_rows_partial(const float* scores, int64_t rows, int64_t c
 hipError_t launch_topk_merge(const uint64_t* partial, int64_t rows, int64_t per_row, int k, int cap,
                              int smallest, int32_t* ids, float* values, hipStream_t s);
 
+// artifact executor steps (kernels_exec.hip)
+hipError_t launch_gather_elems(const void* table, int elem_bytes, int64_t rows, int64_t cols, int64_t bstride,
+                               const int32_t* idx, int64_t B, int64_t K, void* out, unsigned long long* err,
+                               hipStream_t s);
+hipError_t launch_widen_f16(const uint16_t* in, float* out, int64_t n, hipStream_t s);
+hipError_t launch_mean_pool(const float* x, int64_t B, int64_t T, int64_t C, float* out, hipStream_t s);
+
 }  // namespace manta

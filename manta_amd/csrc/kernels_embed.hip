@@ -30,10 +30,6 @@ constexpr int EK = 64;       // K per LDS chunk
 constexpr int LDA = EK + 8;  // halfs per LDS row (pad against bank conflicts)
 constexpr int LDB = EK + 8;
 
-// Records the first out-of-range gather index (flag bit 32 | index).
-__device__ __forceinline__ void report_bad_index(unsigned long long* err, int idx) {
-    if (err) atomicCAS(err, 0ull, (1ull << 32) | (unsigned long long)(uint32_t)idx);
-}
 
 template <bool GATHER, bool Q8B, bool POOL>
 __global__ __launch_bounds__(256) void embed_gemm_kernel(EmbedArgs a) {
@@ -73,7 +69,7 @@ __global__ __launch_bounds__(256) void embed_gemm_kernel(EmbedArgs a) {
                 const int64_t pos = seq * a.T + t;
                 int idx = a.tokens[pos];
                 if (idx < 0 || idx >= a.vocab) {
-                    report_bad_index(a.err, idx);
+                    report_gather_error(a.err, pos, idx);
                 } else if (!a.mask || a.mask[pos] != 0) {
                     arow[h] = (const _Float16*)a.table + (int64_t)idx * a.K;
                     arow_live[h] = true;
@@ -85,7 +81,7 @@ __global__ __launch_bounds__(256) void embed_gemm_kernel(EmbedArgs a) {
                 if (GATHER) {
                     int idx = a.tokens[m];
                     if (idx < 0 || idx >= a.vocab) {
-                        report_bad_index(a.err, idx);
+                        report_gather_error(a.err, m, idx);
                     } else {
                         arow[h] = (const _Float16*)a.table + (int64_t)idx * a.K;
                         arow_live[h] = true;
@@ -288,7 +284,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void e
                 if (t < a.T) {
                     const int idx = a.tokens[seq * a.T + t];
                     if (idx >= 0 && idx < a.vocab) src = idx;
-                    else report_bad_index(a.err, idx);
+                    else report_gather_error(a.err, seq * a.T + t, idx);
                 }
             } else {
                 const int64_t m = m0 + r;
@@ -296,7 +292,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void e
                     if (GATHER) {
                         const int idx = a.tokens[m];
                         if (idx >= 0 && idx < a.vocab) src = idx;
-                        else report_bad_index(a.err, idx);
+                        else report_gather_error(a.err, m, idx);
                     } else {
                         src = m;
                     }
@@ -458,7 +454,7 @@ __global__ void gather_rows_f16_kernel(const uint16_t* __restrict__ table, int64
     const int64_t row = blockIdx.x;
     const int id = idx[row];
     const bool ok = id >= 0 && id < vocab;
-    if (!ok && threadIdx.x == 0) report_bad_index(err, id);
+    if (!ok && threadIdx.x == 0) report_gather_error(err, row, id);
     for (int64_t c = threadIdx.x; c < d; c += blockDim.x)
         out[row * d + c] = ok ? table[(int64_t)id * d + c] : (uint16_t)0;
 }
@@ -562,7 +558,7 @@ __global__ __launch_bounds__(256) void embed_gemm3_kernel(EmbedArgs a) {
             if (t < a.T) {
                 const int idx = a.tokens[seq * a.T + t];
                 if (idx >= 0 && idx < a.vocab) src = idx;
-                else report_bad_index(a.err, idx);
+                else report_gather_error(a.err, seq * a.T + t, idx);
             }
         } else {
             const int64_t m = m0 + r;
@@ -570,7 +566,7 @@ __global__ __launch_bounds__(256) void embed_gemm3_kernel(EmbedArgs a) {
                 if (GATHER) {
                     const int idx = a.tokens[m];
                     if (idx >= 0 && idx < a.vocab) src = idx;
-                    else report_bad_index(a.err, idx);
+                    else report_gather_error(a.err, m, idx);
                 } else {
                     src = m;
                 }
@@ -773,7 +769,7 @@ __global__ __launch_bounds__(256) void embed_gemm4_kernel(EmbedArgs a) {
         if (t < a.T) {
             const int idx = a.tokens[seq * a.T + t];
             if (idx >= 0 && idx < a.vocab) src = idx;
-            else report_bad_index(a.err, idx);
+            else report_gather_error(a.err, seq * a.T + t, idx);
         }
         const int c = (lane & 3) ^ ((r >> 2) & 3);
         asrc[u] = (const uint8_t*)a.table + src * K * 2 + c * 16;
@@ -949,7 +945,7 @@ __global__ __launch_bounds__(512) void embed_gemm5_kernel(EmbedArgs a, const uin
         const int idx = a.tokens[row0 + r];
         int64_t src = 0;
         if (idx >= 0 && idx < a.vocab) src = idx;
-        else report_bad_index(a.err, idx);
+        else report_gather_error(a.err, row0 + r, idx);
         const int c = (lane & 3) ^ ((r >> 2) & 3);
         asrc[u] = (const uint8_t*)a.table + src * K * 2 + c * 16;
     }

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void enc_gather_q8_kernel(const int32_t* __res
         const int c = (int)(i - r * d);
         const int id = tok[r];
         const bool ok = id >= 0 && (int64_t)id < vocab;
-        if (!ok && c == 0 && err) atomicCAS(err, 0ull, (1ull << 32) | (unsigned long long)(uint32_t)id);
+        if (!ok && c == 0) report_gather_error(err, r, id);
         x[i] = ok ? fmul_rn((float)codes[(int64_t)id * d + c], scales[id]) : 0.0f;
     }
 }

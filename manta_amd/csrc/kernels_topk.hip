@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void pack_candidates_kernel(PackArgs a) {
     const int64_t q = slot / a.k;
     const int idx = a.top[slot];
     const bool ok = idx >= 0 && (int64_t)idx < a.n;
-    if (!ok && lane == 0 && a.err) atomicCAS(a.err, 0ull, (1ull << 32) | (unsigned long long)(uint32_t)idx);
+    if (!ok && lane == 0) report_gather_error(a.err, slot, idx);
     const int64_t row = (a.sets == 1 ? 0 : q * a.n) + (ok ? idx : 0);
     if (a.ids_out && lane == 0) a.ids_out[slot] = (a.ids && ok) ? a.ids[row] : 0;
     uint8_t* dst = a.rows_out + slot * a.row_bytes;

@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "manta_rocm.h"
+#include "mll_internal.hpp"
 
 namespace {
 
@@ -242,12 +243,8 @@ void parse_head(MantaMll* m, const uint8_t* p, uint64_t n) {
 const char kPackedKind[] = "packed_candidates";
 const char kPackedVersion[] = "manta/packed-candidates/v0";
 
-void put32(std::vector<uint8_t>& b, uint32_t v) {
-    for (int i = 0; i < 4; i++) b.push_back((uint8_t)(v >> (8 * i)));
-}
-void put64(std::vector<uint8_t>& b, uint64_t v) {
-    for (int i = 0; i < 8; i++) b.push_back((uint8_t)(v >> (8 * i)));
-}
+using manta_mll::put32;
+using manta_mll::put64;
 
 // Expected byte sizes of the code and scale sections of `rows` rows of `dim`
 // values: q8 = int8 codes + one f32 scale per row, q4 = two values per byte
@@ -270,6 +267,96 @@ const MantaMll::Entry* head_value(const MantaMll* m, const char* key) {
 }
 
 }  // namespace
+
+// ------------------------------------------------------ container building
+
+namespace manta_mll {
+
+void put32(std::vector<uint8_t>& b, uint32_t v) {
+    for (int i = 0; i < 4; i++) b.push_back((uint8_t)(v >> (8 * i)));
+}
+void put64(std::vector<uint8_t>& b, uint64_t v) {
+    for (int i = 0; i < 8; i++) b.push_back((uint8_t)(v >> (8 * i)));
+}
+
+std::vector<uint8_t> build_table(std::vector<SectionRef>* secs, uint64_t* total) {
+    uint64_t at = 24 + 64 * (uint64_t)secs->size();
+    for (auto& s : *secs) {
+        if (s.flags & 0x10u) at = (at + 4095) & ~(uint64_t)4095;
+        s.off = at;
+        at += s.n;
+    }
+    *total = at;
+    std::vector<uint8_t> top;
+    top.insert(top.end(), {'M', 'L', 'L', 0});
+    put32(top, 0x00010100u);
+    put64(top, at);
+    put64(top, secs->size());
+    for (const auto& s : *secs) {
+        top.insert(top.end(), s.tag, s.tag + 4);
+        put64(top, s.off);
+        put64(top, s.n);
+        uint8_t d[32];
+        blake3(s.p, (size_t)s.n, d);
+        top.insert(top.end(), d, d + 32);
+        put32(top, s.flags);
+        put64(top, 0);
+    }
+    return top;
+}
+
+std::vector<uint8_t> build_container(std::vector<SectionRef>* secs) {
+    uint64_t total = 0;
+    std::vector<uint8_t> out = build_table(secs, &total);
+    out.resize((size_t)total, 0);
+    for (const auto& s : *secs)
+        if (s.n) memcpy(out.data() + s.off, s.p, (size_t)s.n);
+    return out;
+}
+
+void build_head(const std::string& name, const std::string& description, const std::vector<HeadEntry>& entries,
+                std::vector<uint8_t>* head, std::vector<uint8_t>* strg) {
+    std::vector<std::string> strs(1);
+    auto intern = [&](const std::string& x) -> uint32_t {
+        for (size_t i = 0; i < strs.size(); i++)
+            if (strs[i] == x) return (uint32_t)i;
+        strs.push_back(x);
+        return (uint32_t)(strs.size() - 1);
+    };
+    head->clear();
+    put32(*head, intern(name));
+    put32(*head, intern(description));
+    head->resize(head->size() + 20, 0);
+    head->push_back((uint8_t)(entries.size() & 0xFF));
+    head->push_back((uint8_t)(entries.size() >> 8));
+    for (const auto& e : entries) {
+        put32(*head, intern(e.key));
+        head->push_back((uint8_t)e.kind);
+        if (e.kind == MANTA_MLL_BOOL) head->push_back(e.i64 ? 1 : 0);
+        if (e.kind == MANTA_MLL_I64) put64(*head, (uint64_t)e.i64);
+        if (e.kind == MANTA_MLL_F64) {
+            uint64_t bits;
+            memcpy(&bits, &e.f64, 8);
+            put64(*head, bits);
+        }
+        if (e.kind == MANTA_MLL_STRING) put32(*head, intern(e.str));
+    }
+    strg->clear();
+    put64(*strg, strs.size());
+    for (size_t i = 1; i < strs.size(); i++) {
+        put32(*strg, (uint32_t)strs[i].size());
+        strg->insert(strg->end(), strs[i].begin(), strs[i].end());
+    }
+}
+
+const uint8_t* section_body(const MantaMll* m, const char* tag, uint64_t* size) {
+    const MantaMll::Section* s = find_section(m, tag);
+    if (!s) return nullptr;
+    *size = s->size;
+    return m->bytes.data() + s->offset;
+}
+
+}  // namespace manta_mll
 
 extern "C" {
 
@@ -427,41 +514,14 @@ int manta_mll_write_packed(const char* path, const char* name, int dtype, uint64
     head.push_back(MANTA_MLL_BOOL);
     head.push_back(ids ? 1 : 0);
 
-    struct Out {
-        const char* tag;
-        const uint8_t* p;
-        uint64_t n;
-        uint32_t flags;
-        uint64_t off;
-    };
     // flags: bit 0 required, bit 4 page aligned, schema version in bits 16+
-    std::vector<Out> secs = {{"HEAD", head.data(), head.size(), 0x10001u, 0},
-                             {"STRG", strg.data(), strg.size(), 0x10001u, 0},
-                             {"QCOD", (const uint8_t*)codes, ncode, 0x10011u, 0},
-                             {"QSCL", (const uint8_t*)scales, nscale, 0x10011u, 0}};
+    std::vector<manta_mll::SectionRef> secs = {{"HEAD", head.data(), head.size(), 0x10001u, 0},
+                                               {"STRG", strg.data(), strg.size(), 0x10001u, 0},
+                                               {"QCOD", (const uint8_t*)codes, ncode, 0x10011u, 0},
+                                               {"QSCL", (const uint8_t*)scales, nscale, 0x10011u, 0}};
     if (ids) secs.push_back({"QIDS", (const uint8_t*)ids, rows * 8, 0x10011u, 0});
-    uint64_t at = 24 + 64 * (uint64_t)secs.size();
-    for (auto& s : secs) {
-        if (s.flags & 0x10u) at = (at + 4095) & ~(uint64_t)4095;
-        s.off = at;
-        at += s.n;
-    }
-    const uint64_t total = at;
-    std::vector<uint8_t> top;
-    top.insert(top.end(), {'M', 'L', 'L', 0});
-    put32(top, 0x00010100u);
-    put64(top, total);
-    put64(top, secs.size());
-    for (const auto& s : secs) {
-        top.insert(top.end(), s.tag, s.tag + 4);
-        put64(top, s.off);
-        put64(top, s.n);
-        uint8_t d[32];
-        blake3(s.p, (size_t)s.n, d);
-        top.insert(top.end(), d, d + 32);
-        put32(top, s.flags);
-        put64(top, 0);
-    }
+    uint64_t total = 0;
+    const std::vector<uint8_t> top = manta_mll::build_table(&secs, &total);
     FILE* f = fopen(path, "wb");
     if (!f) return mll_fail(err, "packed candidates: cannot create %s", path);
     bool ok = fwrite(top.data(), 1, top.size(), f) == top.size();

@@ -252,9 +252,10 @@ int set_device(MantaRocm* rt, char** err) {
     return MANTA_ROCM_OK;
 }
 
-// Device gathers record their first out-of-range index instead of faulting;
-// the next synchronizing call reports it with gatherTensor's wording
-// (tensor_ops.go:804-806) and clears it.
+// Device gathers record their out-of-range index of lowest position
+// (report_gather_error) instead of faulting; the next synchronizing call
+// reports it with gatherTensor's wording (tensor_ops.go:804-806) and clears
+// it.
 int check_gather_error(MantaRocm* rt, char** err) {
     if (!rt->gather_pending) return MANTA_ROCM_OK;
     rt->gather_pending = false;
@@ -267,7 +268,7 @@ int check_gather_error(MantaRocm* rt, char** err) {
     HIP_TRY(hipMemcpyAsync(rt->err_word, &zero, sizeof(zero), hipMemcpyHostToDevice, rt->stream),
             "hipMemcpy(error word)");
     HIP_TRY(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
-    return fail(err, MANTA_ROCM_ERROR, "gather index %d out of range", (int)(uint32_t)(w & 0xFFFFFFFFull));
+    return fail(err, MANTA_ROCM_ERROR, "gather index %d out of range", manta_rt::gather_error_index(w));
 }
 
 #define RT_CHECK(rt)                                                          \
@@ -1342,11 +1343,11 @@ int manta_rt::score_topk_impl(MantaRocm* rt, const MantaRocmCandidates* c, int o
 
 int manta_rt::runtime_device(const MantaRocm* rt) { return rt ? rt->device : -1; }
 
-extern "C" {
+void* manta_rt::runtime_stream(const MantaRocm* rt) { return rt ? (void*)rt->stream : nullptr; }
 
-int manta_rocm_pack_candidates(MantaRocm* rt, const MantaRocmCandidates* c, const int32_t* top, int64_t nq,
-                               int64_t k, const int64_t* candidate_ids, int64_t* out_ids, void* out_rows,
-                               void* out_scales, char** err) {
+int manta_rt::pack_candidates_into(MantaRocm* rt, const MantaRocmCandidates* c, const int32_t* top, int64_t nq,
+                                   int64_t k, const int64_t* candidate_ids, int64_t* out_ids, void* out_rows,
+                                   void* out_scales, unsigned long long* err_word, char** err) {
     RT_CHECK(rt);
     if (!c || !top || !out_rows || !out_scales) return fail(err, MANTA_ROCM_ERROR, "nil pack_candidates input");
     if (nq <= 0 || k <= 0) return fail(err, MANTA_ROCM_ERROR, "pack_candidates expects nq > 0 and k > 0");
@@ -1369,10 +1370,21 @@ int manta_rocm_pack_candidates(MantaRocm* rt, const MantaRocmCandidates* c, cons
     a.ids_out = out_ids;
     a.rows_out = (uint8_t*)out_rows;
     a.scales_out = (uint8_t*)out_scales;
-    a.err = rt->err_word;
+    a.err = err_word;
     LAUNCH_TRY(manta::launch_pack_candidates(a, rt->stream), "pack_candidates");
-    rt->gather_pending = true;
     return MANTA_ROCM_OK;
+}
+
+extern "C" {
+
+int manta_rocm_pack_candidates(MantaRocm* rt, const MantaRocmCandidates* c, const int32_t* top, int64_t nq,
+                               int64_t k, const int64_t* candidate_ids, int64_t* out_ids, void* out_rows,
+                               void* out_scales, char** err) {
+    RT_CHECK(rt);
+    const int rc = manta_rt::pack_candidates_into(rt, c, top, nq, k, candidate_ids, out_ids, out_rows, out_scales,
+                                                  rt->err_word, err);
+    if (rc == MANTA_ROCM_OK) rt->gather_pending = true;
+    return rc;
 }
 
 int manta_rocm_topk(MantaRocm* rt, const float* scores, int64_t rows, int64_t cols, int64_t k,
@@ -1490,6 +1502,15 @@ int manta_rocm_mean_pool_masked(MantaRocm* rt, const float* x, const int32_t* ma
     if (!out) return fail(err, MANTA_ROCM_ERROR, "nil mean_pool output");
     if (b <= 0 || t <= 0 || c <= 0) return fail(err, MANTA_ROCM_ERROR, "mean_pool expects rank-2 or rank-3 tensor input");
     LAUNCH_TRY(manta::launch_mean_pool_masked(x, mask, b, t, c, out, rt->stream), "mean_pool");
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_mean_pool(MantaRocm* rt, const float* x, int64_t b, int64_t t, int64_t c, float* out, char** err) {
+    RT_CHECK(rt);
+    if (!x) return fail(err, MANTA_ROCM_ERROR, "nil mean_pool input");
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil mean_pool output");
+    if (b <= 0 || t <= 0 || c <= 0) return fail(err, MANTA_ROCM_ERROR, "mean_pool expects rank-2 or rank-3 tensor input");
+    LAUNCH_TRY(manta::launch_mean_pool(x, b, t, c, out, rt->stream), "mean_pool");
     return MANTA_ROCM_OK;
 }
 

@@ -303,6 +303,13 @@ class Runtime:
              C.c_int64(t), C.c_int64(c), out.ptr)
         return out
 
+    def mean_pool(self, x: DeviceArray) -> DeviceArray:
+        """meanPoolTensor: f32 [b, t, c] -> [b, c] (sum / float32(t))."""
+        b, t, c = x.shape
+        out = self.empty((b, c), np.float32)
+        call("manta_rocm_mean_pool", self.handle, x.ptr, C.c_int64(b), C.c_int64(t), C.c_int64(c), out.ptr)
+        return out
+
     def normalize_rows(self, x: DeviceArray) -> DeviceArray:
         rows, cols = x.shape[0] if len(x.shape) == 2 else x.shape[0] * x.shape[1], x.shape[-1]
         call("manta_rocm_normalize_rows", self.handle, x.ptr, C.c_int64(rows), C.c_int64(cols))

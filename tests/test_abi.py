@@ -18,7 +18,7 @@ def declared_symbols():
     syms = set()
     for h in HEADERS:
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        syms |= set(re.findall(r"\b(manta_(?:rocm|mll)_\w+)\s*\(", text))
+        syms |= set(re.findall(r"\b(manta_(?:rocm|mll|module|manifest)_\w+)\s*\(", text))
     return sorted(syms)
 
 
