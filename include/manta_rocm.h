@@ -85,6 +85,12 @@ enum {
     MANTA_ROCM_Q4_BLOCKS = 4,
 };
 
+/* Dense retrieval vectors (manta_rocm_dense_*). */
+enum {
+    MANTA_ROCM_DENSE_F32 = 32,
+    MANTA_ROCM_DENSE_F16 = 16, /* IEEE binary16 bits, widened exactly */
+};
+
 /* Projection kinds for the embed pipeline. */
 enum {
     MANTA_ROCM_PROJ_F16 = 0,    /* f16 [d, e] */
@@ -295,6 +301,26 @@ int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens_dev, const in
  * form).  Replaces topKTensor (tensor_ops.go:1523-1592). */
 int manta_rocm_topk(MantaRocm* rt, const float* scores_dev, int64_t rows, int64_t cols, int64_t k,
                     int order, int32_t* out_ids_dev, float* out_values_dev, char** err);
+
+/* ---- dense retrieval vectors ------------------------------------------- */
+
+/* dotRetrievalVectors (runtime/retrieval_eval.go:651-661) on device: f32
+ * queries [nq, qd] against rows [n, d] of f32 or f16 values (dtype
+ * MANTA_ROCM_DENSE_F32 / _F16), the sum over min(qd, d) columns in f32,
+ * product and sum rounded separately, in index order -- the reference's
+ * scores bit for bit.  out_scores_dev f32 [nq, n]. */
+int manta_rocm_dense_scores(MantaRocm* rt, const void* rows_dev, int dtype, int64_t n, int64_t d,
+                            const float* queries_dev, int64_t nq, int64_t qd, float* out_scores_dev, char** err);
+
+/* topRetrievalScores (retrieval_eval.go:586-623): the k best rows of each
+ * query by (score desc, row asc) -- retrievalScoreBetter's (score desc, doc
+ * ID asc) when the rows are stored in ascending doc-ID order, which is how a
+ * host binds them (the Python wrapper sorts).  out_rows_dev int32 [nq, k],
+ * out_scores_dev f32 [nq, k] (may be NULL).  k as manta_rocm_topk (the
+ * reference's k <= 0 or k > n, "every doc", is the caller's k = n). */
+int manta_rocm_dense_topk(MantaRocm* rt, const void* rows_dev, int dtype, int64_t n, int64_t d,
+                          const float* queries_dev, int64_t nq, int64_t qd, int64_t k, int32_t* out_rows_dev,
+                          float* out_scores_dev, char** err);
 
 /* ---- embed pipeline ---------------------------------------------------- */
 

@@ -18,6 +18,7 @@ QUANTIZED_QUERY = 0x100
 LARGEST, SMALLEST = 0, 1
 Q8_ROWS, Q4_BLOCKS = 8, 4
 PROJ_F16, PROJ_Q8_COL = 0, 1
+DENSE_F32, DENSE_F16 = 32, 16
 
 OPS = {"dot": DOT, "cosine": COSINE, "l2_distance": L2_DISTANCE}
 
@@ -140,6 +141,8 @@ SIGNATURES = {
     "manta_rocm_mean_pool_masked": (C.c_int, [_p, _p, _p, _i64, _i64, _i64, _p, _err]),
     "manta_rocm_normalize_rows": (C.c_int, [_p, _p, _i64, _i64, _err]),
     "manta_rocm_mean_pool": (C.c_int, [_p, _p, _i64, _i64, _i64, _p, _err]),
+    "manta_rocm_dense_scores": (C.c_int, [_p, _p, C.c_int, _i64, _i64, _p, _i64, _i64, _p, _err]),
+    "manta_rocm_dense_topk": (C.c_int, [_p, _p, C.c_int, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _err]),
     # include/manta_module.h
     "manta_module_decode_json": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(_p), _err]),
     "manta_module_decode_mll": (C.c_int, [_p, C.POINTER(_p), _err]),

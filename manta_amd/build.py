@@ -19,7 +19,7 @@ LIB = os.path.join(HERE, "libmanta_rocm.so")
 SYNTH = os.path.join(HERE, "libmanta_synth.so")
 
 HIP_SOURCES = ["kernels_score.hip", "kernels_ref.hip", "kernels_topk.hip", "kernels_mq.hip", "kernels_mq4.hip", "kernels_mq8.hip",
-               "kernels_embed.hip", "kernels_encoder.hip", "kernels_exec.hip", "noalloc.hip", "runtime.cpp", "mll.cpp",
+               "kernels_embed.hip", "kernels_encoder.hip", "kernels_exec.hip", "kernels_dense.hip", "noalloc.hip", "runtime.cpp", "mll.cpp",
                "module.cpp", "program.cpp"]
 
 HIPCC_FLAGS = [

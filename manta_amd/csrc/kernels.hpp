@@ -316,6 +316,10 @@ hipError_t launch_topk_rows_partial(const float* scores, int64_t rows, int64_t c
 hipError_t launch_topk_merge(const uint64_t* partial, int64_t rows, int64_t per_row, int k, int cap,
                              int smallest, int32_t* ids, float* values, hipStream_t s);
 
+// dotRetrievalVectors score matrix (kernels_dense.hip)
+hipError_t launch_dense_dot(const void* rows, int f16, int64_t n, int64_t pitch, int len, const float* queries,
+                            int64_t qpitch, int nq, float* out, hipStream_t s);
+
 // artifact executor steps (kernels_exec.hip)
 hipError_t launch_gather_elems(const void* table, int elem_bytes, int64_t rows, int64_t cols, int64_t bstride,
                                const int32_t* idx, int64_t B, int64_t K, void* out, unsigned long long* err,

@@ -1426,6 +1426,80 @@ int manta_rocm_topk(MantaRocm* rt, const float* scores, int64_t rows, int64_t co
     return MANTA_ROCM_OK;
 }
 
+// ------------------------------------------------------ dense retrieval
+
+namespace {
+
+int check_dense(const void* rows, int dtype, int64_t n, int64_t d, const float* q, int64_t nq, int64_t qd,
+                char** err) {
+    if (!rows || !q) return fail(err, MANTA_ROCM_ERROR, "nil dense retrieval input");
+    if (dtype != MANTA_ROCM_DENSE_F32 && dtype != MANTA_ROCM_DENSE_F16)
+        return fail(err, MANTA_ROCM_ERROR, "unknown dense vector dtype %d", dtype);
+    if (n <= 0 || d < 0 || nq <= 0 || qd < 0)
+        return fail(err, MANTA_ROCM_ERROR, "dense retrieval: bad shape [%lld,%lld] x [%lld,%lld]", (long long)nq,
+                    (long long)qd, (long long)n, (long long)d);
+    if (std::min(d, qd) > 0x7FFFFFFF || n > ((int64_t)1 << 31) - 1)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "dense retrieval: shape beyond the device path");
+    return MANTA_ROCM_OK;
+}
+
+// Queries per score-matrix launch: the matrix stays within 512 MiB (and the
+// grid's y extent within its limit).
+int64_t dense_chunk(int64_t n, int64_t nq) {
+    const int64_t by_bytes = std::max<int64_t>(1, ((int64_t)512 << 20) / (n * 4));
+    return std::min<int64_t>(std::min<int64_t>(nq, by_bytes), (int64_t)65535 * 8);
+}
+
+}  // namespace
+
+int manta_rocm_dense_scores(MantaRocm* rt, const void* rows, int dtype, int64_t n, int64_t d, const float* q,
+                            int64_t nq, int64_t qd, float* out, char** err) {
+    RT_CHECK(rt);
+    int rc = check_dense(rows, dtype, n, d, q, nq, qd, err);
+    if (rc) return rc;
+    if (!out) return fail(err, MANTA_ROCM_ERROR, "nil dense retrieval output");
+    const int len = (int)std::min(d, qd);
+    const int64_t chunk = std::min<int64_t>(nq, (int64_t)65535 * 8);
+    for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
+        const int nc = (int)std::min(chunk, nq - q0);
+        LAUNCH_TRY(manta::launch_dense_dot(rows, dtype == MANTA_ROCM_DENSE_F16, n, d, len, q + q0 * qd, qd, nc,
+                                           out + q0 * n, rt->stream),
+                   "dense_dot");
+    }
+    return MANTA_ROCM_OK;
+}
+
+int manta_rocm_dense_topk(MantaRocm* rt, const void* rows, int dtype, int64_t n, int64_t d, const float* q,
+                          int64_t nq, int64_t qd, int64_t k, int32_t* out_ids, float* out_scores, char** err) {
+    RT_CHECK(rt);
+    int rc = check_dense(rows, dtype, n, d, q, nq, qd, err);
+    if (rc) return rc;
+    if (!out_ids) return fail(err, MANTA_ROCM_ERROR, "nil topk output");
+    if (k <= 0 || k > n) {
+        if (nq == 1)
+            return fail(err, MANTA_ROCM_ERROR, "topk limit %lld out of range for %lld scores", (long long)k,
+                        (long long)n);
+        return fail(err, MANTA_ROCM_ERROR, "topk limit %lld out of range for row width %lld", (long long)k,
+                    (long long)n);
+    }
+    if (k > kMaxDeviceK)
+        return fail(err, MANTA_ROCM_UNSUPPORTED, "topk limit %lld exceeds the device maximum %lld", (long long)k,
+                    (long long)kMaxDeviceK);
+    const int64_t chunk = std::min<int64_t>(dense_chunk(n, nq), 65535);
+    rc = ensure_ref_workspace(rt, (size_t)(chunk * n) * 4 + 256, err);
+    if (rc) return rc;
+    float* scores = (float*)rt->ws_ref;
+    for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
+        const int64_t nc = std::min(chunk, nq - q0);
+        rc = manta_rocm_dense_scores(rt, rows, dtype, n, d, q + q0 * qd, nc, qd, scores, err);
+        if (rc) return rc;
+        rc = manta_rocm_topk(rt, scores, nc, n, k, MANTA_ROCM_LARGEST, out_ids + q0 * k,
+                             out_scores ? out_scores + q0 * k : nullptr, err);
+        if (rc) return rc;
+    }
+    return MANTA_ROCM_OK;
+}
+
 // ---------------------------------------------------------------- embed
 
 namespace {

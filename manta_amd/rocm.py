@@ -303,6 +303,38 @@ class Runtime:
              C.c_int64(t), C.c_int64(c), out.ptr)
         return out
 
+    # ------------------------------------------------------ dense vectors
+    @staticmethod
+    def _dense_kind(rows: DeviceArray) -> int:
+        if rows.dtype == np.float32:
+            return _lib.DENSE_F32
+        if rows.dtype == np.uint16:
+            return _lib.DENSE_F16
+        raise ValueError("dense rows must be f32 or f16 bits (uint16), not %s" % rows.dtype)
+
+    def dense_scores(self, rows: DeviceArray, queries: DeviceArray) -> DeviceArray:
+        """dotRetrievalVectors of f32 queries [nq, qd] against rows [n, d]."""
+        if queries.dtype != np.float32:
+            raise ValueError("queries must be f32")
+        n, d = rows.shape
+        nq, qd = queries.shape if len(queries.shape) == 2 else (1, queries.shape[0])
+        out = self.empty((nq, n), np.float32)
+        call("manta_rocm_dense_scores", self.handle, rows.ptr, self._dense_kind(rows), C.c_int64(n), C.c_int64(d),
+             queries.ptr, C.c_int64(nq), C.c_int64(qd), out.ptr)
+        return out
+
+    def dense_topk(self, rows: DeviceArray, queries: DeviceArray, k: int):
+        """The k best rows per query, (score desc, row asc): (ids, scores)."""
+        if queries.dtype != np.float32:
+            raise ValueError("queries must be f32")
+        n, d = rows.shape
+        nq, qd = queries.shape if len(queries.shape) == 2 else (1, queries.shape[0])
+        ids = self.empty((nq, max(k, 1)), np.int32)
+        scores = self.empty((nq, max(k, 1)), np.float32)
+        call("manta_rocm_dense_topk", self.handle, rows.ptr, self._dense_kind(rows), C.c_int64(n), C.c_int64(d),
+             queries.ptr, C.c_int64(nq), C.c_int64(qd), C.c_int64(k), ids.ptr, scores.ptr)
+        return ids, scores
+
     def mean_pool(self, x: DeviceArray) -> DeviceArray:
         """meanPoolTensor: f32 [b, t, c] -> [b, c] (sum / float32(t))."""
         b, t, c = x.shape

@@ -756,3 +756,84 @@ done:
     free(hid); free(q); free(k); free(v); free(kt); free(s); free(mixed); free(att); free(f);
     return rc;
 }
+
+/* ---- topRetrievalScores (runtime/retrieval_eval.go:586-661) ------------ */
+
+typedef struct {
+    float score;
+    const char* id;
+    int64_t pos;
+} retrieval_doc;
+
+/* retrievalScoreBetter, retrieval_eval.go:615-623. */
+static int retrieval_better(const retrieval_doc* a, const retrieval_doc* b) {
+    if (a->score > b->score) return 1;
+    if (a->score < b->score) return 0;
+    return strcmp(a->id, b->id) < 0;
+}
+
+/* container/heap over retrievalScoreHeap, whose Less(i, j) is
+ * better(h[j], h[i]): the root is the worst kept doc. */
+static int heap_less(const retrieval_doc* h, int64_t i, int64_t j) { return retrieval_better(&h[j], &h[i]); }
+
+static void heap_up(retrieval_doc* h, int64_t j) {
+    while (j > 0) {
+        int64_t i = (j - 1) / 2;
+        if (i == j || !heap_less(h, j, i)) break;
+        retrieval_doc t = h[i];
+        h[i] = h[j];
+        h[j] = t;
+        j = i;
+    }
+}
+
+static void heap_down(retrieval_doc* h, int64_t i0, int64_t n) {
+    int64_t i = i0;
+    for (;;) {
+        int64_t j1 = 2 * i + 1;
+        if (j1 >= n || j1 < 0) break;
+        int64_t j = j1;
+        if (j1 + 1 < n && heap_less(h, j1 + 1, j1)) j = j1 + 1;
+        if (!heap_less(h, j, i)) break;
+        retrieval_doc t = h[i];
+        h[i] = h[j];
+        h[j] = t;
+        i = j;
+    }
+}
+
+static int retrieval_cmp(const void* pa, const void* pb) {
+    const retrieval_doc* a = (const retrieval_doc*)pa;
+    const retrieval_doc* b = (const retrieval_doc*)pb;
+    if (retrieval_better(a, b)) return -1;
+    if (retrieval_better(b, a)) return 1;
+    return 0;
+}
+
+int64_t orc_top_retrieval_scores(const float* query, int64_t qd, const float* docs, int64_t n, int64_t d,
+                                 const char* const* ids, int64_t top_k, int64_t* out_pos, float* out_scores) {
+    if (top_k <= 0 || top_k > n) top_k = n;
+    retrieval_doc* h = (retrieval_doc*)malloc((size_t)(top_k > 0 ? top_k : 1) * sizeof(retrieval_doc));
+    const int64_t len = qd < d ? qd : d;
+    int64_t cnt = 0;
+    for (int64_t r = 0; r < n; r++) {
+        retrieval_doc s = {ref_dot_row(query, docs + r * d, len), ids[r], r};
+        if (cnt < top_k) {
+            h[cnt] = s; /* heap.Push */
+            heap_up(h, cnt);
+            cnt++;
+            continue;
+        }
+        if (retrieval_better(&s, &h[0])) {
+            h[0] = s; /* heap.Fix(&h, 0) */
+            heap_down(h, 0, cnt);
+        }
+    }
+    qsort(h, (size_t)cnt, sizeof(retrieval_doc), retrieval_cmp);
+    for (int64_t i = 0; i < cnt; i++) {
+        out_pos[i] = h[i].pos;
+        out_scores[i] = h[i].score;
+    }
+    free(h);
+    return cnt;
+}

@@ -111,6 +111,15 @@ void orc_ref_score_q4(int op, const uint16_t* queries, int64_t nq,
  * reference's per-tensor symmetric grid, in place. */
 void orc_fake_quantize(float* data, int64_t n, int bits);
 
+/* topRetrievalScores + dotRetrievalVectors (runtime/retrieval_eval.go:
+ * 586-661) for one f32 query [qd] against n f32 doc vectors [n, d] with
+ * NUL-terminated doc ids: the bounded heap of the top_k (top_k <= 0 or
+ * > n: all n) by retrievalScoreBetter (score desc, then id asc, bytewise),
+ * then sorted; the dot runs over min(qd, d) columns.  Writes the chosen
+ * docs' positions and scores in rank order; returns how many. */
+int64_t orc_top_retrieval_scores(const float* query, int64_t qd, const float* docs, int64_t n, int64_t d,
+                                 const char* const* ids, int64_t top_k, int64_t* out_pos, float* out_scores);
+
 /* ---- 2. packed scoring contract (defined by this repository) ---------- */
 
 /* q8 rows: code = clamp(round((x*127)/maxabs), -127, 127), scale =

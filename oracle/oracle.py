@@ -66,6 +66,7 @@ def lib() -> C.CDLL:
             "orc_softmax_rows": (None, [p, i64, i64]),
             "orc_gelu": (None, [p, i64]),
             "orc_encoder_pooled": (ci, [p, p, i64, i64, p, i64, i64, p, p, p, p, p, p, i64, p, C.c_char_p, ci]),
+            "orc_top_retrieval_scores": (i64, [p, i64, p, i64, i64, p, i64, p, p]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -437,3 +438,17 @@ def fair_embed(tokens, mask, table_f16, proj_f16=None, proj_codes=None, col_scal
     lib().orc_fair_embed(_p(tokens), _p(mask), b, t, _p(table), vocab, d, _p(proj_f16), _p(proj_codes),
                          _p(col_scale), e, int(threads or os.cpu_count() or 1), _p(out))
     return out
+
+
+def top_retrieval_scores(query, docs, ids, top_k):
+    """topRetrievalScores (retrieval_eval.go:586-623) for one query:
+    (positions of the chosen docs, their f32 scores) in rank order."""
+    q = _c(query, np.float32)
+    d = _c(docs, np.float32)
+    n = d.shape[0]
+    arr = (C.c_char_p * max(n, 1))(*[x.encode() if isinstance(x, str) else x for x in ids])
+    pos = np.empty(max(n, 1), np.int64)
+    sc = np.empty(max(n, 1), np.float32)
+    cnt = lib().orc_top_retrieval_scores(_p(q), q.shape[-1], _p(d), n, d.shape[1], C.cast(arr, C.c_void_p),
+                                         int(top_k), _p(pos), _p(sc))
+    return pos[:cnt], sc[:cnt]
