@@ -297,6 +297,15 @@ int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens_dev, const in
                               int64_t t, const MantaRocmEncoderWeights* w, int64_t vocab, int64_t d, int64_t h,
                               uint16_t* out_dev, char** err);
 
+/* The encoder block applied `layers` times (1..64) with the same weights,
+ * each block's encoded output the next block's hidden input:
+ * embed_pooled_batch of examples/encoder_trainable_q8x2.manta:9-50 is
+ * layers = 2 (its manifest's encoder_repeats).  layers = 1 is
+ * manta_rocm_encoder_pooled. */
+int manta_rocm_encoder_pooled_layers(MantaRocm* rt, const int32_t* tokens_dev, const int32_t* mask_dev, int64_t b,
+                                     int64_t t, const MantaRocmEncoderWeights* w, int64_t vocab, int64_t d,
+                                     int64_t h, int64_t layers, uint16_t* out_dev, char** err);
+
 /* top-k over an f32 score matrix [rows, cols] (rows == 1 is the rank-1
  * form).  Replaces topKTensor (tensor_ops.go:1523-1592). */
 int manta_rocm_topk(MantaRocm* rt, const float* scores_dev, int64_t rows, int64_t cols, int64_t k,

@@ -87,6 +87,8 @@ SIGNATURES = {
         [_p, C.c_char_p, C.POINTER(C.c_uint64), C.POINTER(C.c_double), C.c_int, _err],
     ),
     "manta_rocm_span": (C.c_int, [_p, C.c_int, C.POINTER(C.c_double), _err]),
+    "manta_rocm_encoder_pooled_layers": (
+        C.c_int, [_p, _p, _p, _i64, _i64, C.POINTER(EncoderWeights), _i64, _i64, _i64, _i64, _p, _err]),
     "manta_rocm_encoder_pooled": (
         C.c_int, [_p, _p, _p, _i64, _i64, C.POINTER(EncoderWeights), _i64, _i64, _i64, _p, _err]),
     # include/manta_mll.h (host only)

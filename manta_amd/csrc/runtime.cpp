@@ -1599,7 +1599,14 @@ int manta_rocm_normalize_rows(MantaRocm* rt, float* x, int64_t rows, int64_t col
 int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t* mask, int64_t b, int64_t t,
                               const MantaRocmEncoderWeights* w, int64_t vocab, int64_t d, int64_t h,
                               uint16_t* out, char** err) {
+    return manta_rocm_encoder_pooled_layers(rt, tokens, mask, b, t, w, vocab, d, h, 1, out, err);
+}
+
+int manta_rocm_encoder_pooled_layers(MantaRocm* rt, const int32_t* tokens, const int32_t* mask, int64_t b,
+                                     int64_t t, const MantaRocmEncoderWeights* w, int64_t vocab, int64_t d,
+                                     int64_t h, int64_t layers, uint16_t* out, char** err) {
     RT_CHECK(rt);
+    if (layers < 1 || layers > 64) return fail(err, MANTA_ROCM_ERROR, "encoder: %lld layers", (long long)layers);
     if (!tokens || !mask || !w || !out) return fail(err, MANTA_ROCM_ERROR, "nil encoder input");
     if (!w->token_codes || !w->token_scales) return fail(err, MANTA_ROCM_ERROR, "nil encoder token table");
     for (int i = 0; i < 6; i++)
@@ -1634,6 +1641,8 @@ int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens, const int32_
     LAUNCH_TRY(manta::launch_enc_gather_q8(tokens, rows, w->token_codes, w->token_scales, vocab, D, x, rt->err_word, s),
                "encoder_gather");
     rt->gather_pending = true;
+    for (int64_t layer = 0; layer < layers; layer++) {
+    if (layer > 0) std::swap(x, mx);  // this block's hidden input is the last block's encoded output
     LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[0], w->col_scales[0], 0, q, 0, R, D, D, 1, s), "encoder_gemm");
     LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[1], w->col_scales[1], 0, k, 0, R, D, D, 1, s), "encoder_gemm");
     LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[2], w->col_scales[2], 0, v, 0, R, D, D, 1, s), "encoder_gemm");
@@ -1649,6 +1658,7 @@ int manta_rocm_encoder_pooled(MantaRocm* rt, const int32_t* tokens, const int32_
     // projected = gelu @ projection (into v); encoded = layernorm(projected + attn_hidden) (into mx)
     LAUNCH_TRY(manta::launch_enc_gemm(1, ffn, 0, w->codes[5], w->col_scales[5], 0, v, 0, R, D, H, 1, s), "encoder_gemm");
     LAUNCH_TRY(manta::launch_enc_add_layernorm(v, k, mx, rows, D, s), "encoder_layernorm");
+    }
     LAUNCH_TRY(manta::launch_normalize_rows(mx, rows, d, s), "normalize");
     LAUNCH_TRY(manta::launch_mean_pool_masked(mx, mask, b, t, d, pooled, s), "mean_pool");
     LAUNCH_TRY(manta::launch_enc_to_f16(pooled, b * d, out, s), "encoder_out");

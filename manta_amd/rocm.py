@@ -366,10 +366,12 @@ class Runtime:
 
     # ------------------------------------------------------------ encoder
     def encoder_pooled(self, tokens: DeviceArray, mask: DeviceArray, token_codes: DeviceArray,
-                       token_scales: DeviceArray, weights, out: Optional[DeviceArray] = None) -> DeviceArray:
-        """The one-layer encoder's embed_pooled_batch: f16 [b, d].  weights:
-        six (int8 [k, n] codes, f32 [n] column scales) device pairs in the
-        order attn_q, attn_k, attn_v, attn_o, ffn_up, projection."""
+                       token_scales: DeviceArray, weights, out: Optional[DeviceArray] = None,
+                       layers: int = 1) -> DeviceArray:
+        """The encoder's embed_pooled_batch: f16 [b, d].  weights: six (int8
+        [k, n] codes, f32 [n] column scales) device pairs in the order
+        attn_q, attn_k, attn_v, attn_o, ffn_up, projection; `layers` blocks
+        with those weights (encoder_trainable_q8x2: 2)."""
         if len(tokens.shape) != 2 or np.dtype(tokens.dtype) != np.dtype(np.int32):
             raise ValueError("encoder tokens must be int32 [b, t] (got %s %s)" % (tokens.dtype, tokens.shape))
         if tuple(mask.shape) != tuple(tokens.shape) or np.dtype(mask.dtype) != np.dtype(np.int32):
@@ -396,8 +398,8 @@ class Runtime:
             w.codes[i], w.col_scales[i] = codes.addr, scales.addr
         if out is None:
             out = self.empty((b, d), np.uint16)
-        call("manta_rocm_encoder_pooled", self.handle, tokens.ptr, mask.ptr, C.c_int64(b), C.c_int64(t),
-             C.byref(w), C.c_int64(vocab), C.c_int64(d), C.c_int64(h), out.ptr)
+        call("manta_rocm_encoder_pooled_layers", self.handle, tokens.ptr, mask.ptr, C.c_int64(b), C.c_int64(t),
+             C.byref(w), C.c_int64(vocab), C.c_int64(d), C.c_int64(h), C.c_int64(layers), out.ptr)
         return out
 
 

@@ -716,6 +716,19 @@ int orc_encoder_pooled(const int32_t* tokens, const int32_t* mask, int64_t b, in
                        const float* table, int64_t vocab, int64_t d, const float* wq,
                        const float* wk, const float* wv, const float* wo, const float* wup,
                        const float* wproj, int64_t h, float* out, char* msg, int msglen) {
+    return orc_encoder_pooled_layers(tokens, mask, b, t, table, vocab, d, wq, wk, wv, wo, wup, wproj, h, 1, out,
+                                     msg, msglen);
+}
+
+/* The same with the encoder block applied `layers` times with shared
+ * weights, each block's encoded output the next block's hidden input:
+ * examples/encoder_trainable_q8x2.manta:9-50 is layers = 2 (the manifest's
+ * encoder_repeats). */
+int orc_encoder_pooled_layers(const int32_t* tokens, const int32_t* mask, int64_t b, int64_t t,
+                              const float* table, int64_t vocab, int64_t d, const float* wq,
+                              const float* wk, const float* wv, const float* wo, const float* wup,
+                              const float* wproj, int64_t h, int64_t layers, float* out, char* msg,
+                              int msglen) {
     const int64_t rows = b * t;
     float* hid = (float*)malloc((size_t)(rows * d) * sizeof(float));
     float* q = (float*)malloc((size_t)(rows * d) * sizeof(float));
@@ -732,6 +745,8 @@ int orc_encoder_pooled(const int32_t* tokens, const int32_t* mask, int64_t b, in
         goto done;
     }
     if (orc_gather_rows(table, vocab, d, tokens, rows, hid, msg, msglen)) goto done;
+    for (int64_t layer = 0; layer < layers; layer++) {
+    if (layer > 0) memcpy(hid, q, (size_t)(rows * d) * sizeof(float)); /* encoded -> hidden */
     orc_matmul(hid, wq, rows, d, d, q);
     orc_matmul(hid, wk, rows, d, d, k);
     orc_matmul(hid, wv, rows, d, d, v);
@@ -749,6 +764,7 @@ int orc_encoder_pooled(const int32_t* tokens, const int32_t* mask, int64_t b, in
     orc_matmul(f, wproj, rows, h, d, q);                             /* projected */
     for (int64_t i = 0; i < rows * d; i++) q[i] = q[i] + att[i];     /* + attn_hidden */
     orc_layernorm_rows(q, rows, d);                                  /* encoded */
+    }
     orc_normalize_rows(q, rows, d);
     orc_mean_pool_masked(q, mask, b, t, d, out);
     rc = 0;

@@ -111,6 +111,17 @@ void orc_ref_score_q4(int op, const uint16_t* queries, int64_t nq,
  * reference's per-tensor symmetric grid, in place. */
 void orc_fake_quantize(float* data, int64_t n, int bits);
 
+/* The encoder of examples/encoder_trainable_q8.manta (one block) and
+ * encoder_trainable_q8x2.manta (the block applied `layers` times with
+ * shared weights) over dequantized f32 weights; out f32 [b, d]. */
+int orc_encoder_pooled(const int32_t* tokens, const int32_t* mask, int64_t b, int64_t t, const float* table,
+                       int64_t vocab, int64_t d, const float* wq, const float* wk, const float* wv, const float* wo,
+                       const float* wup, const float* wproj, int64_t h, float* out, char* msg, int msglen);
+int orc_encoder_pooled_layers(const int32_t* tokens, const int32_t* mask, int64_t b, int64_t t,
+                              const float* table, int64_t vocab, int64_t d, const float* wq, const float* wk,
+                              const float* wv, const float* wo, const float* wup, const float* wproj, int64_t h,
+                              int64_t layers, float* out, char* msg, int msglen);
+
 /* topRetrievalScores + dotRetrievalVectors (runtime/retrieval_eval.go:
  * 586-661) for one f32 query [qd] against n f32 doc vectors [n, d] with
  * NUL-terminated doc ids: the bounded heap of the top_k (top_k <= 0 or

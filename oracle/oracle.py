@@ -67,6 +67,8 @@ def lib() -> C.CDLL:
             "orc_gelu": (None, [p, i64]),
             "orc_encoder_pooled": (ci, [p, p, i64, i64, p, i64, i64, p, p, p, p, p, p, i64, p, C.c_char_p, ci]),
             "orc_top_retrieval_scores": (i64, [p, i64, p, i64, i64, p, i64, p, p]),
+            "orc_encoder_pooled_layers": (
+                ci, [p, p, i64, i64, p, i64, i64, p, p, p, p, p, p, i64, i64, p, C.c_char_p, ci]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -230,8 +232,9 @@ def gelu(x):
     return x
 
 
-def encoder_pooled(tokens, mask, table, wq, wk, wv, wo, wup, wproj):
-    """f32 [b, d] of the encoder pipeline over dequantized f32 weights."""
+def encoder_pooled(tokens, mask, table, wq, wk, wv, wo, wup, wproj, layers=1):
+    """f32 [b, d] of the encoder pipeline over dequantized f32 weights (the
+    block applied `layers` times with shared weights)."""
     tokens = _c(tokens, np.int32)
     mask = _c(mask, np.int32)
     table = _c(table, np.float32)
@@ -241,8 +244,8 @@ def encoder_pooled(tokens, mask, table, wq, wk, wv, wo, wup, wproj):
     h = ws[4].shape[1]
     out = np.empty((b, d), np.float32)
     msg = C.create_string_buffer(256)
-    rc = lib().orc_encoder_pooled(_p(tokens), _p(mask), b, t, _p(table), vocab, d, *[_p(w) for w in ws], h,
-                                  _p(out), msg, 256)
+    rc = lib().orc_encoder_pooled_layers(_p(tokens), _p(mask), b, t, _p(table), vocab, d, *[_p(w) for w in ws], h,
+                                         int(layers), _p(out), msg, 256)
     if rc:
         raise OracleError(msg.value.decode())
     return out

@@ -71,3 +71,50 @@ def test_encoder_token_out_of_range_is_reported(rt):
     rt.encoder_pooled(rt.to_device(tokens), rt.to_device(mask), rt.to_device(tcodes), rt.to_device(tscales), dev)
     with pytest.raises(MantaRocmError, match="gather index 10 out of range"):
         rt.synchronize()
+
+
+def _run_layers(rt, layers, tokens, mask, tcodes, tscales, packed):
+    dev = [(rt.to_device(c), rt.to_device(s)) for c, s in packed]
+    out = rt.encoder_pooled(rt.to_device(tokens), rt.to_device(mask), rt.to_device(tcodes), rt.to_device(tscales),
+                            dev, layers=layers)
+    return out
+
+
+def _want_layers(layers, tokens, mask, tcodes, tscales, packed):
+    table = (tcodes.astype(np.float32) * tscales[:, None]).astype(np.float32)
+    ws = [(c.astype(np.float32) * s[None, :]).astype(np.float32) for c, s in packed]
+    return orc.encoder_pooled(tokens, mask, table, *ws, layers=layers)
+
+
+@pytest.mark.parametrize("b,t,vocab,d,h", [(6, 16, 50, 64, 128), (8, 64, 300, 384, 1536), (4, 24, 40, 40, 72)])
+def test_two_layer_encoder_matches_oracle(rt, b, t, vocab, d, h):
+    """encoder_trainable_q8x2 (the block twice, shared weights) at the same
+    bar as one layer."""
+    case = _case(b * 77 + t, b, t, vocab, d, h)
+    got = _run_layers(rt, 2, *case).download().view(np.float16).astype(np.float32)
+    want = _want_layers(2, *case)
+    assert np.all(got[0] == 0.0) and np.all(want[0] == 0.0)
+    live = np.linalg.norm(want, axis=1) > 0
+    cos = (got[live] * want[live]).sum(1) / (np.linalg.norm(got[live], axis=1) * np.linalg.norm(want[live], axis=1))
+    assert cos.min() >= 0.9999, cos.min()
+    assert np.abs(got - want).max() < 2e-3
+    one = _run_layers(rt, 1, *case).download().view(np.float16).astype(np.float32)
+    assert np.abs(one - got).max() > 1e-2  # the second block ran
+
+
+def test_encoder_output_feeds_score_topk(rt):
+    """The encoder's device output is the query matrix of the fused score +
+    top-k with no host round trip; the result equals the reference scoring
+    of those embeddings (cosineRows on the dequantized candidates)."""
+    from manta_amd import synth
+    b, t, vocab, d, h = 16, 32, 200, 128, 256
+    case = _case(91, b, t, vocab, d, h, empty_row=False)
+    emb = _run_layers(rt, 2, *case)  # f16 [b, d] on device
+    codes, scales = synth.q8_rows(91, 5, 20000, d, normalize=True)
+    cands = rt.bind_q8(codes, scales)
+    ids, scores, _ = rt.score_topk(cands, "cosine", emb, 25)
+    q = emb.download()
+    ref = orc.cosine_rows(orc.f16_to_f32(q), orc.dequant_q8(codes, scales))
+    want = orc.topk(ref, 25)
+    np.testing.assert_array_equal(ids.download(), want)
+    np.testing.assert_array_equal(scores.download(), np.take_along_axis(ref, want, 1))

@@ -69,23 +69,25 @@ def _case(seed, b, t, vocab, d, h):
     return tokens, mask, table, ws
 
 
-def _numpy_f64(tokens, mask, table, ws):
+def _numpy_f64(tokens, mask, table, ws, layers=1):
     wq, wk, wv, wo, wup, wproj = [w.astype(np.float64) for w in ws]
-    x = table.astype(np.float64)[tokens]
-    q, k, v = x @ wq, x @ wk, x @ wv
-    s = q @ np.swapaxes(k, 1, 2)
-    s = np.exp(s - s.max(-1, keepdims=True))
-    p = s / s.sum(-1, keepdims=True)
-    a = (p @ v) @ wo + x
 
     def ln(z):
         m = z.mean(-1, keepdims=True)
         return (z - m) / np.sqrt(((z - m) ** 2).mean(-1, keepdims=True) + 1e-5)
 
-    ah = ln(a)
-    f = ah @ wup
-    f = 0.5 * f * (1 + np.tanh(0.7978845608 * (f + 0.044715 * f ** 3)))
-    e = ln(f @ wproj + ah)
+    e = table.astype(np.float64)[tokens]
+    for _ in range(layers):  # encoder_trainable_q8x2: the block twice, shared weights
+        x = e
+        q, k, v = x @ wq, x @ wk, x @ wv
+        s = q @ np.swapaxes(k, 1, 2)
+        s = np.exp(s - s.max(-1, keepdims=True))
+        p = s / s.sum(-1, keepdims=True)
+        a = (p @ v) @ wo + x
+        ah = ln(a)
+        f = ah @ wup
+        f = 0.5 * f * (1 + np.tanh(0.7978845608 * (f + 0.044715 * f ** 3)))
+        e = ln(f @ wproj + ah)
     e = e / np.linalg.norm(e, axis=-1, keepdims=True)
     m = mask.astype(np.float64)[..., None]
     cnt = m.sum(1)
@@ -105,3 +107,13 @@ def test_encoder_single_token_passes_v_through():
     got = orc.encoder_pooled(tokens, mask, table, *ws)
     want = _numpy_f64(tokens, mask, table, ws)
     np.testing.assert_allclose(got, want, rtol=0, atol=5e-5)
+
+
+def test_two_layer_encoder_against_float64():
+    """encoder_trainable_q8x2.manta:9-50: the second block reads the first
+    block's encoded output; the same float64 evaluation applied twice."""
+    tokens, mask, table, ws = _case(5, 3, 10, 30, 40, 80)
+    got = orc.encoder_pooled(tokens, mask, table, *ws, layers=2)
+    np.testing.assert_allclose(got, _numpy_f64(tokens, mask, table, ws, layers=2), rtol=0, atol=5e-5)
+    # the second block matters: one block is far from two
+    assert np.max(np.abs(got - _numpy_f64(tokens, mask, table, ws, layers=1))) > 1e-2
