@@ -101,7 +101,11 @@ enum {
 
 /* Value kinds. */
 enum {
-    /* dense tensor: `data` holds prod(shape) elements of type `storage` */
+    /* dense tensor: `data` holds prod(shape) elements of type `storage`;
+     * storage MANTA_DT_Q8: int8 codes with an f32 scale per column (last
+     * dimension) in `scales` -- a q8 weight matrix, whose values are the
+     * f32 products code * scale (a reference per-tensor grid repacks
+     * exactly, one scale repeated) */
     MANTA_VALUE_TENSOR = 0,
     /* a q8 / q4 tensor [n, d] or [sets, n, d] bound on device
      * (manta_rocm_bind_q8_rows / _q4_blocks / _packed): `candidates` */

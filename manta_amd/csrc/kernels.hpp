@@ -309,6 +309,7 @@ hipError_t launch_enc_softmax_rows(float* x, int64_t rows, int cols, hipStream_t
 hipError_t launch_enc_add_layernorm(const float* a, const float* b, float* y, int64_t rows, int cols,
                                     hipStream_t s);
 hipError_t launch_enc_to_f16(const float* x, int64_t n, uint16_t* out, hipStream_t s);
+hipError_t launch_enc_gelu(float* x, int64_t n, hipStream_t s);
 
 hipError_t launch_topk_rows_partial(const float* scores, int64_t rows, int64_t cols, int64_t seg,
                                     int parts, int k, int cap, int smallest, uint64_t* partial,
@@ -326,5 +327,14 @@ hipError_t launch_gather_elems(const void* table, int elem_bytes, int64_t rows, 
                                hipStream_t s);
 hipError_t launch_widen_f16(const uint16_t* in, float* out, int64_t n, hipStream_t s);
 hipError_t launch_mean_pool(const float* x, int64_t B, int64_t T, int64_t C, float* out, hipStream_t s);
+// transposeTensor of [B][R][C] elements of elem_bytes -> [B][C][R]
+hipError_t launch_transpose(const void* in, int elem_bytes, int64_t B, int64_t R, int64_t C, void* out,
+                            hipStream_t s);
+// binaryTensorOp: op 0 add, 1 sub, 2 mul, 3 div (f32, elementwise)
+hipError_t launch_binary_f32(int op, const float* a, const float* b, float* out, int64_t n, hipStream_t s);
+// q8 codes to f32 values: code * scale, the scale per row (per_col 0, rows
+// of `cols` codes) or per column (per_col 1)
+hipError_t launch_dequant_q8(const int8_t* codes, const float* scales, int64_t rows, int64_t cols, int per_col,
+                             float* out, hipStream_t s);
 
 }  // namespace manta

@@ -188,6 +188,8 @@ __global__ __launch_bounds__(256) void enc_softmax_rows_kernel(float* __restrict
 
 // y = layernorm(a + b) per row (binary_add then layerNormRows): one wave per
 // row; f32 mean and variance, f64 reciprocal square root of variance + 1e-5.
+// ADD false: layerNormRows(a) alone (b unused).
+template <bool ADD>
 __global__ __launch_bounds__(256) void enc_add_layernorm_kernel(const float* __restrict__ a,
                                                                 const float* __restrict__ b, float* __restrict__ y,
                                                                 int64_t rows, int cols) {
@@ -195,19 +197,26 @@ __global__ __launch_bounds__(256) void enc_add_layernorm_kernel(const float* __r
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
     const float* ar = a + r * cols;
-    const float* br = b + r * cols;
+    const float* br = ADD ? b + r * cols : nullptr;
     float* yr = y + r * cols;
+    auto in = [&](int c) { return ADD ? fadd_rn(ar[c], br[c]) : ar[c]; };
     float s = 0.0f;
-    for (int c = lane; c < cols; c += 64) s = fadd_rn(s, fadd_rn(ar[c], br[c]));
+    for (int c = lane; c < cols; c += 64) s = fadd_rn(s, in(c));
     const float mean = fdiv_rn(wave_sum_f32(s), (float)cols);
     float v = 0.0f;
     for (int c = lane; c < cols; c += 64) {
-        const float d = fsub_rn(fadd_rn(ar[c], br[c]), mean);
+        const float d = fsub_rn(in(c), mean);
         v = __fmaf_rn(d, d, v);
     }
     const float var = fdiv_rn(wave_sum_f32(v), (float)cols);
     const float inv = (float)(1.0 / sqrt((double)var + 1e-5));
-    for (int c = lane; c < cols; c += 64) yr[c] = fmul_rn(fsub_rn(fadd_rn(ar[c], br[c]), mean), inv);
+    for (int c = lane; c < cols; c += 64) yr[c] = fmul_rn(fsub_rn(in(c), mean), inv);
+}
+
+// geluTensor in place, element by element.
+__global__ __launch_bounds__(256) void enc_gelu_kernel(float* __restrict__ x, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        x[i] = gelu_value(x[i]);
 }
 
 __global__ __launch_bounds__(256) void enc_to_f16_kernel(const float* __restrict__ x, int64_t n,
@@ -260,8 +269,19 @@ hipError_t launch_enc_softmax_rows(float* x, int64_t rows, int cols, hipStream_t
 
 hipError_t launch_enc_add_layernorm(const float* a, const float* b, float* y, int64_t rows, int cols,
                                     hipStream_t s) {
-    hipLaunchKernelGGL(enc_add_layernorm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a, b, y, rows,
-                       cols);
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    if (b)
+        hipLaunchKernelGGL(enc_add_layernorm_kernel<true>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a, b, y,
+                           rows, cols);
+    else
+        hipLaunchKernelGGL(enc_add_layernorm_kernel<false>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a, b,
+                           y, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_enc_gelu(float* x, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(enc_gelu_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, n);
     return hipGetLastError();
 }
 

@@ -55,6 +55,36 @@ __global__ __launch_bounds__(256) void mean_pool_kernel(const float* __restrict_
     out[i] = fdiv_rn(s, (float)T);
 }
 
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ in, int64_t R, int64_t C, int64_t total,
+                                                        T* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        // output element i of [B][C][R]: read in[b][r][c]
+        const int64_t rc = R * C;
+        const int64_t b = i / rc, j = i - b * rc;
+        const int64_t c = j / R, r = j - c * R;
+        out[i] = in[b * rc + r * C + c];
+    }
+}
+
+__global__ __launch_bounds__(256) void binary_f32_kernel(int op, const float* __restrict__ a,
+                                                         const float* __restrict__ b, float* __restrict__ out,
+                                                         int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const float x = a[i], y = b[i];
+        out[i] = op == 0 ? fadd_rn(x, y) : op == 1 ? fsub_rn(x, y) : op == 2 ? fmul_rn(x, y) : fdiv_rn(x, y);
+    }
+}
+
+__global__ __launch_bounds__(256) void dequant_q8_kernel(const int8_t* __restrict__ codes,
+                                                         const float* __restrict__ scales, int64_t cols,
+                                                         int per_col, int64_t total, float* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / cols;
+        out[i] = fmul_rn((float)codes[i], scales[per_col ? i - r * cols : r]);
+    }
+}
+
 unsigned grid_for(int64_t total) {
     const int64_t g = (total + 255) / 256;
     return (unsigned)(g < 65536 * 4 ? (g < 1 ? 1 : g) : 65536 * 4);
@@ -90,6 +120,45 @@ hipError_t launch_gather_elems(const void* table, int elem_bytes, int64_t rows, 
 hipError_t launch_widen_f16(const uint16_t* in, float* out, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(widen_f16_kernel, dim3(grid_for(n)), dim3(256), 0, s, in, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose(const void* in, int elem_bytes, int64_t B, int64_t R, int64_t C, void* out,
+                            hipStream_t s) {
+    const int64_t total = B * R * C;
+    if (total <= 0) return hipSuccess;
+    const unsigned grid = grid_for(total);
+    switch (elem_bytes) {
+        case 2:
+            hipLaunchKernelGGL(transpose_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)in, R, C,
+                               total, (uint16_t*)out);
+            break;
+        case 4:
+            hipLaunchKernelGGL(transpose_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, (const uint32_t*)in, R, C,
+                               total, (uint32_t*)out);
+            break;
+        case 8:
+            hipLaunchKernelGGL(transpose_kernel<uint64_t>, dim3(grid), dim3(256), 0, s, (const uint64_t*)in, R, C,
+                               total, (uint64_t*)out);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_binary_f32(int op, const float* a, const float* b, float* out, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(binary_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, op, a, b, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_q8(const int8_t* codes, const float* scales, int64_t rows, int64_t cols, int per_col,
+                             float* out, hipStream_t s) {
+    const int64_t total = rows * cols;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(dequant_q8_kernel, dim3(grid_for(total)), dim3(256), 0, s, codes, scales, cols, per_col, total,
+                       out);
     return hipGetLastError();
 }
 

@@ -117,7 +117,7 @@ std::string go_shape(const std::vector<int64_t>& s) {
 struct Val {
     int kind = MANTA_VALUE_TENSOR;
     std::string dtype;  // the artifact's dtype string
-    int storage = 0;
+    int storage = 0;    // a q8 TENSOR holds int8 codes and an f32 scale per column in `scales`
     std::vector<int64_t> shape;
     void* data = nullptr;
     void* scales = nullptr;
@@ -307,7 +307,15 @@ bool import_value(const MantaRocmValue& in, Val* v, std::string* e) {
     }
     if (in.kind == MANTA_VALUE_TENSOR) {
         v->storage = in.storage ? in.storage : in.dtype;
-        if (!elem_bytes(v->storage)) return *e = "tensor storage must be f32, f16, i32 or i64", false;
+        if (v->storage == MANTA_DT_Q8) {
+            // int8 codes with an f32 scale per column (a per-tensor grid is
+            // one scale repeated)
+            if (v->shape.empty()) return *e = "a q8 tensor needs a shape", false;
+            if (!in.scales) return *e = "a q8 tensor needs its per-column scales", false;
+            v->scales = in.scales;
+        } else if (!elem_bytes(v->storage)) {
+            return *e = "tensor storage must be f32, f16, i32, i64 or q8", false;
+        }
         if (!in.data && v->elems() > 0) return *e = "nil tensor data", false;
         v->data = in.data;
         return true;
@@ -383,19 +391,38 @@ struct Run {
         *out = &it->second;
         return true;
     }
-    // An f32 copy of a dense value (f16 widened).
-    bool as_f32(const Val& in, Val* out, const char* what) {
-        if (in.kind != MANTA_VALUE_TENSOR || (in.storage != MANTA_DT_F32 && in.storage != MANTA_DT_F16))
+    // The f32 values of a value: itself when it is held in f32 and `copy` is
+    // false, else a new f32 buffer (f16 widened, q8 dequantized to the
+    // f32 products code * scale the reference's tensors hold).
+    bool f32_of(const Val& in, Val* out, const char* what, bool copy) {
+        const bool dense = in.kind == MANTA_VALUE_TENSOR;
+        const bool rows_q8 = in.kind == MANTA_VALUE_ROWS && in.storage == MANTA_DT_Q8;
+        if (!(dense && (in.storage == MANTA_DT_F32 || in.storage == MANTA_DT_F16 || in.storage == MANTA_DT_Q8)) &&
+            !rows_q8)
             return unsupported(std::string(what) + " of a " + dtype_name(in.storage) +
                                " value is not offered by the rocm executor");
+        if (dense && in.storage == MANTA_DT_F32 && !copy) {
+            *out = in;
+            return true;
+        }
         *out = in;
+        out->kind = MANTA_VALUE_TENSOR;
         out->storage = MANTA_DT_F32;
+        out->scales = nullptr;
         out->data = alloc((size_t)in.elems() * 4);
         if (!out->data) return fail("out of device memory");
         if (in.storage == MANTA_DT_F16)
             return hip(manta::launch_widen_f16((const uint16_t*)in.data, (float*)out->data, in.elems(), s), what);
+        if (in.storage == MANTA_DT_Q8) {
+            const int64_t cols = in.shape.back();
+            return hip(manta::launch_dequant_q8((const int8_t*)in.data, (const float*)in.scales,
+                                                cols ? in.elems() / cols : 0, cols, dense ? 1 : 0, (float*)out->data,
+                                                s),
+                       what);
+        }
         return hip(hipMemcpyAsync(out->data, in.data, (size_t)in.elems() * 4, hipMemcpyDeviceToDevice, s), what);
     }
+    bool as_f32(const Val& in, Val* out, const char* what) { return f32_of(in, out, what, true); }
 };
 
 // ------------------------------------------------------------ kernel ops
@@ -452,7 +479,7 @@ bool run_mean_pool(Run& r, const Val& in, const Val* mask, Val* out) {
     if (in.shape.size() != 2 && in.shape.size() != 3)
         return r.fail("mean_pool expects rank-2 or rank-3 tensor input");
     Val x;
-    if (!r.as_f32(in, &x, "mean_pool")) return false;
+    if (!r.f32_of(in, &x, "mean_pool", false)) return false;
     const bool r3 = in.shape.size() == 3;
     const int64_t B = r3 ? in.shape[0] : 1, T = in.shape[r3 ? 1 : 0], C = in.shape.back();
     *out = Val();
@@ -475,6 +502,50 @@ bool run_mean_pool(Run& r, const Val& in, const Val* mask, Val* out) {
     return r.abi(manta_rocm_mean_pool_masked(r.p->rt, (const float*)x.data, (const int32_t*)mask->data, B, T, C,
                                              (float*)out->data, &e),
                  e);
+}
+
+// softmaxRows / layerNormRows / geluTensor (tensor_ops.go:1140-1168,
+// 1303-1344): rank-2 and rank-3 values row by row (softmax and layernorm
+// leave other ranks unchanged, as the reference does); the encoder's
+// kernels, whose reductions run in tree order.
+bool run_rowwise(Run& r, const std::string& op, const Val& in, Val* out) {
+    const int64_t n = in.elems();
+    const bool rowwise = in.shape.size() == 2 || in.shape.size() == 3;
+    const int64_t cols = rowwise ? in.shape.back() : 0, rows = cols ? n / cols : 0;
+    if (cols > 0x7FFFFFFF) return r.unsupported(op + " rows wider than 2^31");
+    if (op == "layernorm" && rowwise) {
+        // out of place: the f32 source, a new output
+        Val src;
+        if (!r.f32_of(in, &src, "layernorm", false)) return false;
+        *out = src;
+        out->data = r.alloc((size_t)n * 4);
+        if (!out->data) return r.fail("out of device memory");
+        return r.hip(manta::launch_enc_add_layernorm((const float*)src.data, nullptr, (float*)out->data, rows,
+                                                     (int)cols, r.s),
+                     "layernorm");
+    }
+    if (!r.as_f32(in, out, op.c_str())) return false;  // a copy the in-place kernels own
+    if (op == "gelu") return r.hip(manta::launch_enc_gelu((float*)out->data, n, r.s), "gelu");
+    if (op == "softmax" && rowwise)
+        return r.hip(manta::launch_enc_softmax_rows((float*)out->data, rows, (int)cols, r.s), "softmax");
+    return true;
+}
+
+// binaryTensorOp (tensor_ops.go:724-742): equal shapes, f32 elementwise.
+bool run_binary(Run& r, const std::string& op, const Val& a, const Val& b, Val* out) {
+    if (a.shape != b.shape) return r.fail("shape mismatch " + go_shape(a.shape) + " vs " + go_shape(b.shape));
+    Val x, y;
+    if (!r.f32_of(a, &x, op.c_str(), false) || !r.f32_of(b, &y, op.c_str(), false)) return false;
+    *out = a;
+    out->kind = MANTA_VALUE_TENSOR;
+    out->storage = MANTA_DT_F32;
+    out->scales = nullptr;
+    out->data = r.alloc((size_t)a.elems() * 4);
+    if (!out->data) return r.fail("out of device memory");
+    const int code = op == "binary_add" ? 0 : op == "binary_sub" ? 1 : op == "binary_mul" ? 2 : 3;
+    return r.hip(manta::launch_binary_f32(code, (const float*)x.data, (const float*)y.data, (float*)out->data,
+                                          a.elems(), r.s),
+                 op.c_str());
 }
 
 // executeKernel (tensor_ops.go:476-516) over the supported ops.
@@ -506,6 +577,10 @@ bool run_kernel(Run& r, const Kernel& k, const std::vector<Val*>& args, std::vec
             ok = arg(0, &a) && (op.inputs.size() > 1 ? arg(1, &b) : true) && run_mean_pool(r, *a, b, &out);
         } else if (is_score_op(op.op)) {
             ok = arg(0, &a) && arg(1, &b) && run_score(r, score_op_code(op.op), *a, *b, &out);
+        } else if (op.op == "softmax" || op.op == "layernorm" || op.op == "gelu") {
+            ok = arg(0, &a) && run_rowwise(r, op.op, *a, &out);
+        } else if (op.op == "binary_add" || op.op == "binary_sub" || op.op == "binary_mul" || op.op == "binary_div") {
+            ok = arg(0, &a) && arg(1, &b) && run_binary(r, op.op, *a, *b, &out);
         } else {
             return r.unsupported("kernel " + q(k.name) + " op " + q(op.op) + " is not offered by the rocm executor");
         }
@@ -697,21 +772,50 @@ bool step_topk(Run& r, const Step& s, Val* out, std::string* dispatch) {
                  e);
 }
 
+// transposeTensor (tensor_ops.go:1064-1112): the last two dimensions.
+bool step_transpose(Run& r, const Step& s, Val* out) {
+    if (s.inputs.size() != 1 || s.outputs.size() != 1)
+        return r.fail("transpose step " + q(s.name) + " expects 1 input and 1 output");
+    Val* in = nullptr;
+    if (!r.tensor(s.inputs[0], &in)) return false;
+    if (in->kind == VK_DEFERRED) return r.fail("a score folded into its top-k has no matrix to transpose");
+    if (in->shape.size() != 2 && in->shape.size() != 3) return r.fail("transpose expects rank-2 or rank-3 tensor input");
+    Val src;
+    if (in->kind != MANTA_VALUE_TENSOR || in->storage == MANTA_DT_Q8) {
+        if (!r.f32_of(*in, &src, "transpose", false)) return false;
+    } else {
+        src = *in;
+    }
+    const bool r3 = src.shape.size() == 3;
+    const int64_t B = r3 ? src.shape[0] : 1, R = src.shape[r3 ? 1 : 0], C = src.shape.back();
+    *out = src;
+    out->shape = r3 ? std::vector<int64_t>{B, C, R} : std::vector<int64_t>{C, R};
+    const int es = elem_bytes(src.storage);
+    out->data = r.alloc((size_t)(B * R * C * es));
+    if (!out->data) return r.fail("out of device memory");
+    return r.hip(manta::launch_transpose(src.data, es, B, R, C, out->data, r.s), "transpose");
+}
+
+// matmulTensor (tensor_ops.go:981-1062): [M,K] x [K,N], [B,M,K] x [K,N] and
+// [B,M,K] x [B,K,N].  f16 x f16 (or q8 columns) runs on the f16 matrix
+// cores; an operand the pipeline holds in f32 runs on the f32 ones (the
+// encoder's GEMM; q8 weights are dequantized while staging).
 bool step_matmul(Run& r, const Step& s, Val* out) {
     if (s.inputs.size() != 2 || s.outputs.size() != 1)
         return r.fail("matmul step " + q(s.name) + " expects 2 inputs and 1 output");
     Val *lhs = nullptr, *rhs = nullptr;
     if (!r.tensor(s.inputs[0], &lhs) || !r.tensor(s.inputs[1], &rhs)) return false;
+    if (lhs->kind == VK_DEFERRED || rhs->kind == VK_DEFERRED)
+        return r.fail("a score folded into its top-k has no matrix to multiply");
     const size_t lr = lhs->shape.size(), rr = rhs->shape.size();
     if ((lr != 2 && lr != 3) || (rr != 2 && rr != 3)) return r.fail("matmul expects rank-2 or rank-3 tensor inputs");
     if (lr == 2 && rr != 2) return r.fail("matmul rank-2 lhs requires rank-2 rhs");
-    if (rr == 3) return r.unsupported("batched rank-3 x rank-3 matmul is not offered by the rocm executor");
-    const int64_t K = lhs->shape.back(), N = rhs->shape[1];
-    if (rhs->shape[0] != K) return r.fail("matmul mismatch " + go_shape(lhs->shape) + " x " + go_shape(rhs->shape));
-    if (lhs->kind != MANTA_VALUE_TENSOR || lhs->storage != MANTA_DT_F16 || rhs->kind != MANTA_VALUE_TENSOR ||
-        rhs->storage != MANTA_DT_F16)
-        return r.unsupported("matmul of " + lhs->dtype + " x " + rhs->dtype +
-                             " values held in f32 is not offered by the rocm executor (f16 operands only)");
+    const int64_t K = lhs->shape.back();
+    const int64_t N = rhs->shape.back();
+    if (rr == 2 && rhs->shape[0] != K)
+        return r.fail("matmul mismatch " + go_shape(lhs->shape) + " x " + go_shape(rhs->shape));
+    if (rr == 3 && (rhs->shape[0] != lhs->shape[0] || rhs->shape[1] != K))
+        return r.fail("matmul mismatch " + go_shape(lhs->shape) + " x " + go_shape(rhs->shape));
     const int64_t M = lhs->elems() / (K ? K : 1);
     *out = Val();
     out->dtype = lhs->dtype;
@@ -720,10 +824,36 @@ bool step_matmul(Run& r, const Step& s, Val* out) {
     out->shape.back() = N;
     out->data = r.alloc((size_t)(M * N) * 4);
     if (!out->data) return r.fail("out of device memory");
-    char* e = nullptr;
-    return r.abi(manta_rocm_matmul_f16(r.p->rt, (const uint16_t*)lhs->data, M, K, rhs->data, MANTA_ROCM_PROJ_F16,
-                                       nullptr, N, (float*)out->data, &e),
-                 e);
+    const bool lhs_f16 = lhs->kind == MANTA_VALUE_TENSOR && lhs->storage == MANTA_DT_F16;
+    const bool rhs_q8 = rhs->kind == MANTA_VALUE_TENSOR && rhs->storage == MANTA_DT_Q8 && rr == 2;
+    const bool rhs_f16 = rhs->kind == MANTA_VALUE_TENSOR && rhs->storage == MANTA_DT_F16 && rr == 2;
+    if (lhs_f16 && (rhs_f16 || rhs_q8)) {
+        char* e = nullptr;
+        const int rc = manta_rocm_matmul_f16(r.p->rt, (const uint16_t*)lhs->data, M, K, rhs->data,
+                                             rhs_q8 ? MANTA_ROCM_PROJ_Q8_COL : MANTA_ROCM_PROJ_F16,
+                                             rhs_q8 ? (const float*)rhs->scales : nullptr, N, (float*)out->data, &e);
+        if (rc != MANTA_ROCM_UNSUPPORTED) return r.abi(rc, e);
+        free(e);  // a shape the f16 GEMM does not take: the f32 path below
+    }
+    if (M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF || (M + 63) / 64 > 65535)
+        return r.unsupported("matmul shape beyond the device path");
+    Val a;
+    if (!r.f32_of(*lhs, &a, "matmul", false)) return false;
+    if (rhs_q8)
+        return r.hip(manta::launch_enc_gemm(1, (const float*)a.data, 0, rhs->data, (const float*)rhs->scales, 0,
+                                            (float*)out->data, 0, (int)M, (int)N, (int)K, 1, r.s),
+                     "matmul");
+    Val b;
+    if (!r.f32_of(*rhs, &b, "matmul", false)) return false;
+    if (rr == 2)
+        return r.hip(manta::launch_enc_gemm(0, (const float*)a.data, 0, b.data, nullptr, 0, (float*)out->data, 0,
+                                            (int)M, (int)N, (int)K, 1, r.s),
+                     "matmul");
+    const int64_t B = lhs->shape[0], Mb = lhs->shape[1];
+    if (B > 65535 || (Mb + 63) / 64 > 65535) return r.unsupported("batched matmul shape beyond the device path");
+    return r.hip(manta::launch_enc_gemm(0, (const float*)a.data, Mb * K, b.data, nullptr, K * N, (float*)out->data,
+                                        Mb * N, (int)Mb, (int)N, (int)K, (int)B, r.s),
+                 "matmul");
 }
 
 // Finds the fused score + top-k pairs of an entry (see the file comment).
@@ -831,15 +961,25 @@ bool run_entry(Run& r) {
             if (s.inputs.size() != 1 || s.outputs.size() != 1) {
                 ok = r.fail("dequant step " + q(s.name) + " expects 1 input and 1 output");
             } else {
+                // the reference relabels a clone f16 (tensor_ops.go:416-428):
+                // dense values pass as they are (a q8 tensor stays codes +
+                // column scales until a step needs its f32 values), gathered
+                // q8 rows become their f32 products
                 Val* in = nullptr;
                 ok = r.tensor(s.inputs[0], &in);
-                if (ok && in->kind != MANTA_VALUE_TENSOR)
+                Val v;
+                if (ok && in->kind == MANTA_VALUE_TENSOR) {
+                    v = *in;
+                    dispatch = "alias";
+                } else if (ok && in->kind == MANTA_VALUE_ROWS && in->storage == MANTA_DT_Q8) {
+                    ok = r.f32_of(*in, &v, "dequant", false);
+                    dispatch = "hip:dequant";
+                } else if (ok) {
                     ok = r.unsupported("dequant of " + in->dtype + " values is not offered by the rocm executor");
+                }
                 if (ok) {
-                    Val v = *in;
                     v.dtype = "f16";
                     values.push_back(v);
-                    dispatch = "alias";
                 }
             }
         } else if (s.kind == "launch_kernel") {
@@ -897,9 +1037,14 @@ bool run_entry(Run& r) {
                     dispatch = "hip:" + k->name;
                 }
             }
+        } else if (s.kind == "transpose") {
+            Val out;
+            ok = step_transpose(r, s, &out);
+            values.push_back(out);
+            dispatch = "hip:transpose";
         } else if (s.kind == "return") {
             dispatch = "return";
-        } else if (s.kind == "transpose" || s.kind == "kv_read" || s.kind == "kv_write" || s.kind == "conv2d" ||
+        } else if (s.kind == "kv_read" || s.kind == "kv_write" || s.kind == "conv2d" ||
                    s.kind == "conv2d_transpose" || s.kind == "gdn" || s.kind == "igdn" ||
                    s.kind == "turboquant_encode" || s.kind == "turboquant_decode" ||
                    s.kind == "cross_entropy_factorized" || s.kind == "mse_loss" || s.kind == "ms_ssim_loss" ||
@@ -987,8 +1132,10 @@ int manta_rocm_program_supports(const MantaRocmProgram* p, const char* entry, ch
     const EntryPoint* en = manta_mod::find_entry(p->m, name);
     if (!en) return set_err(err, MANTA_ROCM_ERROR, "unknown entrypoint " + q(name));
     static const std::set<std::string> steps = {"alias", "gather", "pack_candidates", "matmul", "topk",
-                                                "dequant", "launch_kernel", "return"};
-    static const std::set<std::string> ops = {"normalize", "rmsnorm", "mean_pool", "dot", "cosine", "l2_distance"};
+                                                "dequant", "transpose", "launch_kernel", "return"};
+    static const std::set<std::string> ops = {"normalize", "rmsnorm", "mean_pool", "dot", "cosine", "l2_distance",
+                                              "softmax", "layernorm", "gelu", "binary_add", "binary_sub",
+                                              "binary_mul", "binary_div"};
     for (const auto& s : p->m.steps) {
         if (s.entry != name) continue;
         if (!steps.count(s.kind))

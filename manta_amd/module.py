@@ -127,6 +127,18 @@ class Docs:
         return (self.cands.n, self.cands.d) if self.rank == 2 else (self.cands.sets, self.cands.n, self.cands.d)
 
 
+class Q8Columns:
+    """A q8 matrix value: int8 codes [k, n] with an f32 scale per column (a
+    reference per-tensor grid is one scale repeated); uploaded on first use."""
+
+    def __init__(self, codes: np.ndarray, col_scales: np.ndarray, dtype: str = "q8"):
+        self.codes = np.ascontiguousarray(codes, dtype=np.int8)
+        self.scales = np.ascontiguousarray(col_scales, dtype=np.float32)
+        if self.codes.ndim < 1 or self.scales.shape != (self.codes.shape[-1],):
+            raise ValueError("q8 columns: codes [..., n] and n scales expected")
+        self.dtype = dtype
+
+
 class Program:
     """An artifact loaded on a runtime (MantaRocmProgram*)."""
 
@@ -162,6 +174,18 @@ class Program:
                 val.shape[i] = s
             val.candidates = v.cands.handle.value
             keep.append(v)
+            return val
+        if isinstance(v, Q8Columns):
+            codes, scales = self.rt.to_device(v.codes), self.rt.to_device(v.scales)
+            keep.extend([codes, scales])
+            val.kind = TENSOR
+            val.storage = Q8
+            val.dtype = DTYPE_CODES[v.dtype]
+            val.rank = v.codes.ndim
+            for i, s in enumerate(v.codes.shape):
+                val.shape[i] = s
+            val.data = codes.addr
+            val.scales = scales.addr
             return val
         if isinstance(v, DeviceArray):
             dev, arr_dtype, shape = v, v.dtype, v.shape

@@ -41,7 +41,7 @@ def artifact_type(t):
 
 
 # expression trees: ("id", name) | ("call", callee, [args]) | ("matmul", [a, b])
-# | ("topk", arg, k)
+# | ("topk", arg, k) | ("bin", op, a, b)
 def ID(n):
     return ("id", n)
 
@@ -58,15 +58,39 @@ def TOPK(a, k):
     return ("topk", a, k)
 
 
+def ADD(a, b):
+    return ("bin", "+", a, b)
+
+
+BIN_NAMES = {"+": "add", "-": "sub", "*": "mul", "/": "div"}
+
+
+def expr_name(e):
+    """exprName (compiler.go:1471-1486)."""
+    if e[0] == "id":
+        return e[1]
+    if e[0] == "call":
+        return e[1]
+    if e[0] == "matmul":
+        return "matmul"
+    if e[0] == "topk":
+        return "topk"
+    return expr_name(e[2]) + "_" + BIN_NAMES[e[1]] + "_" + expr_name(e[3])
+
+
 def hints_for(name, ops):
     h = {"tile": [128], "vector_width": 4, "subgroup": False, "memory": "device_local"}
     for op in ops:
-        if op in ("normalize", "rmsnorm", "layernorm"):
+        if op == "softmax":
+            h.update(tile=[64], vector_width=1, subgroup=True, memory="workgroup_local")
+        elif op in ("normalize", "rmsnorm", "layernorm"):
             h.update(tile=[128], vector_width=4, subgroup=True, memory="workgroup_local")
         elif op in ("dot", "cosine", "l2_distance"):
             h.update(tile=[128], vector_width=4, subgroup=True, memory="workgroup_local")
         elif op == "mean_pool":
             h.update(tile=[64], vector_width=1, subgroup=True, memory="workgroup_local")
+        elif op.startswith("binary_"):
+            h.update(tile=[128], vector_width=4)
     if "norm" in name:
         h["subgroup"] = True
     return h
@@ -76,12 +100,16 @@ REDUCE_OPS = {"normalize", "rmsnorm", "layernorm", "softmax", "dot", "cosine", "
 
 
 def make_kernel(name, inputs, output_type, ops):
-    """ops: [(op, [input names], output)]; a return of the last output."""
+    """ops: [(op, [input names], output, attributes)]; a return of the last
+    output."""
     hints = hints_for(name, [o[0] for o in ops])
     body = []
-    for op, ins, out in ops:
-        body.append({"kind": "reduce" if op in REDUCE_OPS else "pointwise", "name": out, "op": op,
-                     "inputs": ins, "outputs": [out]})
+    for op, ins, out, attrs in ops:
+        o = {"kind": "reduce" if op in REDUCE_OPS else "pointwise", "name": out, "op": op, "inputs": ins,
+             "outputs": [out]}
+        if attrs:
+            o["attributes"] = dict(sorted(attrs.items()))
+        body.append(o)
     body.append({"kind": "return", "op": "return", "outputs": [ops[-1][2]]})
     tile = lambda v: "[" + ",".join(str(x) for x in v) + "]"
     meta = {"tile": tile(hints["tile"]), "tile_2d": "[]", "vector_width": str(hints["vector_width"]),
@@ -122,7 +150,7 @@ class Lowering:
 
     def kernel(self, name, inputs, result_type, ops):
         # a declared kernel: its body lowered with output "result"
-        k = make_kernel(name, inputs, result_type, ops)
+        k = make_kernel(name, inputs, result_type, [o + ({},) for o in ops])
         self.kernels.append(k)
         self.user_kernels[name] = result_type
 
@@ -142,32 +170,47 @@ class Lowering:
         if not any(x["name"] == k["name"] for x in self.kernels):
             self.kernels.append(k)
 
-    def plan(self, expr, out, env, steps):
+    def type_of(self, expr, env):
+        """inferExprType (compiler.go:1821-...): no steps, no buffers."""
+        return self.plan(expr, "", env, [], dry=True)
+
+    def plan(self, expr, out, env, steps, dry=False):
+        """inferExprPlan / inferCallPlan: appends the steps, returns the type."""
         kind = expr[0]
         if kind == "id":
             t = env[expr[1]]
-            if out and out != expr[1]:
+            if out and out != expr[1] and not dry:
                 steps.append({"kind": "alias", "name": out, "inputs": [expr[1]], "outputs": [out]})
                 self.buffer(out, t)
             return t
-        if kind == "topk":
-            arg = self.arg(expr[1], out, "topk", 0, env, steps)
-            st = env[arg] if isinstance(arg, str) else arg
-            at = env[arg]
-            k = expr[2]
-            if len(at["shape"]) == 1:
-                t = T("i32", str(k))
-            else:
-                t = T("i32", at["shape"][0], str(k))
-            steps.append({"kind": "topk", "name": "topk", "inputs": [arg], "outputs": [out] if out else [],
-                          "attributes": {"k": str(k)}})
-            if out:
+        if kind == "bin":
+            t = self.type_of(expr[2], env)
+            if out and not dry:
+                name = "binary_" + BIN_NAMES[expr[1]]
+                steps.append({"kind": "launch_kernel", "name": name, "kernel": name,
+                              "inputs": [expr_name(expr[2]), expr_name(expr[3])], "outputs": [out]})
                 self.buffer(out, t)
+                ins = [("lhs", self.type_of(expr[2], env)), ("rhs", self.type_of(expr[3], env))]
+                self.add_kernel(make_kernel(name, ins, t, [(name, ["lhs", "rhs"], "result", {"operator": expr[1]})]))
+            return t
+        if kind == "topk":
+            at = self.type_of(expr[1], env)
+            arg = self.arg(expr[1], out, "topk", 0, env, steps, dry)
+            k = expr[2]
+            t = T("i32", str(k)) if len(at["shape"]) == 1 else T("i32", at["shape"][0], str(k))
+            if not dry:
+                steps.append({"kind": "topk", "name": "topk", "inputs": [arg], "outputs": [out] if out else [],
+                              "attributes": {"k": str(k)}})
+                if out:
+                    self.buffer(out, t)
             return t
         callee = expr[1] if kind == "call" else "matmul"
         args = expr[2] if kind == "call" else expr[1]
         types = [self.type_of(a, env) for a in args]
-        names = [self.arg(a, out, callee, i, env, steps) for i, a in enumerate(args)]
+        names = [self.arg(a, out, callee, i, env, steps, dry) for i, a in enumerate(args)]
+        step = {"kind": "launch_kernel", "name": callee, "kernel": callee, "inputs": names,
+                "outputs": [out] if out else []}
+        kernel = None
         if kind == "matmul":
             l, r = types
             shape = []
@@ -175,8 +218,19 @@ class Lowering:
                 shape = [l["shape"][0], r["shape"][1]]
             if len(l["shape"]) == 3 and len(r["shape"]) == 2:
                 shape = [l["shape"][0], l["shape"][1], r["shape"][1]]
+            if len(l["shape"]) == 3 and len(r["shape"]) == 3:
+                shape = [l["shape"][0], l["shape"][1], r["shape"][2]]
             t = T(l["dtype"], *shape)
-            steps.append({"kind": "matmul", "name": "matmul", "inputs": names, "outputs": [out] if out else []})
+            step = {"kind": "matmul", "name": "matmul", "inputs": names, "outputs": step["outputs"]}
+        elif callee == "transpose":
+            x = types[0]
+            shape = []
+            if len(x["shape"]) == 2:
+                shape = [x["shape"][1], x["shape"][0]]
+            if len(x["shape"]) == 3:
+                shape = [x["shape"][0], x["shape"][2], x["shape"][1]]
+            t = T(x["dtype"], *shape)
+            step = {"kind": "transpose", "name": "transpose", "inputs": names, "outputs": step["outputs"]}
         elif callee == "gather":
             tb, ix = types
             shape = []
@@ -192,7 +246,7 @@ class Lowering:
             if len(tb["shape"]) == 3 and len(ix["shape"]) == 2:
                 shape = [ix["shape"][0], ix["shape"][1], tb["shape"][2]]
             t = T(tb["dtype"], *shape)
-            steps.append({"kind": "gather", "name": "gather", "inputs": names, "outputs": [out] if out else []})
+            step = {"kind": "gather", "name": "gather", "inputs": names, "outputs": step["outputs"]}
         elif callee == "pack_candidates":
             ids, sc, docs = types
             shape = []
@@ -201,8 +255,11 @@ class Lowering:
             if len(ids["shape"]) == 2 and len(sc["shape"]) == 2 and len(docs["shape"]) == 3:
                 shape = list(docs["shape"])
             t = PACK(*shape)
-            steps.append({"kind": "pack_candidates", "name": "pack_candidates", "inputs": names,
-                          "outputs": [out] if out else []})
+            step = {"kind": "pack_candidates", "name": "pack_candidates", "inputs": names,
+                    "outputs": step["outputs"]}
+        elif callee == "dequant":
+            t = T("f16", *types[0]["shape"])
+            step = {"kind": "dequant", "name": "dequant", "inputs": names, "outputs": step["outputs"]}
         elif callee == "mean_pool":
             x = types[0]
             shape = []
@@ -211,9 +268,7 @@ class Lowering:
             if len(x["shape"]) == 3:
                 shape = [x["shape"][0], x["shape"][2]]
             t = T(x["dtype"], *shape)
-            steps.append({"kind": "launch_kernel", "name": "mean_pool", "kernel": "mean_pool", "inputs": names,
-                          "outputs": [out] if out else []})
-            self.add_kernel(self.builtin(callee, args, types, t))
+            kernel = self.builtin(callee, args, types, t)
         elif callee in ("dot", "cosine", "l2_distance"):
             q, d = types
             shape = []
@@ -222,15 +277,16 @@ class Lowering:
             if len(q["shape"]) == 2 and len(d["shape"]) == 3:
                 shape = [q["shape"][0], d["shape"][1]]
             t = T("f32", *shape)
-            steps.append({"kind": "launch_kernel", "name": callee, "kernel": callee, "inputs": names,
-                          "outputs": [out] if out else []})
-            self.add_kernel(self.builtin(callee, args, types, t))
+            kernel = self.builtin(callee, args, types, t)
         else:
             t = types[0]
-            steps.append({"kind": "launch_kernel", "name": callee, "kernel": callee, "inputs": names,
-                          "outputs": [out] if out else []})
             if callee not in self.user_kernels:
-                self.add_kernel(self.builtin(callee, args, types, t))
+                kernel = self.builtin(callee, args, types, t)
+        if dry:
+            return t
+        steps.append(step)
+        if kernel:
+            self.add_kernel(kernel)
         if out:
             self.buffer(out, t)
         for s in steps:
@@ -239,20 +295,17 @@ class Lowering:
         return t
 
     def builtin(self, callee, args, types, out_type):
-        names = [a[1] if a[0] == "id" else "input%d" % i for i, a in enumerate(args)]
-        return make_kernel(callee, list(zip(names, types)), out_type, [(callee, names, "result")])
+        names = [expr_name(a) for a in args]
+        attrs = {"axis": "-1"} if callee == "softmax" else {}
+        return make_kernel(callee, list(zip(names, types)), out_type, [(callee, names, "result", attrs)])
 
-    def type_of(self, expr, env):
-        if expr[0] == "id":
-            return env[expr[1]]
-        return self.plan(expr, "", dict(env), [])
-
-    def arg(self, expr, out, callee, index, env, steps):
+    def arg(self, expr, out, callee, index, env, steps, dry=False):
+        """materializeCallArg (compiler.go:2069-2093)."""
         if expr[0] == "id":
             return expr[1]
-        name = "%s_arg%d_%s" % (out or callee, index, "")
-        self.plan(expr, name, env, steps)
-        env[name] = self.type_of(expr, env)
+        name = "%s_arg%d_%s" % (out or callee, index, expr_name(expr))
+        if not dry:
+            env[name] = self.plan(expr, name, env, steps)
         return name
 
     def pipeline(self, name, inputs, results, body):
@@ -457,6 +510,47 @@ def modules():
             ("let", "batch_projected", MATMUL(ID("batch_hidden"), ID("projection"))),
             ("let", "batch_normalized", CALL("normalize", ID("batch_projected"))),
             ("return", [pool("batch_normalized")])])
+        out[name] = lw.module()
+
+    # examples/encoder_trainable_q8.manta and encoder_trainable_q8x2.manta
+    for name, layers in (("encoder_trainable_q8", 1), ("encoder_trainable_q8x2", 2)):
+        lw = Lowering(name, 9)
+        shapes = {"token_embedding": ("V", "D"), "attn_q": ("D", "D"), "attn_k": ("D", "D"), "attn_v": ("D", "D"),
+                  "attn_o": ("D", "D"), "ffn_up": ("D", "H"), "projection": ("H", "D")}
+        for pname, shp in shapes.items():
+            lw.param(pname, T("q8", *shp), "weights/" + pname, trainable=True)
+        for entry, single in (("embed_pooled", True), ("embed_pooled_batch", False)):
+            lead = ("T",) if single else ("B", "T")
+            body = [("let", "hidden_q", CALL("gather", ID("token_embedding"), ID("tokens"))),
+                    ("let", "hidden", CALL("dequant", ID("hidden_q"))),
+                    ("let", "wq_f", CALL("dequant", ID("attn_q"))),
+                    ("let", "wk_f", CALL("dequant", ID("attn_k"))),
+                    ("let", "wv_f", CALL("dequant", ID("attn_v"))),
+                    ("let", "wo_f", CALL("dequant", ID("attn_o"))),
+                    ("let", "ffn_up_f", CALL("dequant", ID("ffn_up"))),
+                    ("let", "projection_f", CALL("dequant", ID("projection")))]
+            x = "hidden"
+            for layer in range(1, layers + 1):
+                sfx = "" if layers == 1 else str(layer)
+                v = lambda n: n + sfx
+                body += [("let", v("q"), MATMUL(ID(x), ID("wq_f"))),
+                         ("let", v("k"), MATMUL(ID(x), ID("wk_f"))),
+                         ("let", v("v"), MATMUL(ID(x), ID("wv_f"))),
+                         ("let", v("kt"), CALL("transpose", ID(v("k")))),
+                         ("let", v("scores"), MATMUL(ID(v("q")), ID(v("kt")))),
+                         ("let", v("probs"), CALL("softmax", ID(v("scores")))),
+                         ("let", v("mixed"), MATMUL(ID(v("probs")), ID(v("v")))),
+                         ("let", v("attended"), MATMUL(ID(v("mixed")), ID("wo_f"))),
+                         ("let", v("attn_hidden"), CALL("layernorm", ADD(ID(v("attended")), ID(x)))),
+                         ("let", v("ffn_hidden"), MATMUL(ID(v("attn_hidden")), ID("ffn_up_f"))),
+                         ("let", v("activated"), CALL("gelu", ID(v("ffn_hidden")))),
+                         ("let", v("projected"), MATMUL(ID(v("activated")), ID("projection_f"))),
+                         ("let", v("encoded"), CALL("layernorm", ADD(ID(v("projected")), ID(v("attn_hidden")))))]
+                x = v("encoded")
+            body += [("let", "normalized", CALL("normalize", ID(x))),
+                     ("return", [CALL("mean_pool", ID("normalized"), ID("attention_mask"))])]
+            lw.pipeline(entry, [("tokens", T("i32", *lead)), ("attention_mask", T("i32", *lead))],
+                        [("result", T("f16", *(("D",) if single else ("B", "D"))))], body)
         out[name] = lw.module()
     return out
 

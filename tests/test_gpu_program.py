@@ -333,19 +333,20 @@ def test_return_of_unproduced_value(rt):
 def test_supports_and_unsupported_steps(rt):
     for name in ["tiny_score", "tiny_rerank", "tiny_select", "tiny_retrieve", "tiny_candidates",
                  "tiny_batch_candidates", "tiny_packed_candidates", "packed_batch", "score_bundle", "tiny_embed",
-                 "tiny_embed_pooled", "embed_masked_pooled", "ref_packed", "ref_demo"]:
+                 "tiny_embed_pooled", "embed_masked_pooled", "ref_packed", "ref_demo", "encoder_trainable_q8",
+                 "encoder_trainable_q8x2"]:
         p = program(rt, name)
         for en in fixture(name)["entry_points"]:
             p.supports(en["name"])
     obj = fixture("tiny_embed")
-    obj["kernels"][0]["body"][0]["op"] = "softmax"
+    obj["kernels"][0]["body"][0]["op"] = "rope"
     p = program(rt, obj)
-    with pytest.raises(Unsupported, match='op "softmax" is not offered'):
+    with pytest.raises(Unsupported, match='op "rope" is not offered'):
         p.supports("embed")
     obj = fixture("tiny_embed")
-    obj["steps"][1]["kind"] = "transpose"
+    obj["steps"][1]["kind"] = "kv_read"
     p = program(rt, obj)
-    with pytest.raises(Unsupported, match='kind "transpose"'):
+    with pytest.raises(Unsupported, match='kind "kv_read"'):
         p.supports("embed")
 
 
@@ -368,3 +369,47 @@ def test_program_outputs_reused_across_runs(rt):
             first = out
         if i == 2:
             assert out["ids"].tolist() == first["ids"].tolist()
+
+
+def _encoder_case(seed, b, t, vocab, d, h):
+    rng = np.random.default_rng(seed)
+    tokens = rng.integers(0, vocab, size=(b, t), dtype=np.int32)
+    lengths = rng.integers(1, t + 1, size=b)
+    mask = (np.arange(t)[None, :] < lengths[:, None]).astype(np.int32)
+    table = (rng.standard_normal((vocab, d)) * 0.5).astype(np.float32)
+    tcodes, tscales = orc.pack_q8_rows(table)
+    ws = []
+    for s in [(d, d), (d, d), (d, d), (d, d), (d, h), (h, d)]:
+        w = (rng.standard_normal(s) / np.sqrt(s[0])).astype(np.float32)
+        cs = (np.abs(w).max(0) / 127.0).astype(np.float32)
+        cs[cs == 0] = 1.0
+        ws.append((np.clip(np.round(w / cs), -127, 127).astype(np.int8), cs))
+    return tokens, mask, tcodes, tscales, ws
+
+
+@pytest.mark.parametrize("name,layers", [("encoder_trainable_q8", 1), ("encoder_trainable_q8x2", 2)])
+def test_encoder_entries_run_step_by_step(rt, name, layers):
+    """The encoder examples through the executor: gather of q8 token rows,
+    dequant, q/k/v GEMMs, transpose, batched attention products, softmax,
+    residual add + layernorm, gelu, normalize, masked mean pool -- every step
+    on device; within the encoder's bar (cosine >= 0.9999) of the oracle."""
+    from manta_amd.module import Q8Columns
+    b, t, vocab, d, h = 4, 12, 60, 64, 128
+    tokens, mask, tcodes, tscales, ws = _encoder_case(51 + layers, b, t, vocab, d, h)
+    p = program(rt, name)
+    p.bind("token_embedding", Docs(rt.bind_q8(tcodes, tscales), "q8"))
+    for pname, (codes, cs) in zip(["attn_q", "attn_k", "attn_v", "attn_o", "ffn_up", "projection"], ws):
+        p.bind(pname, Q8Columns(codes, cs))
+    p.supports("embed_pooled_batch")
+    got = p.run("embed_pooled_batch", {"tokens": tokens, "attention_mask": mask})["result"]
+    table = (tcodes.astype(np.float32) * tscales[:, None]).astype(np.float32)
+    wf = [(c.astype(np.float32) * s[None, :]).astype(np.float32) for c, s in ws]
+    want = orc.encoder_pooled(tokens, mask, table, *wf, layers=layers)
+    cos = (got * want).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(want, axis=1))
+    assert cos.min() >= 0.9999, cos.min()
+    assert np.abs(got - want).max() < 1e-3
+    # the single-sequence entry on the first sequence
+    one = p.run("embed_pooled", {"tokens": tokens[0], "attention_mask": mask[0]})["result"]
+    np.testing.assert_allclose(one, got[0], rtol=0, atol=1e-5)
+    kinds = {k for k, _, _ in p.trace()}
+    assert {"transpose", "dequant", "matmul", "launch_kernel"} <= kinds
