@@ -2,23 +2,30 @@
 // scores (E8 query codes), on v_mfma_i32_16x16x64_i8.
 //
 // mq8_scan_kernel: workgroup = 8 waves (512 threads, one workgroup per CU),
-// grid = (row ranges, groups of 512 queries).  Each wave keeps 64 queries'
-// codes resident as the A operand (4 blocks of 16 queries x PITCH bytes).
-// Candidate rows stream through LDS in chunks of CH rows, moved by
-// direct-to-LDS loads NBUF-1 chunks ahead of their use; every wave reads all
-// rows of a chunk as B fragments (16 rows x 64 bytes), so each candidate
-// byte is fetched from L2 once per 512 queries.  A row pair (two 16-row
-// blocks) is eight independent accumulator chains of PITCH/64 MFMAs each.
+// grid = (row ranges, groups of 512 / WS queries).  Each wave keeps 64
+// queries' codes resident as the A operand (4 blocks of 16 queries x PITCH
+// bytes).  Candidate rows stream through LDS in chunks of 64*WS rows, moved
+// by direct-to-LDS loads NBUF-1 chunks ahead of their use; every wave reads
+// 64 rows of a chunk (two row pairs) as B fragments (16 rows x 64 bytes), so
+// each candidate byte is fetched from L2 once per 512 / WS queries.  A row
+// pair (two 16-row blocks) is eight independent accumulator chains of
+// PITCH/64 MFMAs each.
 //
 // 16x16 output layout: lane l holds D[4*(l/16) + r][l%16], r = 0..3, i.e.
 // queries 16*qb + 4*(l/16) + r of its A blocks against row l%16 of each B
-// block.  The filter is one fma per (query, row): scale*acc - bound, with
-// the bound loosened past the exact test's, reduced by v_max3 over a query
-// block's 8 pairs per lane; only a block with a passing lane takes the
-// exact f32 test p = fmul_rn(scale, acc) against the bound.  A pair that
-// passes goes to its region as (bits of p) << 32 | row: the division and the
-// key are left to the select kernel, where every lane has one.  Row scales
-// must be finite (the runtime routes other candidates to kernels_mq.hip).
+// block.  A wave orders its 64 queries by their current bound before the
+// scan (slot L of the wave holds the L-th), so a lane's 4 queries have
+// nearly equal bounds, and the pre-filter takes four VALU instructions per
+// lane, query block and 16-row block: the best of the lane's 4
+// accumulators, converted, times the row scale, less the loosest of the 4
+// bounds (loosened past the exact test's).  The filter of a row pair runs
+// under the MFMAs of the wave's next pair (a chunk's second pair under the
+// next chunk's first).  Only a query block with a passing lane takes the
+// exact f32 test p = fmul_rn(scale, acc) against each query's bound.  A
+// pair that passes goes to its query's region as (bits of p) << 32 | row:
+// the division and the key are left to the select kernel, where every lane
+// has one.  Row scales must be finite and not negative (the runtime routes
+// other candidates to kernels_mq.hip).
 //
 // The LDS tile stores row r's 16-byte column c at column c ^ ((r >> 1) & 7)
 // (PITCH is a multiple of 128, so a row holds a multiple of 8 columns): the
@@ -36,13 +43,12 @@ namespace {
 constexpr int kMq8Waves = 8;
 constexpr int kMq8Threads = kMq8Waves * 64;
 constexpr int kMq8QG = kMq8Waves * 64;  // queries per workgroup
-constexpr int kMq8RB = 4;               // 16-row blocks per chunk
-constexpr int kMq8CH = kMq8RB * 16;     // rows per chunk
+constexpr int kMq8CH = 64;             // rows per chunk and wave group (two row pairs per wave)
 
 // chunk tiles (with their row scales) in the LDS the static arrays leave:
 // those take 24 bytes per query plus about 2 KB
-constexpr int mq8_nbuf(int tile, int qg) {
-    int n = (160 * 1024 - qg * 24 - 2560) / (tile + kMq8CH * 4);
+constexpr int mq8_nbuf(int tile, int qg, int ch) {
+    int n = (160 * 1024 - qg * 24 - 2560) / (tile + ch * 4);
     return n > 6 ? 6 : (n < 2 ? 2 : n);
 }
 }  // namespace
@@ -50,23 +56,26 @@ constexpr int mq8_nbuf(int tile, int qg) {
 template <int KS64, bool SMALL, int WS, bool SHADOW>
 __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))) void mq8_scan_kernel(MqArgs a) {
     constexpr int PITCH = KS64 * 64;
-    constexpr int CH = kMq8CH;
+    constexpr int CH = kMq8CH * WS;                      // rows per chunk
+    constexpr int PPW = CH / 32 / WS;                    // row pairs per wave and chunk
     constexpr int TILE = CH * PITCH;                     // bytes per chunk tile
     constexpr int LPW = TILE / 1024 / kMq8Waves;         // 16-byte direct-to-LDS loads per wave per chunk
     static_assert(LPW * 1024 * kMq8Waves == TILE, "chunk tile must split evenly over the waves");
+    static_assert(WS == 1 || WS == 2, "one or two wave groups");
     constexpr int QG = kMq8QG / WS;          // queries per workgroup
-    constexpr int NBUF = mq8_nbuf(TILE, QG);
+    constexpr int NBUF = mq8_nbuf(TILE, QG, CH);
     static_assert((NBUF - 2) * (LPW + 1) <= 63, "vmcnt range");
     constexpr int NFW = QG / 64;             // waves per query group
-    static_assert(kMq8RB == 2 * 2 && (WS == 1 || WS == 2), "row pairs split over WS wave groups");
+    static_assert(PPW == 2, "a wave's two row pairs alternate between two accumulator sets");
 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* tiles = smem;                               // [NBUF][TILE]
     float* cscale = (float*)(smem + NBUF * TILE);        // [NBUF][CH] row scales
+    // query state by slot: slot lw + L of a wave holds query qmap_s[lw + L]
     __shared__ uint64_t tau_s[QG];
     __shared__ __attribute__((aligned(16))) float bnd_s[QG];
-    __shared__ __attribute__((aligned(16))) float qa_s[QG];
-    __shared__ __attribute__((aligned(16))) float pre_s[QG];  // pre-filter bounds (loosened further)
+    __shared__ int qmap_s[QG];
+    __shared__ float pmin_s[QG / 4];  // loosest pre-filter bound of each 4 consecutive slots
     __shared__ int cnt_s[QG];
     __shared__ uint64_t flags[2][NFW];
     __shared__ RadixShared ss;
@@ -79,7 +88,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     const int g = lane >> 4, j = lane & 15;
     const int q0 = blockIdx.y * QG;
     const int lw = (wave % NFW) * 64;  // this wave's first workgroup-local query
-    const int rp0 = (wave / NFW) * 2;  // this wave's first row pair of a chunk
+    const int rw = (wave / NFW) * (CH / WS);  // this wave's first row of a chunk (PPW row pairs)
 
     uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.nq * a.rc;
     const int64_t r0 = a.row_begin + (int64_t)blockIdx.x * a.rows_per_wg;
@@ -101,6 +110,8 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     }
     const uint32_t tbase = lds_addr(tiles);
     const uint32_t sbase = lds_addr(cscale);
+    // the last WS waves also load the chunk's row scales (64 each)
+    const int sw = wave_s - (kMq8Waves - WS);
     auto issue_chunk = [&](int64_t c0, int buf) {
         const int8_t* base = a.codes + c0 * PITCH;
         const int left = (int)(r1 - c0 < CH ? r1 - c0 : CH);
@@ -109,11 +120,11 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         const uint32_t dst = __builtin_amdgcn_readfirstlane(tbase + buf * TILE + wave_s * LPW * 1024);
 #pragma unroll
         for (int i = 0; i < LPW; i++) lds_load16(base + (soff[i] < lim ? soff[i] : lim), dst + i * 1024);
-        // the chunk's row scales (only the exact test reads them): one more
-        // 4-byte load per lane, by the last wave
-        if (wave_s == kMq8Waves - 1)
-            lds_load4(a.scales + c0 + (lane < left ? lane : left - 1),
-                      __builtin_amdgcn_readfirstlane(sbase + buf * CH * 4));
+        if (sw >= 0) {
+            const int si = sw * 64 + lane;
+            lds_load4(a.scales + c0 + (si < left ? si : left - 1),
+                      __builtin_amdgcn_readfirstlane(sbase + buf * CH * 4 + sw * 256));
+        }
     };
     // the first chunks' loads go out first: the A fragments and the query
     // state load under them
@@ -121,29 +132,66 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     for (int b = 0; b < NBUF - 1; b++)
         if (r0 + b * CH < r1) issue_chunk(r0 + b * CH, b);
 
-    // A operand: 4 blocks of 16 queries, K steps of 64 bytes
+    // Each wave orders its 64 queries by their bound (a bitonic sort across
+    // the lanes): slot lw + L takes the L-th, so the 4 queries a lane filters
+    // together have nearly equal bounds.  Both wave groups of WS = 2 sort the
+    // same queries the same way.
+    auto bound_of = [&](int q) {
+        const QConst qc = a.qconst[q];
+        const uint64_t tk = a.tau[q];
+        return SHADOW ? shadow_bound(tk, a.qbound[2 * q], a.qbound[2 * q + 1], SMALL) : mq_bound<OP_DOT>(tk, qc, SMALL);
+    };
+    uint64_t skey;
+    {
+        const int q = q0 + lw + lane;
+        uint32_t ord = 0xFFFFFFFFu;  // missing queries go last
+        if (q < a.nq) {
+            const uint32_t u = __float_as_uint(bound_of(q));
+            ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+            ord = ord == 0xFFFFFFFFu ? 0xFFFFFFFEu : ord;
+        }
+        skey = ((uint64_t)ord << 32) | (uint32_t)lane;
+#pragma unroll
+        for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+            for (int jj = k >> 1; jj > 0; jj >>= 1) {
+                const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(skey >> 32), jj) << 32) |
+                                   (uint32_t)__shfl_xor((int)(uint32_t)skey, jj);
+                const bool keep_min = ((lane & jj) == 0) == ((lane & k) == 0);
+                skey = keep_min ? (o < skey ? o : skey) : (o > skey ? o : skey);
+            }
+    }
+    const int my_src = (int)(skey & 63);  // slot lw + lane holds query q0 + lw + my_src
+
+    // A operand: 4 blocks of 16 slots, K steps of 64 bytes
     v4i av[4][KS64];
 #pragma unroll
     for (int qb = 0; qb < 4; qb++) {
-        const int q = q0 + lw + qb * 16 + j;
+        const int q = q0 + lw + __shfl(my_src, qb * 16 + j);
         const bool ok = q < a.nq;
         const int8_t* src = a.qc8 + (int64_t)(ok ? q : 0) * PITCH + 16 * g;
 #pragma unroll
         for (int ks = 0; ks < KS64; ks++) av[qb][ks] = ok ? *(const v4i*)(src + ks * 64) : v4i{0, 0, 0, 0};
     }
 
-    for (int i = tid; i < QG; i += kMq8Threads) {
-        const int q = q0 + i;
+    // slot i = tid: the wave that owns slot i runs this thread
+    if (tid < QG) {
+        const int i = tid;
+        const int q = q0 + lw + my_src;
         const bool ok = q < a.nq;
-        const QConst qc = ok ? a.qconst[q] : QConst{1.0f, 0.0f, 0.0f, 0.0f};
-        const uint64_t tk = ok ? a.tau[q] : 0ull;
-        qa_s[i] = qc.a;
-        tau_s[i] = ok ? tk : ~0ull;
-        float b = SMALL ? -__builtin_inff() : __builtin_inff();
-        if (ok) b = SHADOW ? shadow_bound(tk, a.qbound[2 * q], a.qbound[2 * q + 1], SMALL) : mq_bound<OP_DOT>(tk, qc, SMALL);
+        tau_s[i] = ok ? a.tau[q] : ~0ull;
+        const float b = ok ? bound_of(q) : (SMALL ? -__builtin_inff() : __builtin_inff());
         bnd_s[i] = b;
-        pre_s[i] = SMALL ? loosen_up(bnd_s[i]) : loosen_down(bnd_s[i]);
+        qmap_s[i] = q;
         cnt_s[i] = 0;
+        float pre = SMALL ? loosen_up(b) : loosen_down(b);
+        // the loosest of 4 consecutive slots (lanes 4m .. 4m+3)
+#pragma unroll
+        for (int x = 1; x <= 2; x <<= 1) {
+            const float o = __shfl_xor(pre, x);
+            pre = SMALL ? fmaxf(pre, o) : fminf(pre, o);
+        }
+        if ((lane & 3) == 0) pmin_s[i >> 2] = pre;
     }
 
     __syncthreads();  // query state above is complete
@@ -151,14 +199,23 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     // fragments' first use in the loop
     __builtin_amdgcn_s_waitcnt(0);
 
-    // pre-filter bounds of a query block's 4 queries of this lane (one LDS read)
-    auto load_bq = [&](int qb, float (&b)[4]) {
-        const float4 b4 = *(const float4*)&pre_s[lw + qb * 16 + 4 * g];
-        b[0] = b4.x, b[1] = b4.y, b[2] = b4.z, b[3] = b4.w;
-    };
-    // pre-score of one (query, row): >= 0 unless the exact test must fail
-    auto pre = [&](float scale, int acc, float b) {
-        return SMALL ? __fmaf_rn(-scale, (float)acc, b) : __fmaf_rn(scale, (float)acc, -b);
+    // Pre-filter of query block qb of a row pair: per 16-row block, the
+    // lane's best accumulator over its 4 queries, scaled (row scales are >= 0,
+    // so that is the best score of the row's 4 pairs), less the loosest bound
+    // of those queries (read where it is used, one LDS read); pm[qb] >= 0
+    // unless every exact test of the block's pairs in this lane must fail
+    // (fma rounds monotonically in each operand).  The slot order keeps the
+    // 4 bounds close, so this is nearly as tight as a test per query.
+    auto prefilter = [&](const v4i (&acc)[2][4], const float (&sc)[2], float (&pm)[4], int qb) {
+        const float pb = pmin_s[((lw + qb * 16) >> 2) + g];
+        float v[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const v4i x = acc[h][qb];
+            const int e = SMALL ? min(min(x[0], x[1]), min(x[2], x[3])) : max(max(x[0], x[1]), max(x[2], x[3]));
+            v[h] = SMALL ? __fmaf_rn(-sc[h], (float)e, pb) : __fmaf_rn(sc[h], (float)e, -pb);
+        }
+        pm[qb] = fmaxf(v[0], v[1]);
     };
 
     // The pairs of one query block of a row pair that pass the exact test,
@@ -188,30 +245,107 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
             for (int i = 1; i < 8; i++) p = b == i ? pv[i] : p;
             const int lq = lw + qb * 16 + 4 * g + (b & 3);
             const int pos = atomicAdd(&cnt_s[lq], 1);
-            wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = dot_pair(p, (uint32_t)(rb0 + (b >> 2) * 16 + j));
+            wreg[(uint32_t)(qmap_s[lq] * a.rc + pos)] = dot_pair(p, (uint32_t)(rb0 + (b >> 2) * 16 + j));
+        }
+    };
+    // Exact tests of the query blocks of a row pair whose pre-filter passed
+    // in some lane (rare once the bounds are tight).
+    auto check = [&](const v4i (&acc)[2][4], int64_t rb0, const float (&sc)[2], const float (&pm)[4]) {
+        if (__ballot(fmaxf(fmaxf(pm[0], pm[1]), fmaxf(pm[2], pm[3])) >= 0.0f)) {
+#pragma unroll
+            for (int qb = 0; qb < 4; qb++)
+                if (__ballot(pm[qb] >= 0.0f)) survivors(acc, qb, rb0, sc);
+        }
+    };
+    // B fragments of K step ks of the row pair at tile row row0
+    auto load_b = [&](v4i (&b)[2], const uint8_t* tile, int row0, int ks) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int row = row0 + h * 16 + j;
+            b[h] = *(const v4i*)(tile + row * PITCH + (((ks * 4 + g) ^ ((row >> 1) & 7)) * 16));
+        }
+    };
+    // MFMAs of the row pair at tile row row0 into acc (its first fragments
+    // already in bc), with the pre-filter of the other pair (oacc, osc)
+    // spread over the K steps: its VALU work issues while the matrix cores
+    // run.  B fragments are read one K step ahead, the last step reading the
+    // first fragments of the pair at next0 (if any) into bc (the scheduling
+    // barrier keeps the compiler from hoisting every step's reads, which
+    // would hold all 2*KS64 fragments in registers).
+    auto mfma_pair = [&](v4i (&acc)[2][4], v4i (&bc)[2], const uint8_t* tile, int row0, int next0,
+                         const v4i (&oacc)[2][4], const float (&osc)[2], float (&pm)[4]) {
+        v4i bn[2];
+#pragma unroll
+        for (int ks = 0; ks < KS64; ks++) {
+            if (ks + 1 < KS64) load_b(bn, tile, row0, ks + 1);
+            else if (next0 >= 0) load_b(bn, tile, next0, 0);
+#pragma unroll
+            for (int qb = 0; qb < 4; qb++)
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+                    acc[h][qb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[qb][ks], bc[h],
+                                                                       ks == 0 ? v4i{0, 0, 0, 0} : acc[h][qb], 0, 0, 0);
+            if (KS64 >= 4) {
+                if (ks < 4) prefilter(oacc, osc, pm, ks);
+            } else {
+                prefilter(oacc, osc, pm, 2 * ks);
+                prefilter(oacc, osc, pm, 2 * ks + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks + 1 < KS64 || next0 >= 0) {
+                bc[0] = bn[0];
+                bc[1] = bn[1];
+            }
         }
     };
 
+    // A wave's row pairs of a chunk alternate between the accumulator sets
+    // accs[0] and accs[1]; each pair's filter runs under the next pair's
+    // MFMAs, the chunk's last pair under the next chunk's first.  Before the
+    // first chunk accs[1] holds no pair: its NaN scales make every pre-filter
+    // value NaN, which no ballot passes (the filter stays unconditional, so
+    // the compiler keeps it among the MFMAs).
+    v4i accs[2][2][4];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int qb = 0; qb < 4; qb++) accs[1][h][qb] = v4i{0, 0, 0, 0};
+    float scs[2][2] = {{0.0f, 0.0f}, {__builtin_nanf(""), __builtin_nanf("")}};
+    int64_t rbs[2] = {r1, r1};  // first row of each set's pair
+    float pm[4];
+
     int buf = 0, par = 0;
     for (int64_t c0 = r0; c0 < r1; c0 += CH, buf = buf == NBUF - 1 ? 0 : buf + 1, par ^= 1) {
-        // Flag regions that might not take one more chunk of keys (a count
-        // read before the barrier may miss up to CH keys of the chunk other
-        // waves are filtering: margin of two chunks, rc >= k + 2*CH + 1).
+        // Flag regions that might not take 2.5 more chunks of keys.  Between
+        // two compactions (after the barriers of chunks c and c+1) each wave
+        // appends the pairs of PPW row pairs, the previous chunk's last and
+        // this chunk's others: one chunk of rows over the WS waves that share
+        // a query.  A count read here may miss up to one such window, the
+        // window up to the next compaction adds one chunk, and after the
+        // last chunk the pending last pairs add at most half a chunk.  The
+        // runtime sizes regions rc >= k + 2.5*CH, so a compacted region (k
+        // pairs) is never flagged again at once.
         if (wave < NFW) {
             const int i = wave * 64 + lane;
-            const uint64_t m = __ballot(cnt_s[i] > a.rc - 2 * CH);
+            const uint64_t m = __ballot(cnt_s[i] > a.rc - (5 * CH) / 2);
             if (lane == 0) flags[par][wave] = m;
         }
         // this wave's loads of chunk c are done once at most the loads of
         // the chunks issued after it are outstanding; the barrier extends
         // that to every wave, retires the previous chunk's reads of the tile
         // about to be refilled, and publishes the flags
-        // (the last wave issues one more load per chunk: the row scales)
-        if (wave == kMq8Waves - 1)
+        // (the scale-loading waves issue one more load per chunk)
+        if (sw >= 0)
             mq_wait_barrier<LPW + 1, NBUF - 2>((r1 - c0 - 1) / CH);
         else
             mq_wait_barrier<LPW, NBUF - 2>((r1 - c0 - 1) / CH);
         const int nbuf = buf == 0 ? NBUF - 1 : buf - 1;  // tile of chunk c+NBUF-1 (free now)
+        const uint8_t* tile = tiles + buf * TILE;
+        const float* cs = cscale + buf * CH;
+        // the first pair's first fragments go out with the flags' read (a
+        // compaction writes neither this tile nor the fragments)
+        v4i bc[2];
+        load_b(bc, tile, rw, 0);
         {
             bool any = false;
 #pragma unroll
@@ -223,20 +357,21 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                 uint64_t* spairs = skeys + a.rc;
                 for (int lq = 0; lq < QG; lq++) {
                     if (!((flags[par][lq >> 6] >> (lq & 63)) & 1)) continue;
-                    uint64_t* reg = wreg + (uint32_t)((q0 + lq) * a.rc);
+                    const int qx = qmap_s[lq];
+                    uint64_t* reg = wreg + (uint32_t)(qx * a.rc);
                     const int c = cnt_s[lq];
                     for (int i = tid; i < c; i += kMq8Threads) {
                         const uint64_t e = reg[i];
                         spairs[i] = e;
                         if (SHADOW) {
                             // the exact q4 score of the pair's row
-                            const int64_t q = q0 + lq;
+                            const int64_t q = qx;
                             const float sc = q4_exact_score(a.op, a.q4codes, a.q4scales, a.dnorm, a.dd, a.d,
                                                             (int64_t)(uint32_t)e, (const int*)(a.qhi + q * a.d),
                                                             (const int*)(a.qlo + q * a.d), a.qconst[q]);
                             skeys[i] = make_key(sc, (uint32_t)e, SMALL);
                         } else {
-                            skeys[i] = dot_pair_key(e, qa_s[lq], SMALL);
+                            skeys[i] = dot_pair_key(e, a.qconst[qx].a, SMALL);
                         }
                     }
                     if (tid == 0) {
@@ -260,10 +395,15 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                         cnt_s[lq] = a.k;
                         if (minkey > tau_s[lq]) {
                             tau_s[lq] = minkey;
-                            const int q = q0 + lq;
-                            bnd_s[lq] = SHADOW ? shadow_bound(minkey, a.qbound[2 * q], a.qbound[2 * q + 1], SMALL)
-                                               : mq_bound<OP_DOT>(minkey, a.qconst[q], SMALL);
-                            pre_s[lq] = SMALL ? loosen_up(bnd_s[lq]) : loosen_down(bnd_s[lq]);
+                            bnd_s[lq] = SHADOW ? shadow_bound(minkey, a.qbound[2 * qx], a.qbound[2 * qx + 1], SMALL)
+                                               : mq_bound<OP_DOT>(minkey, a.qconst[qx], SMALL);
+                            const int m0 = lq & ~3;
+                            float pre = SMALL ? loosen_up(bnd_s[m0]) : loosen_down(bnd_s[m0]);
+                            for (int x = 1; x < 4; x++) {
+                                const float o = SMALL ? loosen_up(bnd_s[m0 + x]) : loosen_down(bnd_s[m0 + x]);
+                                pre = SMALL ? fmaxf(pre, o) : fminf(pre, o);
+                            }
+                            pmin_s[lq >> 2] = pre;
                         }
                     }
                     __syncthreads();
@@ -271,57 +411,26 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
             }
         }
         if (c0 + (NBUF - 1) * CH < r1) issue_chunk(c0 + (NBUF - 1) * CH, nbuf);
-        const uint8_t* tile = tiles + buf * TILE;
+        // pair p into accs[p & 1], under which pair p-1 (the previous
+        // chunk's last for p = 0) is filtered
 #pragma unroll
-        for (int rp = rp0; rp < kMq8RB; rp += 2 * WS) {
-            // B fragments one K step ahead of their MFMAs (the scheduling
-            // barrier keeps the compiler from hoisting every step's reads,
-            // which would hold all 2*KS64 fragments in registers)
-            auto load_b = [&](v4i (&b)[2], int ks) {
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int row = (rp + h) * 16 + j;
-                    b[h] = *(const v4i*)(tile + row * PITCH + (((ks * 4 + g) ^ ((row >> 1) & 7)) * 16));
-                }
-            };
-            v4i acc[2][4];
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-#pragma unroll
-                for (int qb = 0; qb < 4; qb++) acc[h][qb] = v4i{0, 0, 0, 0};
-            v4i bc[2], bn[2];
-            load_b(bc, 0);
-#pragma unroll
-            for (int ks = 0; ks < KS64; ks++) {
-                if (ks + 1 < KS64) load_b(bn, ks + 1);
-#pragma unroll
-                for (int qb = 0; qb < 4; qb++)
-#pragma unroll
-                    for (int h = 0; h < 2; h++)
-                        acc[h][qb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[qb][ks], bc[h], acc[h][qb], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                bc[0] = bn[0];
-                bc[1] = bn[1];
-            }
-            // one fma per (query, row) and a running max (v_max3) per query block
-            const int64_t rb0 = c0 + rp * 16;
-            const float sc[2] = {cscale[buf * CH + rp * 16 + j], cscale[buf * CH + rp * 16 + 16 + j]};
-#pragma unroll
-            for (int qb = 0; qb < 4; qb++) {
-                float bq[4];
-                load_bq(qb, bq);
-                float m = -__builtin_inff();
-#pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) m = fmaxf(m, pre(sc[h], acc[h][qb][r], bq[r]));
-                if (__ballot(m >= 0.0f)) survivors(acc, qb, rb0, sc);
-            }
+        for (int p = 0; p < PPW; p++) {
+            const int cur = p & 1, oth = cur ^ 1;
+            const int row0 = rw + 32 * p;
+            mfma_pair(accs[cur], bc, tile, row0, p + 1 < PPW ? row0 + 32 : -1, accs[oth], scs[oth], pm);
+            check(accs[oth], rbs[oth], scs[oth], pm);
+            scs[cur][0] = cs[row0 + j];
+            scs[cur][1] = cs[row0 + 16 + j];
+            rbs[cur] = c0 + row0;
         }
     }
+    // the last chunk's last pair
+#pragma unroll
+    for (int qb = 0; qb < 4; qb++) prefilter(accs[1], scs[1], pm, qb);
+    check(accs[1], rbs[1], scs[1], pm);
     __syncthreads();
     for (int i = tid; i < QG; i += kMq8Threads)
-        if (q0 + i < a.nq) a.counts[(int64_t)blockIdx.x * a.nq + q0 + i] = cnt_s[i];
+        if (qmap_s[i] < a.nq) a.counts[(int64_t)blockIdx.x * a.nq + qmap_s[i]] = cnt_s[i];
 }
 
 // ------------------------------------------------------ q4 int8 shadow
@@ -460,9 +569,9 @@ MqShape mq8_shape(int pitch, int ws, bool shadow) {
     s.ws = ws;
     s.shadow = shadow ? 1 : 0;
     s.qg = kMq8QG / ws;
-    s.chunk = kMq8CH;
-    s.tile = kMq8CH * pitch;
-    s.tile_bytes = mq8_nbuf(s.tile, s.qg) * (s.tile + kMq8CH * 4);  // chunk tiles + row scales
+    s.chunk = kMq8CH * ws;  // the kernel's CH
+    s.tile = s.chunk * pitch;
+    s.tile_bytes = mq8_nbuf(s.tile, s.qg, s.chunk) * (s.tile + s.chunk * 4);  // chunk tiles + row scales
     s.threads = kMq8Threads;
     return s;
 }

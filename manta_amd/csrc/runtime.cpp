@@ -81,6 +81,7 @@ struct MantaRocmCandidates {
     bool ref_ranked = false;
     mutable size_t bytes = 0;
     bool scales_finite = false;  // every row / block scale is finite (the 512-query kernel needs it)
+    bool scales_nonneg = false;  // q8: no row scale is below zero (the 512-query kernel's pre-filter needs it)
     // q4: int8 shadow for many-query top-k (built on first use): codes
     // [n][shadow_pitch], scales [2][n] (dot, cosine), error bounds
     mutable int shadow_state = 0;  // 0 not built, 1 built, -1 unavailable
@@ -582,13 +583,15 @@ int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* sca
     auto* c = new MantaRocmCandidates();
     c->rt = rt;
     c->format = MANTA_ROCM_Q8_ROWS;
-    bool finite = true, ranked = true;
+    bool finite = true, ranked = true, nonneg = true;
     for (int64_t r = 0; r < rows; r++) {
         const float a = std::fabs(scales[r]);
         finite = finite && std::isfinite(scales[r]);
         ranked = ranked && (a == 0.0f || (a >= 0x1p-60f && a <= 0x1p60f));
+        nonneg = nonneg && !(scales[r] < 0.0f);
     }
     c->scales_finite = finite;
+    c->scales_nonneg = nonneg;
     c->ref_ranked = finite && ranked;
     set_row_maxima(c, dnorm, dd);
     c->sets = sets;
@@ -952,7 +955,8 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int dop, int64_t nq, int64_t k, boo
     // split over two wave groups
     const int ws8 = nq >= 512 ? 1 : 2;
     if (c->format == MANTA_ROCM_Q8_ROWS) {
-        if (topk && dop == manta::OP_DOT && nq >= 256 && c->scales_finite && mq8_fits(c->pitch, k)) {
+        if (topk && dop == manta::OP_DOT && nq >= 256 && c->scales_finite && c->scales_nonneg &&
+            mq8_fits(c->pitch, k)) {
             p.sh = manta::mq8_shape(c->pitch, ws8, false);
         } else {
             if (c->pitch % 32 != 0 || !manta::mq_supported_ks(c->pitch / 32)) return p;
@@ -980,7 +984,8 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int dop, int64_t nq, int64_t k, boo
         return p;
     }
     // region: the best k after a compaction plus one chunk of appends, with
-    // slack so a compaction frees at least k slots
+    // slack so a compaction frees at least k slots (the 512-query kernel
+    // needs rc >= k + 2.5 chunks: true for its chunks of 64 or 128 rows)
     p.rc = (int)(((2 * k + 2 * chunk + 64) + 63) / 64 * 64);
     p.lds = (size_t)p.sh.tile_bytes +
             (p.sh.kind == 0 && (size_t)p.rc * 8 > (size_t)p.sh.tile ? (size_t)p.rc * 8 : 0);
