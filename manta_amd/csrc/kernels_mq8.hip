@@ -46,7 +46,7 @@ constexpr int kMq8QG = kMq8Waves * 64;  // queries per workgroup
 constexpr int kMq8CH = 64;             // rows per chunk and wave group (two row pairs per wave)
 
 // chunk tiles (with their row scales) in the LDS the static arrays leave:
-// those take 24 bytes per query plus about 2 KB
+// those take 24 bytes per query plus about 2.5 KB
 constexpr int mq8_nbuf(int tile, int qg, int ch) {
     int n = (160 * 1024 - qg * 24 - 2560) / (tile + ch * 4);
     return n > 6 ? 6 : (n < 2 ? 2 : n);
@@ -98,16 +98,20 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     // Direct-to-LDS chunk loads: lane i of load s fills tile bytes
     // [1024 s + 16 i, +16), which hold row x / PITCH, stored column
     // (x % PITCH) / 16, i.e. source column stored ^ ((row >> 1) & 7).
-    // Rows past the range read the last row of the range instead.
+    // Rows past the range read the last row of the range instead.  The
+    // source offsets are recomputed per chunk (the empty asm keeps the
+    // compiler from hoisting them out of the loop): held in registers they
+    // get spilled, and a scratch reload's vmcnt wait would also wait for the
+    // chunk loads in flight.
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-    int soff[LPW];
-#pragma unroll
-    for (int i = 0; i < LPW; i++) {
-        const int x = (wave_s * LPW + i) * 1024 + lane * 16;
+    auto soff = [&](int i) {
+        int ws = wave_s;
+        asm volatile("" : "+s"(ws));
+        const int x = (ws * LPW + i) * 1024 + lane * 16;
         const int row = x / PITCH;
         const int col = ((x % PITCH) / 16) ^ ((row >> 1) & 7);
-        soff[i] = row * PITCH + col * 16;
-    }
+        return row * PITCH + col * 16;
+    };
     const uint32_t tbase = lds_addr(tiles);
     const uint32_t sbase = lds_addr(cscale);
     // the last WS waves also load the chunk's row scales (64 each)
@@ -119,9 +123,14 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         // the LDS destination goes to M0: keep it in a scalar register
         const uint32_t dst = __builtin_amdgcn_readfirstlane(tbase + buf * TILE + wave_s * LPW * 1024);
 #pragma unroll
-        for (int i = 0; i < LPW; i++) lds_load16(base + (soff[i] < lim ? soff[i] : lim), dst + i * 1024);
+        for (int i = 0; i < LPW; i++) {
+            const int o = soff(i);
+            lds_load16(base + (o < lim ? o : lim), dst + i * 1024);
+        }
         if (sw >= 0) {
-            const int si = sw * 64 + lane;
+            int sws = sw;
+            asm volatile("" : "+s"(sws));  // recomputed per chunk, as soff
+            const int si = sws * 64 + lane;
             lds_load4(a.scales + c0 + (si < left ? si : left - 1),
                       __builtin_amdgcn_readfirstlane(sbase + buf * CH * 4 + sw * 256));
         }
@@ -205,9 +214,16 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     // of those queries (read where it is used, one LDS read); pm[qb] >= 0
     // unless every exact test of the block's pairs in this lane must fail
     // (fma rounds monotonically in each operand).  The slot order keeps the
-    // 4 bounds close, so this is nearly as tight as a test per query.
+    // 4 bounds close, so this is nearly as tight as a test per query.  The
+    // bounds come from registers (pb, read once per chunk): an LDS read here
+    // would make the wait for it also wait for the B fragments read ahead.
+    auto load_pb = [&](float (&pbr)[4]) {
+#pragma unroll
+        for (int qb = 0; qb < 4; qb++) pbr[qb] = pmin_s[((lw + qb * 16) >> 2) + g];
+    };
+    float pbr[4];
     auto prefilter = [&](const v4i (&acc)[2][4], const float (&sc)[2], float (&pm)[4], int qb) {
-        const float pb = pmin_s[((lw + qb * 16) >> 2) + g];
+        const float pb = pbr[qb];
         float v[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -218,10 +234,12 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         pm[qb] = fmaxf(v[0], v[1]);
     };
 
-    // The pairs of one query block of a row pair that pass the exact test,
-    // appended as (pre-score, row) pairs (a wave where one passed the filter):
-    // the lane's 8 tests go to a bit mask first, and the appends loop over
-    // its set bits, so a lane pays one LDS atomic per pair it appends.
+    // The pairs of one query block of a row pair that pass the exact test
+    // against each query's bound, appended as (pre-score, row) pairs (a wave
+    // where one passed the filter): the lane's 8 tests go to a bit mask
+    // first, and the appends loop over its set bits, so a lane pays one LDS
+    // atomic per pair it appends.  (Slots without a query have bound +inf,
+    // or -inf for smallest-k, and never append.)
     auto survivors = [&](const v4i (&acc)[2][4], int qb, int64_t rb0, const float (&sc)[2]) {
         const float4 b4 = *(const float4*)&bnd_s[lw + qb * 16 + 4 * g];
         const float bx[4] = {b4.x, b4.y, b4.z, b4.w};
@@ -325,10 +343,12 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         // last chunk the pending last pairs add at most half a chunk.  The
         // runtime sizes regions rc >= k + 2.5*CH, so a compacted region (k
         // pairs) is never flagged again at once.
-        if (wave < NFW) {
-            const int i = wave * 64 + lane;
-            const uint64_t m = __ballot(cnt_s[i] > a.rc - (5 * CH) / 2);
-            if (lane == 0) flags[par][wave] = m;
+        if (wave_s < NFW) {
+            // (slot index from the scalar wave index and the lane count, so
+            // the compiler recomputes it instead of spilling it)
+            const int ln = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0));
+            const uint64_t m = __ballot(cnt_s[wave_s * 64 + ln] > a.rc - (5 * CH) / 2);
+            if (ln == 0) flags[par][wave_s] = m;
         }
         // this wave's loads of chunk c are done once at most the loads of
         // the chunks issued after it are outstanding; the barrier extends
@@ -342,10 +362,12 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         const int nbuf = buf == 0 ? NBUF - 1 : buf - 1;  // tile of chunk c+NBUF-1 (free now)
         const uint8_t* tile = tiles + buf * TILE;
         const float* cs = cscale + buf * CH;
-        // the first pair's first fragments go out with the flags' read (a
-        // compaction writes neither this tile nor the fragments)
+        // the first pair's first fragments and the bounds go out with the
+        // flags' read (a compaction writes neither this tile nor the
+        // fragments; it reloads the bounds it may change)
         v4i bc[2];
         load_b(bc, tile, rw, 0);
+        load_pb(pbr);
         {
             bool any = false;
 #pragma unroll
@@ -408,6 +430,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                     }
                     __syncthreads();
                 }
+                load_pb(pbr);
             }
         }
         if (c0 + (NBUF - 1) * CH < r1) issue_chunk(c0 + (NBUF - 1) * CH, nbuf);
@@ -417,14 +440,17 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         for (int p = 0; p < PPW; p++) {
             const int cur = p & 1, oth = cur ^ 1;
             const int row0 = rw + 32 * p;
-            mfma_pair(accs[cur], bc, tile, row0, p + 1 < PPW ? row0 + 32 : -1, accs[oth], scs[oth], pm);
-            check(accs[oth], rbs[oth], scs[oth], pm);
+            // this pair's scales, read before its MFMAs: the next pair's
+            // filter uses them, long after they arrive
             scs[cur][0] = cs[row0 + j];
             scs[cur][1] = cs[row0 + 16 + j];
+            mfma_pair(accs[cur], bc, tile, row0, p + 1 < PPW ? row0 + 32 : -1, accs[oth], scs[oth], pm);
+            check(accs[oth], rbs[oth], scs[oth], pm);
             rbs[cur] = c0 + row0;
         }
     }
     // the last chunk's last pair
+    load_pb(pbr);
 #pragma unroll
     for (int qb = 0; qb < 4; qb++) prefilter(accs[1], scs[1], pm, qb);
     check(accs[1], rbs[1], scs[1], pm);
