@@ -678,6 +678,8 @@ __global__ __launch_bounds__(256) void embed_gemm3_kernel(EmbedArgs a) {
             __hip_atomic_store(pdst + wave * 96 + cb * 32 + l32, __float_as_uint(sum), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
+    // publication order as finish_wave_lists (kernels_score.hip): agent-scope
+    // atomic stores retired by s_waitcnt vmcnt(0), barrier, then the ticket
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0)

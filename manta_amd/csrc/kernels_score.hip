@@ -255,6 +255,14 @@ __device__ inline void finish_wave_lists(const ScanArgs& a, uint64_t list, uint6
     const int64_t per_q = (int64_t)gridDim.x * a.k;
     uint64_t* dst = a.partial + (int64_t)qi * per_q + (int64_t)blockIdx.x * a.k;
     if (wave == 0 && lane < a.k) __hip_atomic_store(dst + lane, list, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Publication order at the ISA level (gfx950): every access to the parts
+    // and the ticket is an agent-scope atomic, which the AMDGPU memory model
+    // implements as sc1 accesses performed at the device coherence point
+    // (past the per-XCD L2s); s_waitcnt vmcnt(0) retires this wave's part
+    // stores there before the barrier, the ticket RMW is issued after it,
+    // and the last workgroup's sc1 loads read the coherence point.  A
+    // source-level release/acquire pair would add an L2 writeback per
+    // workgroup (buffer_wbl2): 11% more time on a 32-problem q8 scan.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0)
