@@ -400,12 +400,14 @@ def run_c4(rt, steps, warmup, cpu_s) -> dict:
     k = 50
     cands = rt.bind_q8(codes, scales)
     td, md, tbd, pd, csd = (rt.to_device(x) for x in (tokens, mask, table, pcodes, cs))
+    # the projection is a bound weight: put in the MFMA layout once
+    pp = rt.prepare_projection(pd)
     emb = rt.empty((b, e), np.uint16)
     ids = rt.empty((b, k), np.int32)
     sc = rt.empty((b, k), np.float32)
 
     def step():
-        rt.embed_pooled(td, md, tbd, pd, csd, out=emb)
+        rt.embed_pooled(td, md, tbd, pp, csd, out=emb)
         rt.score_topk(cands, "dot", emb, k, out=(ids, sc, None), quantized=True)
 
     fams = ["embed", "embed_transpose", "embed_finalize", "mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]

@@ -95,6 +95,11 @@ enum {
 enum {
     MANTA_ROCM_PROJ_F16 = 0,    /* f16 [d, e] */
     MANTA_ROCM_PROJ_Q8_COL = 1, /* int8 [d, e] + f32 scale per output column */
+    /* the two above prepared once by manta_rocm_prepare_projection: f16
+     * [e, d], the matrix cores' operand layout (int8 codes widened exactly,
+     * the column scales still applied after accumulation) */
+    MANTA_ROCM_PROJ_F16_T = 2,
+    MANTA_ROCM_PROJ_Q8_COL_T = 3, /* + f32 scale per output column */
 };
 
 typedef struct MantaRocm MantaRocm;
@@ -363,6 +368,16 @@ int manta_rocm_mean_pool(MantaRocm* rt, const float* x_dev, int64_t b, int64_t t
  * CUDA row-wise kernel at compiler/compiler.go:731-745). */
 int manta_rocm_normalize_rows(MantaRocm* rt, float* x_dev, int64_t rows, int64_t cols,
                               char** err);
+
+/* A projection weight in the layout the MFMA embed and matmul kernels read
+ * (no counterpart in the reference: its weights are re-read per call).
+ * proj_kind MANTA_ROCM_PROJ_F16 or MANTA_ROCM_PROJ_Q8_COL, [d, e]; writes
+ * f16 [e, d] to out_dev (e*d*2 bytes) and the kind to pass with it
+ * (MANTA_ROCM_PROJ_F16_T / _Q8_COL_T, same column scales) to *out_kind.
+ * Prepared once when a weight is bound, it saves the per-call transpose
+ * launch of the pipelined GEMMs.  Stream-ordered. */
+int manta_rocm_prepare_projection(MantaRocm* rt, const void* proj_dev, int proj_kind, int64_t d, int64_t e,
+                                  uint16_t* out_dev, int* out_kind, char** err);
 
 /* The whole embed entry point in one fused launch sequence:
  * gather(table, tokens) -> @matmul(proj) -> mean_pool(mask) -> normalize,

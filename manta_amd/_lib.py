@@ -17,7 +17,7 @@ DOT, COSINE, L2_DISTANCE = 0, 1, 2
 QUANTIZED_QUERY = 0x100
 LARGEST, SMALLEST = 0, 1
 Q8_ROWS, Q4_BLOCKS = 8, 4
-PROJ_F16, PROJ_Q8_COL = 0, 1
+PROJ_F16, PROJ_Q8_COL, PROJ_F16_T, PROJ_Q8_COL_T = 0, 1, 2, 3
 DENSE_F32, DENSE_F16 = 32, 16
 
 OPS = {"dot": DOT, "cosine": COSINE, "l2_distance": L2_DISTANCE}
@@ -177,6 +177,7 @@ SIGNATURES = {
         C.c_int,
         [_p, _p, _p, _i64, _i64, _p, _i64, _i64, _p, C.c_int, _p, _i64, _p, _err],
     ),
+    "manta_rocm_prepare_projection": (C.c_int, [_p, _p, C.c_int, _i64, _i64, _p, C.POINTER(C.c_int), _err]),
 }
 
 

@@ -126,6 +126,10 @@ struct Val {
     int ids_storage = 0;
     const MantaRocmCandidates* cands = nullptr;
     int rows_format = 0;  // MANTA_ROCM_Q8_ROWS / Q4_BLOCKS for rows and packs
+    // a bound [K, N] matmul weight prepared at bind time
+    // (manta_rocm_prepare_projection): f16 [N][K], owned by the program
+    void* prep = nullptr;
+    int prep_kind = -1;
     // deferred score: op and the names of its query and docs values
     int op = -1;
     std::string qname, dname;
@@ -829,9 +833,11 @@ bool step_matmul(Run& r, const Step& s, Val* out) {
     const bool rhs_f16 = rhs->kind == MANTA_VALUE_TENSOR && rhs->storage == MANTA_DT_F16 && rr == 2;
     if (lhs_f16 && (rhs_f16 || rhs_q8)) {
         char* e = nullptr;
-        const int rc = manta_rocm_matmul_f16(r.p->rt, (const uint16_t*)lhs->data, M, K, rhs->data,
-                                             rhs_q8 ? MANTA_ROCM_PROJ_Q8_COL : MANTA_ROCM_PROJ_F16,
-                                             rhs_q8 ? (const float*)rhs->scales : nullptr, N, (float*)out->data, &e);
+        const bool prep = rhs->prep != nullptr;
+        const int rc = manta_rocm_matmul_f16(
+            r.p->rt, (const uint16_t*)lhs->data, M, K, prep ? rhs->prep : rhs->data,
+            prep ? rhs->prep_kind : (rhs_q8 ? MANTA_ROCM_PROJ_Q8_COL : MANTA_ROCM_PROJ_F16),
+            rhs_q8 ? (const float*)rhs->scales : nullptr, N, (float*)out->data, &e);
         if (rc != MANTA_ROCM_UNSUPPORTED) return r.abi(rc, e);
         free(e);  // a shape the f16 GEMM does not take: the f32 path below
     }
@@ -1106,6 +1112,8 @@ int manta_rocm_program_load(MantaRocm* rt, const MantaModule* mod, MantaRocmProg
 
 void manta_rocm_program_destroy(MantaRocmProgram* p) {
     if (!p) return;
+    for (auto& kv : p->weights)
+        if (kv.second.prep) (void)hipFree(kv.second.prep);
     for (auto& kv : p->plans) {
         for (auto& b : kv.second.pool)
             if (b.p) (void)hipFree(b.p);
@@ -1122,6 +1130,35 @@ int manta_rocm_program_bind(MantaRocmProgram* p, const MantaRocmValue* value, ch
     Val v;
     std::string e;
     if (!import_value(*value, &v, &e)) return set_err(err, MANTA_ROCM_ERROR, "param " + q(value->name) + ": " + e);
+    // an f16 or q8-column [K, N] weight the pipelined f16 GEMM takes is
+    // transposed once here, not on every matmul step
+    if (v.kind == MANTA_VALUE_TENSOR && v.shape.size() == 2 &&
+        (v.storage == MANTA_DT_F16 || v.storage == MANTA_DT_Q8) && v.shape[0] % 32 == 0 && v.shape[1] % 128 == 0 &&
+        v.shape[1] <= 4096) {
+        void* prep = nullptr;
+        if (hipMalloc(&prep, (size_t)(v.shape[0] * v.shape[1]) * 2) == hipSuccess) {
+            int kind = -1;
+            char* pe = nullptr;
+            const int rc = manta_rocm_prepare_projection(
+                p->rt, v.data, v.storage == MANTA_DT_Q8 ? MANTA_ROCM_PROJ_Q8_COL : MANTA_ROCM_PROJ_F16, v.shape[0],
+                v.shape[1], (uint16_t*)prep, &kind, &pe);
+            free(pe);
+            if (rc == MANTA_ROCM_OK) {
+                v.prep = prep;
+                v.prep_kind = kind;
+            } else {
+                (void)hipFree(prep);
+            }
+        } else {
+            (void)hipGetLastError();  // no room: matmul steps transpose per call
+        }
+    }
+    auto old = p->weights.find(value->name);
+    if (old != p->weights.end() && old->second.prep) {
+        // the previous binding's copy may still be read by queued work
+        (void)hipStreamSynchronize((hipStream_t)manta_rt::runtime_stream(p->rt));
+        (void)hipFree(old->second.prep);
+    }
     p->weights[value->name] = v;
     return MANTA_ROCM_OK;
 }

@@ -1509,17 +1509,20 @@ int manta_rocm_dense_topk(MantaRocm* rt, const void* rows, int dtype, int64_t n,
 
 namespace {
 
+bool proj_q8(int kind) { return kind == MANTA_ROCM_PROJ_Q8_COL || kind == MANTA_ROCM_PROJ_Q8_COL_T; }
+bool proj_prepared(int kind) { return kind == MANTA_ROCM_PROJ_F16_T || kind == MANTA_ROCM_PROJ_Q8_COL_T; }
+
 int check_proj(int proj_kind, const void* proj, const float* col_scale, int64_t k, int64_t n, char** err) {
     if (!proj) return fail(err, MANTA_ROCM_ERROR, "nil matmul input");
-    if (proj_kind != MANTA_ROCM_PROJ_F16 && proj_kind != MANTA_ROCM_PROJ_Q8_COL)
+    if (proj_kind < MANTA_ROCM_PROJ_F16 || proj_kind > MANTA_ROCM_PROJ_Q8_COL_T)
         return fail(err, MANTA_ROCM_ERROR, "unknown projection kind %d", proj_kind);
-    if (proj_kind == MANTA_ROCM_PROJ_Q8_COL && !col_scale)
+    if (proj_q8(proj_kind) && !col_scale)
         return fail(err, MANTA_ROCM_ERROR, "q8 projection needs per-column scales");
     if (k <= 0 || n <= 0) return fail(err, MANTA_ROCM_ERROR, "matmul mismatch: empty operand");
     if (k % 8 != 0)
         return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: inner dimension %lld is not a multiple of 8",
                     (long long)k);
-    if (n % (proj_kind == MANTA_ROCM_PROJ_Q8_COL ? 4 : 2) != 0)
+    if (n % (proj_q8(proj_kind) ? 4 : 2) != 0)
         return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: output width %lld not supported", (long long)n);
     if (n > 4096 || k > (1 << 20))
         return fail(err, MANTA_ROCM_UNSUPPORTED, "matmul: shape beyond the device path");
@@ -1557,7 +1560,16 @@ int manta_rocm_matmul_f16(MantaRocm* rt, const uint16_t* lhs, int64_t m, int64_t
     a.B = rhs;
     a.colscale = col_scale;
     a.Y = out;
-    const bool q8b = proj_kind == MANTA_ROCM_PROJ_Q8_COL;
+    const bool q8b = proj_q8(proj_kind);
+    if (proj_prepared(proj_kind)) {
+        // the operand is already f16 [n][k]: the pipelined GEMM only
+        if (!manta::embed_gemm2_supported(a))
+            return fail(err, MANTA_ROCM_UNSUPPORTED,
+                        "matmul: a prepared projection needs k %% 32 == 0 and n %% 128 == 0 (got %lld x %lld)",
+                        (long long)k, (long long)n);
+        LAUNCH_TRY(manta::launch_embed_gemm2(a, false, q8b, false, (const uint16_t*)rhs, rt->stream), "matmul");
+        return MANTA_ROCM_OK;
+    }
     if (manta::embed_gemm3_supported(a, q8b)) {
         LAUNCH_TRY(manta::launch_embed_gemm3(a, false, false, rt->stream), "matmul");
         return MANTA_ROCM_OK;
@@ -1670,6 +1682,26 @@ int manta_rocm_encoder_pooled_layers(MantaRocm* rt, const int32_t* tokens, const
     return MANTA_ROCM_OK;
 }
 
+int manta_rocm_prepare_projection(MantaRocm* rt, const void* proj, int proj_kind, int64_t d, int64_t e,
+                                  uint16_t* out, int* out_kind, char** err) {
+    RT_CHECK(rt);
+    if (!out || !out_kind) return fail(err, MANTA_ROCM_ERROR, "nil prepare_projection output");
+    if (proj_kind != MANTA_ROCM_PROJ_F16 && proj_kind != MANTA_ROCM_PROJ_Q8_COL)
+        return fail(err, MANTA_ROCM_ERROR, "prepare_projection: kind %d is not a [d, e] projection", proj_kind);
+    // (the scales stay with the caller; check_proj only needs a non-null one)
+    static const float kOne = 1.0f;
+    int rc = check_proj(proj_kind, proj, &kOne, d, e, err);
+    if (rc) return rc;
+    manta::EmbedArgs a{};
+    a.K = (int)d;
+    a.N = (int)e;
+    a.B = proj;
+    LAUNCH_TRY(manta::launch_embed_transpose_b(a, proj_kind == MANTA_ROCM_PROJ_Q8_COL, out, rt->stream),
+               "embed_transpose");
+    *out_kind = proj_kind == MANTA_ROCM_PROJ_Q8_COL ? MANTA_ROCM_PROJ_Q8_COL_T : MANTA_ROCM_PROJ_F16_T;
+    return MANTA_ROCM_OK;
+}
+
 int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t* mask, int64_t b,
                             int64_t t, const uint16_t* table, int64_t vocab, int64_t d, const void* proj,
                             int proj_kind, const float* col_scale, int64_t e, uint16_t* out, char** err) {
@@ -1680,7 +1712,8 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
                     (long long)t, (long long)vocab, (long long)d);
     int rc = check_proj(proj_kind, proj, col_scale, d, e, err);
     if (rc) return rc;
-    const bool q8b = proj_kind == MANTA_ROCM_PROJ_Q8_COL;
+    const bool q8b = proj_q8(proj_kind);
+    const bool prepared = proj_prepared(proj_kind);
     manta::EmbedArgs a{};
     a.tokens = tokens;
     a.mask = mask;
@@ -1695,17 +1728,21 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
     a.err = rt->err_word;
     if (manta::embed_gemm5_supported(a) && b * t / 256 >= 128) {
         // many short sequences: 256-row workgroups of whole sequences finish
-        // their embeddings themselves (after the projection's transpose)
-        rc = ensure_workspace(rt, (size_t)d * e * 2 + 256, err);
-        if (rc) return rc;
+        // their embeddings themselves (after the projection's transpose,
+        // unless it came prepared)
         a.out = out;
-        uint16_t* bt = (uint16_t*)rt->ws;
-        LAUNCH_TRY(manta::launch_embed_transpose_b(a, q8b, bt, rt->stream), "embed_transpose");
+        const uint16_t* bt = (const uint16_t*)proj;
+        if (!prepared) {
+            rc = ensure_workspace(rt, (size_t)d * e * 2 + 256, err);
+            if (rc) return rc;
+            bt = (uint16_t*)rt->ws;
+            LAUNCH_TRY(manta::launch_embed_transpose_b(a, q8b, (uint16_t*)rt->ws, rt->stream), "embed_transpose");
+        }
         LAUNCH_TRY(manta::launch_embed_gemm5(a, q8b, bt, rt->stream), "embed");
         rt->gather_pending = true;
         return MANTA_ROCM_OK;
     }
-    if (manta::embed_gemm3_supported(a, q8b) && b <= kTickets) {
+    if (!prepared && manta::embed_gemm3_supported(a, q8b) && b <= kTickets) {
         // one launch: 128-row x 96-column tiles, the last tile of each
         // sequence finishes it
         a.tiles_per_seq = (int)((t + 127) / 128);
@@ -1726,10 +1763,19 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
     if (rc) return rc;
     a.tiles_per_seq = (int)tiles;
     a.P = (float*)rt->ws;
+    if (prepared && !manta::embed_gemm2_supported(a))
+        return fail(err, MANTA_ROCM_UNSUPPORTED,
+                    "embed: a prepared projection needs d %% 32 == 0 and e %% 128 == 0 (got %lld x %lld)", (long long)d,
+                    (long long)e);
     if (manta::embed_gemm2_supported(a)) {
-        // the projection transposed to f16 [e][d] after the partials
-        uint16_t* bt = (uint16_t*)((char*)rt->ws + pbytes);
-        LAUNCH_TRY(manta::launch_embed_transpose_b(a, q8b, bt, rt->stream), "embed_transpose");
+        // the projection as f16 [e][d]: prepared, or transposed after the
+        // partials
+        const uint16_t* bt = (const uint16_t*)proj;
+        if (!prepared) {
+            uint16_t* w = (uint16_t*)((char*)rt->ws + pbytes);
+            LAUNCH_TRY(manta::launch_embed_transpose_b(a, q8b, w, rt->stream), "embed_transpose");
+            bt = w;
+        }
         LAUNCH_TRY(manta::launch_embed_gemm2(a, true, q8b, true, bt, rt->stream), "embed");
     } else {
         LAUNCH_TRY(manta::launch_embed_gemm(a, true, q8b, true, rt->stream), "embed");

@@ -27,6 +27,14 @@ def device_count() -> int:
     return n.value
 
 
+class PreparedProjection:
+    """A projection in the MFMA kernels' layout: data is f16 [e, d]; kind is
+    PROJ_F16_T or PROJ_Q8_COL_T (the latter still takes its column scales)."""
+
+    def __init__(self, data: "DeviceArray", kind: int, d: int, e: int):
+        self.data, self.kind, self.d, self.e = data, kind, d, e
+
+
 class DeviceArray:
     """A device allocation with a numpy dtype and shape."""
 
@@ -284,15 +292,33 @@ class Runtime:
              idx.ptr, C.c_int64(nidx), out.ptr)
         return out
 
-    def matmul_f16(self, lhs: DeviceArray, rhs: DeviceArray, col_scale: Optional[DeviceArray] = None
+    def prepare_projection(self, proj: DeviceArray) -> "PreparedProjection":
+        """A [d, e] f16 or int8 projection in the MFMA kernels' layout (f16
+        [e, d]), for embed_pooled / matmul_f16 without a per-call transpose."""
+        d, e = proj.shape
+        kind = _lib.PROJ_Q8_COL if proj.dtype == np.int8 else _lib.PROJ_F16
+        out = self.empty((e, d), np.uint16)
+        k = C.c_int()
+        call("manta_rocm_prepare_projection", self.handle, proj.ptr, C.c_int(kind), C.c_int64(d), C.c_int64(e),
+             out.ptr, C.byref(k))
+        return PreparedProjection(out, k.value, d, e)
+
+    @staticmethod
+    def _proj(rhs) -> tuple:
+        """(pointer, kind, k, n) of a [k, n] projection or a prepared one."""
+        if isinstance(rhs, PreparedProjection):
+            return rhs.data.ptr, rhs.kind, rhs.d, rhs.e
+        k, n = rhs.shape
+        return rhs.ptr, (_lib.PROJ_Q8_COL if rhs.dtype == np.int8 else _lib.PROJ_F16), k, n
+
+    def matmul_f16(self, lhs: DeviceArray, rhs, col_scale: Optional[DeviceArray] = None
                    ) -> DeviceArray:
         m, k = lhs.shape
-        k2, n = rhs.shape
+        ptr, kind, k2, n = self._proj(rhs)
         if k2 != k:
-            raise ValueError("matmul mismatch %s x %s" % (lhs.shape, rhs.shape))
-        kind = _lib.PROJ_Q8_COL if rhs.dtype == np.int8 else _lib.PROJ_F16
+            raise ValueError("matmul mismatch %s x [%d,%d]" % (lhs.shape, k2, n))
         out = self.empty((m, n), np.float32)
-        call("manta_rocm_matmul_f16", self.handle, lhs.ptr, C.c_int64(m), C.c_int64(k), rhs.ptr,
+        call("manta_rocm_matmul_f16", self.handle, lhs.ptr, C.c_int64(m), C.c_int64(k), ptr,
              C.c_int(kind), _ptr(col_scale), C.c_int64(n), out.ptr)
         return out
 
@@ -348,18 +374,18 @@ class Runtime:
         return x
 
     def embed_pooled(self, tokens: DeviceArray, mask: DeviceArray, table: DeviceArray,
-                     proj: DeviceArray, col_scale: Optional[DeviceArray] = None,
+                     proj, col_scale: Optional[DeviceArray] = None,
                      out: Optional[DeviceArray] = None) -> DeviceArray:
+        """proj: [d, e] f16 or int8 device array, or prepare_projection's result."""
         b, t = tokens.shape
         vocab, d = table.shape
-        d2, e = proj.shape
+        ptr, kind, d2, e = self._proj(proj)
         if d2 != d:
-            raise ValueError("matmul mismatch [%d,%d,%d] x %s" % (b, t, d, proj.shape))
-        kind = _lib.PROJ_Q8_COL if proj.dtype == np.int8 else _lib.PROJ_F16
+            raise ValueError("matmul mismatch [%d,%d,%d] x [%d,%d]" % (b, t, d, d2, e))
         if out is None:
             out = self.empty((b, e), np.uint16)
         call("manta_rocm_embed_pooled", self.handle, tokens.ptr, mask.ptr, C.c_int64(b),
-             C.c_int64(t), table.ptr, C.c_int64(vocab), C.c_int64(d), proj.ptr, C.c_int(kind),
+             C.c_int64(t), table.ptr, C.c_int64(vocab), C.c_int64(d), ptr, C.c_int(kind),
              _ptr(col_scale), C.c_int64(e), out.ptr)
         return out
 

@@ -182,3 +182,68 @@ def test_embed_large_batch_whole_sequence_tiles(rt, nq, t, q8):
     empty = lengths == 0
     assert np.all(g[empty] == 0) and np.all(want32[empty] == 0)
     assert _cos_rows(g[~empty], want32[~empty]).min() >= 0.9999
+
+
+# ---------------------------------------------------------------------------
+# Projections prepared once (manta_rocm_prepare_projection): the same GEMMs
+# read the prepared f16 [e, d] operand, so the outputs equal the per-call
+# transpose path bit for bit.
+
+@pytest.mark.parametrize("nq,t,q8", [(512, 64, True), (256, 128, False), (6, 100, True), (5, 70, False)])
+def test_embed_prepared_projection_bit_identical(rt, nq, t, q8):
+    """Whole-sequence tiles (the first two) and the partial-sum path (the
+    last two, e = 256 so the single-pass f16 kernel does not apply)."""
+    d, e = (384, 384) if nq >= 256 else (128, 256)
+    tokens = synth.uniform_i32(19, 0, nq * t, 0, 32000).reshape(nq, t)
+    lengths = synth.uniform_i32(19, 1, nq, 0, t + 1)
+    mask = (np.arange(t)[None, :] < lengths[:, None]).astype(np.int32)
+    table = rt.to_device(synth.normal_f16(19, 2, 32000, d, 0.02))
+    td, md = rt.to_device(tokens), rt.to_device(mask)
+    if q8:
+        proj = rt.to_device(synth.uniform_i8(19, 3, d * e, -127, 127).reshape(d, e))
+        cs = rt.to_device(((np.arange(e) + 1.0) / (127.0 * np.sqrt(d) * e)).astype(np.float32))
+    else:
+        proj = rt.to_device(synth.normal_f16(19, 3, d, e, 1.0 / np.sqrt(d)))
+        cs = None
+    pp = rt.prepare_projection(proj)
+    assert pp.data.shape == (e, d)
+    want = rt.embed_pooled(td, md, table, proj, cs).download()
+    got = rt.embed_pooled(td, md, table, pp, cs).download()
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_matmul_prepared_projection(rt, q8):
+    m, k, n = 300, 256, 256
+    a = synth.normal_f16(21, 0, m, k, 0.02)
+    ad = rt.to_device(a)
+    if q8:
+        codes = synth.uniform_i8(21, 1, k * n, -127, 127).reshape(k, n)
+        csh = ((np.arange(n) + 1.0) / (127.0 * np.sqrt(k) * n)).astype(np.float32)
+        rhs, cs = rt.to_device(codes), rt.to_device(csh)
+        w = codes.astype(np.float32) * csh[None, :]
+    else:
+        wf = synth.normal_f16(21, 1, k, n, 1.0 / np.sqrt(k))
+        rhs, cs = rt.to_device(wf), None
+        w = orc.f16_to_f32(wf)
+    want = rt.matmul_f16(ad, rhs, cs).download()
+    got = rt.matmul_f16(ad, rt.prepare_projection(rhs), cs).download()
+    np.testing.assert_array_equal(got, want)
+    af = orc.f16_to_f32(a)
+    assert np.all(np.abs(got - orc.matmul(af, w)) <= _matmul_bound(af, w))
+
+
+def test_prepared_projection_errors(rt):
+    """A prepared operand serves only the pipelined GEMM's shapes; a prepared
+    kind cannot be prepared again."""
+    a = rt.to_device(synth.normal_f16(23, 0, 10, 64, 0.02))
+    proj = rt.to_device(synth.normal_f16(23, 1, 64, 96, 0.1))
+    pp = rt.prepare_projection(proj)
+    with pytest.raises(MantaRocmError, match="prepared projection needs k % 32 == 0 and n % 128 == 0"):
+        rt.matmul_f16(a, pp)
+    from manta_amd import _lib
+    import ctypes as C
+    k = C.c_int()
+    with pytest.raises(MantaRocmError, match="is not a \\[d, e\\] projection"):
+        _lib.call("manta_rocm_prepare_projection", rt.handle, pp.data.ptr, C.c_int(_lib.PROJ_F16_T), C.c_int64(64),
+                  C.c_int64(96), pp.data.ptr, C.byref(k))
