@@ -1003,11 +1003,13 @@ MqPlan mq_plan(const MantaRocmCandidates* c, int dop, int64_t nq, int64_t k, boo
         const double span = (double)c->n / (double)s;
         const double gmax = std::max(4.0, (double)kMqSelectKeys / (double)k);
         int npass = std::max(1, (int)std::ceil(std::log(span) / std::log(gmax) - 1e-9));
-        // the 512-query kernel appends about k*g pairs per query and pass:
-        // keep g near 10 (k*g*npass is smallest there for the spans that
-        // occur) at one select per pass
+        // the 512-query kernel appends about k*(g-1) pairs per query and
+        // pass, each an exact test and an LDS atomic in the scan: keep g
+        // near 4.5 (measured on 1024 queries over 1024x the first pass's
+        // rows: 5 passes beat 3 by 4% of the step, 6 and 7 lose to 5 on the
+        // selects)
         if (p.sh.kind == 1 && !p.shadow)
-            npass = std::max(npass, (int)std::ceil(std::log(span) / std::log(12.0) - 1e-9));
+            npass = std::max(npass, (int)std::ceil(std::log(span) / std::log(4.5) - 1e-9));
         // shadow pairs: every pair the select keeps is rescored from a random
         // row, so fewer, larger passes win as long as a pass's pairs (about
         // 4*k*g with the margins) fit the 512-thread select's 8K-key buffer,
