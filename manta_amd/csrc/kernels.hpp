@@ -147,8 +147,8 @@ struct MqArgs {
     const int8_t* qlo;
     const QConst* qconst;       // [nq]
     const uint64_t* tau;        // [nq] threshold keys of this pass (0: none)
-    uint64_t* regions;          // [nq][R][rc] appended keys, R = the pass's grid.x (nq*R*rc < 2^31)
-    int* counts;                // [nq][R] keys per region
+    uint64_t* regions;          // [R][nq][rc] appended keys (nq*R*rc < 2^31)
+    int* counts;                // [R][nq] keys per region
     int R;                      // gridDim.x
     int rc;                     // region capacity (>= k + 2 * chunk rows + 1)
     int k;
@@ -165,8 +165,8 @@ struct MqArgs {
 
 // Arguments of the per-query merge after a pass.
 struct MqSelectArgs {
-    const uint64_t* regions;    // [nq][R][rc]
-    const int* counts;          // [nq][R]
+    const uint64_t* regions;    // [R][nq][rc]
+    const int* counts;          // [R][nq]
     int R;
     int rc;
     uint64_t* best;             // [nq][k] best keys so far (sorted), updated

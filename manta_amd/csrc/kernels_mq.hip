@@ -132,10 +132,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
             if (q0 + slot_lq(na, u) < a.nq) live[na] |= 1u << u;
     }
 
-    // this workgroup's key region of query q: wreg + q * qstride (a query's
-    // regions are contiguous; 32-bit indices, checked on the host)
-    uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.rc;
-    const uint32_t qstride = gridDim.x * (uint32_t)a.rc;
+    // this workgroup's key regions: [query][rc] (32-bit indices, checked on the host)
+    uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.nq * a.rc;
     const int64_t r0 = a.row_begin + (int64_t)blockIdx.x * a.rows_per_wg;
     int64_t r1 = r0 + a.rows_per_wg;
     if (r1 > a.row_end) r1 = a.row_end;
@@ -277,7 +275,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                     // displace; live excludes the padding queries)
                     const uint64_t key = make_key(score_of(p, lq, rowc), (uint32_t)row, SMALL);
                     const int pos = atomicAdd(&cnt_s[lq], 1);
-                    wreg[(uint32_t)(q0 + lq) * qstride + pos] = key;
+                    wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = key;
                 }
             }
         }
@@ -329,7 +327,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                 uint64_t* scratch = a.rc * 8 <= TILE ? (uint64_t*)(tiles + nbuf * TILE) : scratch_extra;
                 for (int lq = 0; lq < QG; lq++) {
                     if (!((flags[par][lq >> 6] >> (lq & 63)) & 1)) continue;
-                    uint64_t* reg = wreg + (uint32_t)(q0 + lq) * qstride;
+                    uint64_t* reg = wreg + (uint32_t)((q0 + lq) * a.rc);
                     const int c = cnt_s[lq];
                     for (int i = tid; i < c; i += 256) scratch[i] = reg[i];
                     if (tid == 0) {
@@ -385,7 +383,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     if (!APPEND) return;
     __syncthreads();
     for (int i = tid; i < QG; i += 256)
-        if (q0 + i < a.nq) a.counts[(int64_t)(q0 + i) * gridDim.x + blockIdx.x] = cnt_s[i];
+        if (q0 + i < a.nq) a.counts[(int64_t)blockIdx.x * a.nq + q0 + i] = cnt_s[i];
 }
 
 // ------------------------------------------------------------- select
@@ -419,7 +417,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     int carry = 0;
     for (int base = 0; base < a.R; base += NT) {
         const int w = base + tid;
-        int c = w < a.R ? a.counts[(int64_t)q * a.R + w] : 0;
+        int c = w < a.R ? a.counts[(int64_t)w * a.nq + q] : 0;
         c = c < a.rc ? c : a.rc;
         const int incl = wave_incl_scan(c);
         if (lane == 63) wsum[wave] = incl;
@@ -475,7 +473,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
         fill = k;
     };
 
-    const uint64_t* regq = a.regions + (int64_t)q * a.R * a.rc;  // region w at regq + w*rc
+    const uint64_t* regq = a.regions + (int64_t)q * a.rc;  // region w at regq + w*nq*rc
     const float qmax = PM == 1 ? a.qconst[q].a : 0.0f;
     if (PM == 2) {
         // the query's E16 digit planes, read by every rescoring below
@@ -553,7 +551,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
                         if (pre[mid] <= g) lo = mid;
                         else hi = mid;
                     }
-                    v[t] = regq[(int64_t)lo * a.rc + (g - pre[lo])];
+                    v[t] = regq[(int64_t)lo * a.nq * a.rc + (g - pre[lo])];
                     if (PM == 1) v[t] = dot_pair_key(v[t], qmax, a.smallest);
                 }
             }

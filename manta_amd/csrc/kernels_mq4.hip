@@ -117,8 +117,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
             if (q0 + slot_lq(na, u) < a.nq) live[na] |= 1u << u;
     }
 
-    uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.rc;  // query q's region at wreg + q * qstride
-    const uint32_t qstride = gridDim.x * (uint32_t)a.rc;
+    uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.nq * a.rc;
     const int64_t r0 = a.row_begin + (int64_t)blockIdx.x * a.rows_per_wg;
     int64_t r1 = r0 + a.rows_per_wg;
     if (r1 > a.row_end) r1 = a.row_end;
@@ -267,7 +266,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                 uint64_t* scratch = a.rc * 8 <= TILE ? (uint64_t*)(tiles + nbuf * TILE) : scratch_extra;
                 for (int lq = 0; lq < QG; lq++) {
                     if (!((flags[par][lq >> 6] >> (lq & 63)) & 1)) continue;
-                    uint64_t* reg = wreg + (uint32_t)(q0 + lq) * qstride;
+                    uint64_t* reg = wreg + (uint32_t)((q0 + lq) * a.rc);
                     const int c = cnt_s[lq];
                     for (int i = tid; i < c; i += 256) scratch[i] = reg[i];
                     if (tid == 0) {
@@ -340,7 +339,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                             const uint64_t key = make_key(score_of(p, lq, rowc), (uint32_t)row, SMALL);
                             if (key > tau_s[lq]) {
                                 const int pos = atomicAdd(&cnt_s[lq], 1);
-                                wreg[(uint32_t)(q0 + lq) * qstride + pos] = key;
+                                wreg[(uint32_t)((q0 + lq) * a.rc + pos)] = key;
                             }
                         }
                     }
@@ -352,7 +351,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     if (!APPEND) return;
     __syncthreads();
     for (int i = tid; i < QG; i += 256)
-        if (q0 + i < a.nq) a.counts[(int64_t)(q0 + i) * gridDim.x + blockIdx.x] = cnt_s[i];
+        if (q0 + i < a.nq) a.counts[(int64_t)blockIdx.x * a.nq + q0 + i] = cnt_s[i];
 }
 
 // ----------------------------------------------------------------- hosts

@@ -90,8 +90,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     const int lw = (wave % NFW) * 64;  // this wave's first workgroup-local query
     const int rw = (wave / NFW) * (CH / WS);  // this wave's first row of a chunk (PPW row pairs)
 
-    uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.rc;  // query q's region at wreg + q * qstride
-    const uint32_t qstride = gridDim.x * (uint32_t)a.rc;
+    uint64_t* wreg = a.regions + (int64_t)blockIdx.x * a.nq * a.rc;
     const int64_t r0 = a.row_begin + (int64_t)blockIdx.x * a.rows_per_wg;
     int64_t r1 = r0 + a.rows_per_wg;
     if (r1 > a.row_end) r1 = a.row_end;
@@ -264,7 +263,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
             for (int i = 1; i < 8; i++) p = b == i ? pv[i] : p;
             const int lq = lw + qb * 16 + 4 * g + (b & 3);
             const int pos = atomicAdd(&cnt_s[lq], 1);
-            wreg[(uint32_t)qmap_s[lq] * qstride + pos] = dot_pair(p, (uint32_t)(rb0 + (b >> 2) * 16 + j));
+            wreg[(uint32_t)(qmap_s[lq] * a.rc + pos)] = dot_pair(p, (uint32_t)(rb0 + (b >> 2) * 16 + j));
         }
     };
     // Exact tests of the query blocks of a row pair whose pre-filter passed
@@ -387,7 +386,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                 for (int lq = 0; lq < QG; lq++) {
                     if (!((flags[par][lq >> 6] >> (lq & 63)) & 1)) continue;
                     const int qx = qmap_s[lq];
-                    uint64_t* reg = wreg + (uint32_t)qx * qstride;
+                    uint64_t* reg = wreg + (uint32_t)(qx * a.rc);
                     const int c = cnt_s[lq];
                     for (int i = tid; i < c; i += kMq8Threads) {
                         const uint64_t e = reg[i];
@@ -463,7 +462,7 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     check(accs[1], rbs[1], scs[1], pm);
     __syncthreads();
     for (int i = tid; i < QG; i += kMq8Threads)
-        if (qmap_s[i] < a.nq) a.counts[(int64_t)qmap_s[i] * gridDim.x + blockIdx.x] = cnt_s[i];
+        if (qmap_s[i] < a.nq) a.counts[(int64_t)blockIdx.x * a.nq + qmap_s[i]] = cnt_s[i];
 }
 
 // ------------------------------------------------------ q4 int8 shadow
