@@ -161,6 +161,10 @@ struct MqArgs {
     const uint16_t* q4scales;   // [n][d/32]
     int d;
     int op;                     // OP_COSINE or OP_DOT
+    // mq8 kernel, first top-k pass (no threshold yet): every (query, row)
+    // pair goes to its region at the row's offset in the workgroup's range,
+    // without tests or atomics (rows_per_wg <= rc)
+    int keep_all;
 };
 
 // Arguments of the per-query merge after a pass.

@@ -317,6 +317,59 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         }
     };
 
+    if (a.keep_all) {
+        // First pass: no threshold exists, so every pair is kept.  Each
+        // lane stores its pairs straight to the slot the row's offset in the
+        // range gives (16 lanes of a query and row block write 128
+        // contiguous bytes); the region counts are the range's rows.
+        int buf = 0;
+        for (int64_t c0 = r0; c0 < r1; c0 += CH, buf = buf == NBUF - 1 ? 0 : buf + 1) {
+            if (sw >= 0)
+                mq_wait_barrier<LPW + 1, NBUF - 2>((r1 - c0 - 1) / CH);
+            else
+                mq_wait_barrier<LPW, NBUF - 2>((r1 - c0 - 1) / CH);
+            if (c0 + (NBUF - 1) * CH < r1) issue_chunk(c0 + (NBUF - 1) * CH, buf == 0 ? NBUF - 1 : buf - 1);
+            const uint8_t* tile = tiles + buf * TILE;
+            const float* cs = cscale + buf * CH;
+#pragma unroll
+            for (int p = 0; p < PPW; p++) {
+                const int row0 = rw + 32 * p;
+                v4i acc[2][4];
+#pragma unroll
+                for (int ks = 0; ks < KS64; ks++) {
+                    v4i b[2];
+                    load_b(b, tile, row0, ks);
+#pragma unroll
+                    for (int qb = 0; qb < 4; qb++)
+#pragma unroll
+                        for (int h = 0; h < 2; h++)
+                            acc[h][qb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[qb][ks], b[h],
+                                                                               ks == 0 ? v4i{0, 0, 0, 0} : acc[h][qb],
+                                                                               0, 0, 0);
+                }
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int64_t row = c0 + row0 + h * 16 + j;
+                    const float sc = cs[row0 + h * 16 + j];
+                    if (row < r1) {
+#pragma unroll
+                        for (int qb = 0; qb < 4; qb++)
+#pragma unroll
+                            for (int r = 0; r < 4; r++) {
+                                const int q = qmap_s[lw + qb * 16 + 4 * g + r];
+                                if (q < a.nq)
+                                    wreg[(uint32_t)(q * a.rc) + (uint32_t)(row - r0)] =
+                                        dot_pair(fmul_rn(sc, (float)acc[h][qb][r]), (uint32_t)row);
+                            }
+                    }
+                }
+            }
+        }
+        for (int i = tid; i < QG; i += kMq8Threads)
+            if (qmap_s[i] < a.nq) a.counts[(int64_t)blockIdx.x * a.nq + qmap_s[i]] = (int)(r1 - r0);
+        return;
+    }
+
     // A wave's row pairs of a chunk alternate between the accumulator sets
     // accs[0] and accs[1]; each pair's filter runs under the next pair's
     // MFMAs, the chunk's last pair under the next chunk's first.  Before the

@@ -1141,6 +1141,9 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, cons
         a.row_end = ps.end;
         a.rows_per_wg = ps.rows_per_wg;
         a.R = ps.R;
+        // the first pass of the 512-query kernel keeps every pair: its
+        // workgroups take at most rc - 2*chunk rows, one slot per row
+        a.keep_all = i == 0 && p.sh.kind == 1 ? 1 : 0;
         LAUNCH_TRY(launch_mq_pass(p, dop, a, ps.R, rt->stream), "mq_scan");
         sa.R = ps.R;
         const bool last = i + 1 == p.passes.size();
