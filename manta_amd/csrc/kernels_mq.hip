@@ -324,6 +324,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 #pragma unroll
             for (int w = 0; w < NFW; w++) any |= flags[par][w] != 0;
             if (any) {
+                // every wave's appends (stores the barrier's vmcnt count may
+                // leave in flight) are complete before a region is read back:
+                // the workgroup shares one L1
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
                 uint64_t* scratch = a.rc * 8 <= TILE ? (uint64_t*)(tiles + nbuf * TILE) : scratch_extra;
                 for (int lq = 0; lq < QG; lq++) {
                     if (!((flags[par][lq >> 6] >> (lq & 63)) & 1)) continue;
