@@ -31,7 +31,9 @@
 // (PITCH is a multiple of 128, so a row holds a multiple of 8 columns): the
 // 16 lanes reading one column of 16 consecutive rows hit distinct banks.
 // Top-k runs in the same threshold passes as kernels_mq.hip (regions per
-// (workgroup, query), compaction when a region might overflow).
+// (workgroup, query), compaction when a region might overflow); the first
+// pass, which has no threshold, stores every pair at its row's slot without
+// tests or atomics.
 #include <algorithm>
 
 #include "mq_common.hpp"
