@@ -183,6 +183,8 @@ struct MqSelectArgs {
     int smallest;
     int pairs;                  // region entries: 0 keys; 1 q8 dot pairs (bits of p = scale*acc) << 32 | row,
                                 // the key's score p*qmax/127; 2 shadow pairs, the key the exact q4 score
+    int uniform;                // > 0: every region but the last holds exactly this many entries
+                                // (a pass that keeps every pair), so entry g is in region g / uniform
     const QConst* qconst;       // [nq] (pairs 1: E8 qmax; pairs 2: E16 constants)
     // pairs 2: the q4 matrix and the E16 digit planes in the q4 order [nq][d]
     const uint8_t* q4codes;

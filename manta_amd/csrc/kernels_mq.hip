@@ -550,13 +550,20 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
                 v[t] = 0;
                 if (j < take) {
                     const int g = base + j;
-                    int lo = 0, hi = a.R;  // last region w with pre[w] <= g
-                    while (hi - lo > 1) {
-                        const int mid = (lo + hi) >> 1;
-                        if (pre[mid] <= g) lo = mid;
-                        else hi = mid;
+                    int lo = 0, off;  // last region w with pre[w] <= g, g's place in it
+                    if (a.uniform > 0) {
+                        lo = g / a.uniform;
+                        off = g - lo * a.uniform;
+                    } else {
+                        int hi = a.R;
+                        while (hi - lo > 1) {
+                            const int mid = (lo + hi) >> 1;
+                            if (pre[mid] <= g) lo = mid;
+                            else hi = mid;
+                        }
+                        off = g - pre[lo];
                     }
-                    v[t] = regq[(int64_t)lo * a.nq * a.rc + (g - pre[lo])];
+                    v[t] = regq[(int64_t)lo * a.nq * a.rc + off];
                     if (PM == 1) v[t] = dot_pair_key(v[t], qmax, a.smallest);
                 }
             }

@@ -1146,6 +1146,7 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, cons
         a.keep_all = i == 0 && p.sh.kind == 1 ? 1 : 0;
         LAUNCH_TRY(launch_mq_pass(p, dop, a, ps.R, rt->stream), "mq_scan");
         sa.R = ps.R;
+        sa.uniform = a.keep_all ? (int)ps.rows_per_wg : 0;
         const bool last = i + 1 == p.passes.size();
         sa.out_ids = last ? out_ids : nullptr;
         sa.out_scores = last ? out_topk_scores : nullptr;
