@@ -410,6 +410,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     __shared__ RadixShared rs;
     __shared__ int wsum[NW];
     __shared__ int wpos, wpos2;
+    __shared__ int cmax_s;
     __shared__ unsigned long long minkey;
     __shared__ int qh_s[PM == 2 ? kMaxQueryDim / 4 : 1];
     __shared__ int ql_s[PM == 2 ? kMaxQueryDim / 4 : 1];
@@ -418,12 +419,14 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     const int q = blockIdx.x;
     const int k = a.k;
 
-    // exclusive prefix of the pass's region counts
-    int carry = 0;
+    // exclusive prefix of the pass's region counts, and their maximum
+    int carry = 0, cmax = 0;
+    if (tid == 0) cmax_s = 0;
     for (int base = 0; base < a.R; base += NT) {
         const int w = base + tid;
         int c = w < a.R ? a.counts[(int64_t)w * a.nq + q] : 0;
         c = c < a.rc ? c : a.rc;
+        cmax = c > cmax ? c : cmax;
         const int incl = wave_incl_scan(c);
         if (lane == 63) wsum[wave] = incl;
         __syncthreads();
@@ -436,10 +439,20 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
         __syncthreads();
     }
     const int M = carry;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const int o = __shfl_xor(cmax, off);
+        cmax = o > cmax ? o : cmax;
+    }
+    if (lane == 0 && cmax > 0) atomicMax(&cmax_s, cmax);
+    if (tid == 0) pre[a.R] = M;
 
     int fill = a.bcnt[q];
     for (int i = tid; i < fill; i += NT) buf[i] = a.best[(int64_t)q * k + i];
     __syncthreads();
+    // regions holding 4 to 64 entries on average and at most: gather region
+    // by region (sparser regions take fewer rounds of loads entry by entry)
+    const bool by_region = a.uniform == 0 && cmax_s <= 64 && M >= 4 * a.R;
 
     // keep the best k of buf[0..fill): the radix prefix, then a block-wide
     // append of the kept keys to the front; the smallest kept key is the
@@ -541,6 +554,36 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     for (int base = 0; base < M;) {
         const int take = (M - base) < (LCAP - fill) ? (M - base) : (LCAP - fill);
         int added = take;  // keys this batch leaves in buf (fewer after pruning)
+        if (by_region) {
+            // Wave w takes regions w, w + NW, ...; lane l moves entry l of
+            // each, 8 regions' loads in flight at once.  Entries outside the
+            // batch [base, base + take) stay for a later batch.
+            for (int w0 = wave; w0 < a.R; w0 += 8 * NW) {
+                uint64_t v[8];
+                int dst[8];
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const int w = w0 + t * NW;
+                    dst[t] = -1;
+                    v[t] = 0;
+                    if (w < a.R) {
+                        const int g = pre[w] + lane;
+                        if (g < pre[w + 1] && g >= base && g < base + take) {
+                            dst[t] = fill + (g - base);
+                            v[t] = regq[(int64_t)w * a.nq * a.rc + lane];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    if (dst[t] < 0) continue;
+                    uint64_t x = v[t];
+                    if (PM == 1) x = dot_pair_key(x, qmax, a.smallest);
+                    if (PM == 2 && prune) x = make_key(__uint_as_float((uint32_t)(x >> 32)), (uint32_t)x, a.smallest);
+                    buf[dst[t]] = x;
+                }
+            }
+        } else {
         // batches of 8 independent loads per thread keep many in flight
         for (int j0 = 0; j0 < take; j0 += 8 * NT) {
             uint64_t v[8];
@@ -577,6 +620,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
                 const int j = j0 + t * NT + tid;
                 if (j < take) buf[fill + j] = v[t];
             }
+        }
         }
         __syncthreads();
         if (PM == 2) {
