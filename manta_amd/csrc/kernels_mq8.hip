@@ -21,7 +21,9 @@
 // bounds (loosened past the exact test's).  The filter of a row pair runs
 // under the MFMAs of the wave's next pair (a chunk's second pair under the
 // next chunk's first).  Only a query block with a passing lane takes the
-// exact f32 test p = fmul_rn(scale, acc) against each query's bound.  A
+// exact f32 test p = fmul_rn(scale, acc), against the loosest bound of the
+// lane's 4 queries (or, for shadow pairs and query counts that are not a
+// multiple of 4, each query's own bound: OWNB).  A
 // pair that passes goes to its query's region as (bits of p) << 32 | row:
 // the division and the key are left to the select kernel, where every lane
 // has one.  Row scales must be finite and not negative (the runtime routes
@@ -55,7 +57,7 @@ constexpr int mq8_nbuf(int tile, int qg, int ch) {
 }
 }  // namespace
 
-template <int KS64, bool SMALL, int WS, bool SHADOW>
+template <int KS64, bool SMALL, int WS, bool SHADOW, bool OWNB>
 __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))) void mq8_scan_kernel(MqArgs a) {
     constexpr int PITCH = KS64 * 64;
     constexpr int CH = kMq8CH * WS;                      // rows per chunk
@@ -236,15 +238,29 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         pm[qb] = fmaxf(v[0], v[1]);
     };
 
-    // The pairs of one query block of a row pair that pass the exact test
-    // against each query's bound, appended as (pre-score, row) pairs (a wave
-    // where one passed the filter): the lane's 8 tests go to a bit mask
-    // first, and the appends loop over its set bits, so a lane pays one LDS
-    // atomic per pair it appends.  (Slots without a query have bound +inf,
-    // or -inf for smallest-k, and never append.)
+    // The pairs of one query block of a row pair that pass the exact test,
+    // appended as (pre-score, row) pairs (a wave where one passed the
+    // filter): the lane's 8 tests go to a bit mask first, and the appends
+    // loop over its set bits, so a lane pays one LDS atomic per pair it
+    // appends.  q8 dot pairs are tested against the loosest bound of the
+    // lane's 4 queries, already in registers (the slot order keeps it close
+    // to each query's own; a pair between the two is a key below the
+    // threshold, which the select drops): a triggered block then waits on one
+    // LDS round trip, the append's, not two.  Shadow pairs, which the select
+    // rescores at a row load each, take each query's own bound (OWNB).
+    // Slots without a query have bound +inf (-inf for smallest-k) and sort
+    // last; a group of 4 slots whose bounds are all infinite has a NaN
+    // loosest bound, which no test passes, and when the query count is not a
+    // multiple of 4 (one group then mixes queries and empty slots) the
+    // runtime launches the OWNB kernel too, so an empty slot never appends.
     auto survivors = [&](const v4i (&acc)[2][4], int qb, int64_t rb0, const float (&sc)[2]) {
-        const float4 b4 = *(const float4*)&bnd_s[lw + qb * 16 + 4 * g];
-        const float bx[4] = {b4.x, b4.y, b4.z, b4.w};
+        float bx[4];
+        if constexpr (OWNB) {
+            const float4 b4 = *(const float4*)&bnd_s[lw + qb * 16 + 4 * g];
+            bx[0] = b4.x, bx[1] = b4.y, bx[2] = b4.z, bx[3] = b4.w;
+        } else {
+            bx[0] = bx[1] = bx[2] = bx[3] = pbr[qb];
+        }
         float pv[8];
         uint32_t mask = 0;
 #pragma unroll
@@ -663,33 +679,40 @@ MqShape mq8_shape(int pitch, int ws, bool shadow) {
     return s;
 }
 
-template <int KS64, bool SMALL, int WS, bool SHADOW>
+template <int KS64, bool SMALL, int WS, bool SHADOW, bool OWNB>
 static hipError_t launch_mq8_one(const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)mq8_scan_kernel<KS64, SMALL, WS, SHADOW>,
+        hipError_t e = hipFuncSetAttribute((const void*)mq8_scan_kernel<KS64, SMALL, WS, SHADOW, OWNB>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((mq8_scan_kernel<KS64, SMALL, WS, SHADOW>), grid, dim3(kMq8Threads), lds, s, a);
+    hipLaunchKernelGGL((mq8_scan_kernel<KS64, SMALL, WS, SHADOW, OWNB>), grid, dim3(kMq8Threads), lds, s, a);
     return hipGetLastError();
 }
 
 template <int KS64>
 static hipError_t launch_mq8_ks(const MqShape& sh, const MqArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     const bool sm = a.smallest != 0;
-#define MANTA_MQ8(SM, W, SH)                                     \
-    if (sm == SM && sh.ws == W && (sh.shadow != 0) == SH)        \
-        return launch_mq8_one<KS64, SM, W, SH>(a, grid, lds, s);
-    MANTA_MQ8(false, 1, false)
-    MANTA_MQ8(true, 1, false)
-    MANTA_MQ8(false, 2, false)
-    MANTA_MQ8(true, 2, false)
-    MANTA_MQ8(false, 1, true)
-    MANTA_MQ8(true, 1, true)
-    MANTA_MQ8(false, 2, true)
-    MANTA_MQ8(true, 2, true)
+    // each query's own bound in the exact test: shadow pairs, and query
+    // counts that leave a group of 4 slots partly empty
+    const bool own = sh.shadow != 0 || (a.nq & 3) != 0;
+#define MANTA_MQ8(SM, W, SH, OB)                                                  \
+    if (sm == SM && sh.ws == W && (sh.shadow != 0) == SH && own == OB)            \
+        return launch_mq8_one<KS64, SM, W, SH, OB>(a, grid, lds, s);
+    MANTA_MQ8(false, 1, false, false)
+    MANTA_MQ8(true, 1, false, false)
+    MANTA_MQ8(false, 2, false, false)
+    MANTA_MQ8(true, 2, false, false)
+    MANTA_MQ8(false, 1, true, true)
+    MANTA_MQ8(true, 1, true, true)
+    MANTA_MQ8(false, 2, true, true)
+    MANTA_MQ8(true, 2, true, true)
+    MANTA_MQ8(false, 1, false, true)
+    MANTA_MQ8(true, 1, false, true)
+    MANTA_MQ8(false, 2, false, true)
+    MANTA_MQ8(true, 2, false, true)
 #undef MANTA_MQ8
     return hipErrorInvalidValue;
 }

@@ -322,11 +322,15 @@ def test_multi_query_all_ties(rt, op):
 
 @pytest.mark.parametrize("smallest", [False, True])
 @pytest.mark.parametrize("nq,n,d,k", [(512, 6000, 384, 50), (600, 5003, 128, 10), (1024, 4500, 256, 1),
-                                      (520, 3000, 384, 300), (256, 6000, 384, 50), (300, 5003, 256, 10)])
+                                      (520, 3000, 384, 300), (256, 6000, 384, 50), (300, 5003, 256, 10),
+                                      (515, 3001, 128, 1500)])
 def test_q8_dot_512_queries_bit_exact(rt, smallest, nq, n, d, k):
     """A full and a partial 512-query group (and 256-query groups for fewer
     than 512 queries), row counts that leave a partial last chunk; ids,
-    scores and accumulators bit-exact."""
+    scores and accumulators bit-exact.  515 queries with k about n/2: the
+    last wave holds 3 queries, so a group of 4 slots mixes queries and empty
+    slots, and the thresholds sit near 0, where an empty slot's zero scores
+    would pass its neighbours' bound."""
     q, codes, scales = _q8_case(nq + n + d + k, nq, n, d, sets=1)
     cands = rt.bind_q8(codes[0], scales[0])
     ids, sc, acc = _qtopk(rt, cands, "dot", rt.to_device(q), k, smallest=smallest, with_acc=True)
