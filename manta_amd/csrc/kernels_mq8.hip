@@ -139,8 +139,36 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
                       __builtin_amdgcn_readfirstlane(sbase + buf * CH * 4 + sw * 256));
         }
     };
-    // the first chunks' loads go out first: the A fragments and the query
-    // state load under them
+    // Lane L's query (q0 + lw + L): its threshold and bound, loaded first
+    // and retired before the chunk loads go out (behind those, a few
+    // megabytes of chunks per XCD, they would take microseconds); the empty
+    // asm keeps the query constants' load beside tau's (the bound reads them
+    // only when tau is set), so one wait covers both.
+    auto bound_of = [&](int q, uint64_t& tk) {
+        tk = a.tau[q];
+        if (SHADOW) {
+            const float m = a.qbound[2 * q], f = a.qbound[2 * q + 1];
+            asm volatile("" ::"v"(m), "v"(f));
+            return shadow_bound(tk, m, f, SMALL);
+        }
+        const QConst qc = a.qconst[q];
+        asm volatile("" ::"v"(qc.a));
+        return mq_bound<OP_DOT>(tk, qc, SMALL);
+    };
+    uint64_t my_tau = ~0ull;
+    float my_bnd = SMALL ? -__builtin_inff() : __builtin_inff();
+    uint32_t ord = 0xFFFFFFFFu;  // missing queries go last
+    {
+        const int q = q0 + lw + lane;
+        if (q < a.nq) {
+            my_bnd = bound_of(q, my_tau);
+            const uint32_t u = __float_as_uint(my_bnd);
+            ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+            ord = ord == 0xFFFFFFFFu ? 0xFFFFFFFEu : ord;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    // then the first chunks' loads; the sort and the A fragments run under them
 #pragma unroll
     for (int b = 0; b < NBUF - 1; b++)
         if (r0 + b * CH < r1) issue_chunk(r0 + b * CH, b);
@@ -149,20 +177,8 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
     // the lanes): slot lw + L takes the L-th, so the 4 queries a lane filters
     // together have nearly equal bounds.  Both wave groups of WS = 2 sort the
     // same queries the same way.
-    auto bound_of = [&](int q) {
-        const QConst qc = a.qconst[q];
-        const uint64_t tk = a.tau[q];
-        return SHADOW ? shadow_bound(tk, a.qbound[2 * q], a.qbound[2 * q + 1], SMALL) : mq_bound<OP_DOT>(tk, qc, SMALL);
-    };
     uint64_t skey;
     {
-        const int q = q0 + lw + lane;
-        uint32_t ord = 0xFFFFFFFFu;  // missing queries go last
-        if (q < a.nq) {
-            const uint32_t u = __float_as_uint(bound_of(q));
-            ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-            ord = ord == 0xFFFFFFFFu ? 0xFFFFFFFEu : ord;
-        }
         skey = ((uint64_t)ord << 32) | (uint32_t)lane;
 #pragma unroll
         for (int k = 2; k <= 64; k <<= 1)
@@ -187,13 +203,16 @@ __global__ __launch_bounds__(kMq8Threads) __attribute__((amdgpu_waves_per_eu(2))
         for (int ks = 0; ks < KS64; ks++) av[qb][ks] = ok ? *(const v4i*)(src + ks * 64) : v4i{0, 0, 0, 0};
     }
 
-    // slot i = tid: the wave that owns slot i runs this thread
+    // slot i = tid: the wave that owns slot i runs this thread (its query's
+    // threshold and bound from the lane that loaded them)
+    const uint64_t src_tau = ((uint64_t)(uint32_t)__shfl((int)(my_tau >> 32), my_src) << 32) |
+                             (uint32_t)__shfl((int)(uint32_t)my_tau, my_src);
+    const float src_bnd = __shfl(my_bnd, my_src);
     if (tid < QG) {
         const int i = tid;
         const int q = q0 + lw + my_src;
-        const bool ok = q < a.nq;
-        tau_s[i] = ok ? a.tau[q] : ~0ull;
-        const float b = ok ? bound_of(q) : (SMALL ? -__builtin_inff() : __builtin_inff());
+        tau_s[i] = src_tau;
+        const float b = src_bnd;
         bnd_s[i] = b;
         qmap_s[i] = q;
         cnt_s[i] = 0;
