@@ -23,6 +23,7 @@ scores on packed data with heap top-k on all host cores.
 from __future__ import annotations
 
 import argparse
+import math
 import json
 import os
 import sys
@@ -34,6 +35,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 N, D, K = 65536, 256, 10
+# the per-config lines time at least this long (more steps than --steps when
+# a step is short); the C0 headline times exactly --steps
+MIN_TIMED_S = 0.02
 
 
 def c0_bytes_per_problem(n=N, d=D, k=K) -> int:
@@ -146,7 +150,7 @@ I8_PEAK = 5033.0           # dense i8 MFMA TOP/s
 F32_PEAK = 157.3           # dense f32 MFMA TFLOP/s
 
 
-def _timed(rt, fn, steps, warmup, families, min_warm_s=0.5):
+def _timed(rt, fn, steps, warmup, families, min_warm_s=0.5, min_timed_s=0.0):
     """Run fn warmup times, then time exactly `steps` calls with no per-launch
     instrumentation: seconds per step on the host clock (synchronized on both
     sides) and device ms per step from two HIP events on the runtime's stream
@@ -156,7 +160,10 @@ def _timed(rt, fn, steps, warmup, families, min_warm_s=0.5):
     microseconds to a launch, which is why the timed run has none.)  The
     warmup runs at least
     min_warm_s seconds: the part's clocks take a few hundred milliseconds of
-    load to settle, and steps timed before that read up to 15% slower."""
+    load to settle, and steps timed before that read up to 15% slower.
+    With min_timed_s > 0 the timed run takes at least that long (more steps
+    than `steps` when a step is short), so the synchronize around it does
+    not weigh on the per-step time; the count timed comes back last."""
     t_w = time.perf_counter()
     done = 0
     while done < warmup or time.perf_counter() - t_w < min_warm_s:
@@ -165,9 +172,13 @@ def _timed(rt, fn, steps, warmup, families, min_warm_s=0.5):
         if done >= warmup:
             rt.synchronize()
     rt.synchronize()
+    est = (time.perf_counter() - t_w) / max(done, 1)  # per step, synchronizes included (an upper bound)
+    nt = steps
+    if min_timed_s > 0.0 and est * steps < min_timed_s:
+        nt = int(math.ceil(min_timed_s / est))
     t0 = time.perf_counter()
     rt.span(False)
-    for _ in range(steps):
+    for _ in range(nt):
         fn()
     span_ms = rt.span(True)
     rt.synchronize()
@@ -184,7 +195,7 @@ def _timed(rt, fn, steps, warmup, families, min_warm_s=0.5):
         fam[f] = (n / steps, ms / max(n, 1), ms / steps)
     rt.set_timing(False)
     rt.timing(reset=True)
-    return el / steps, fam, span_ms / steps
+    return el / nt, fam, span_ms / nt, nt
 
 
 def _kernels(fam) -> dict:
@@ -201,8 +212,8 @@ def run_c1(rt, steps, warmup, cpu_s) -> dict:
     d, e = proj.shape
     td, md, tbd, pd = (rt.to_device(x) for x in (tokens, mask, table, proj))
     out = rt.empty((b, e), np.uint16)
-    step_s, fam, dev_ms = _timed(rt, lambda: rt.embed_pooled(td, md, tbd, pd, out=out), steps, warmup,
-                                 ["embed", "embed_transpose", "embed_finalize"])
+    step_s, fam, dev_ms, nt = _timed(rt, lambda: rt.embed_pooled(td, md, tbd, pd, out=out), steps, warmup,
+                                     ["embed", "embed_transpose", "embed_finalize"], min_timed_s=MIN_TIMED_S)
     flops = 2.0 * b * t * d * e
     # one launch per step: the uninstrumented run's device time per step
     # bounds the kernel's (it adds only the gap between back-to-back
@@ -213,7 +224,7 @@ def run_c1(rt, steps, warmup, cpu_s) -> dict:
     achieved = flops / (k_ms / 1000.0) / 1e12
     return {
         "workload": "c1_embed_f16", "shape": {"b": b, "t": t, "vocab": table.shape[0], "d": d, "e": e},
-        "value": b * t / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0,
+        "value": b * t / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0, "timed_steps": nt,
         "device_ms_per_step": dev_ms,
         "roofline": {"bound": "mfma", "kernel": "embed_gemm4_kernel (f16 MFMA 32x32x16, 128x96 tiles, LDS transpose "
                                                 "reads of the projection, finalize fused)",
@@ -261,13 +272,13 @@ def run_c2(rt, steps, warmup, cpu_s) -> dict:
     ids = rt.empty((nq, k), np.int32)
     sc = rt.empty((nq, k), np.float32)
     fams = ["mq_scan", "mq_select", "q4_scan", "topk_merge", "query_encode", "mq_clear", "ref_rescore", "ref_finish", "ref_scan"]
-    step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "cosine", qd, k, out=(ids, sc, None)),
-                                 steps, warmup, fams)
+    step_s, fam, dev_ms, nt = _timed(rt, lambda: rt.score_topk(cands, "cosine", qd, k, out=(ids, sc, None)),
+                                     steps, warmup, fams, min_timed_s=MIN_TIMED_S)
     # the presets' step after top-k: candidate ids, packed rows and scales of
     # the selected rows
     cid = rt.to_device(np.arange(n, dtype=np.int64) * 7 + 3)
-    pack_s, pfam, _ = _timed(rt, lambda: rt.pack_candidates(cands, ids, cid), steps, warmup, ["pack_candidates"],
-                             min_warm_s=0.1)
+    pack_s, pfam, _, _ = _timed(rt, lambda: rt.pack_candidates(cands, ids, cid), steps, warmup, ["pack_candidates"],
+                                min_warm_s=0.1, min_timed_s=MIN_TIMED_S)
     pack_bytes = nq * k * (4 + 8 + d // 2 + d // 16 + 8 + d // 2 + d // 16)  # reads + writes
     dom = "mq_scan" if fam["mq_scan"][0] else "q4_scan"
     # the scan reads the q4 matrix's int8 shadow: 384 code bytes and one f32
@@ -280,7 +291,7 @@ def run_c2(rt, steps, warmup, cpu_s) -> dict:
     return {
         "workload": "c2_q4_cosine_top100", "shape": {"q": nq, "n": n, "d": d, "k": k},
         "semantics": "reference cosineRows on the dequantized q4 values (ids and scores bit-exact)",
-        "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0,
+        "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0, "timed_steps": nt,
         "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         # The contraction is Q x N x D against f16 queries: priced at the f16
         # MFMA peak (the exact two-int8-digit split would execute twice the
@@ -341,8 +352,9 @@ def run_c3(rt, steps, warmup, cpu_s) -> dict:
     ids = rt.empty((nq, k), np.int32)
     sc = rt.empty((nq, k), np.float32)
     fams = ["mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear", "ref_rescore", "ref_finish", "ref_scan"]
-    step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "l2_distance", qd, k, smallest=True,
-                                                           out=(ids, sc, None)), steps, warmup, fams)
+    step_s, fam, dev_ms, nt = _timed(rt, lambda: rt.score_topk(cands, "l2_distance", qd, k, smallest=True,
+                                                               out=(ids, sc, None)), steps, warmup, fams,
+                                     min_timed_s=MIN_TIMED_S)
     dom = "mq_scan" if fam["mq_scan"][0] else "q8_scan"
     nbytes = n * (d + 4) + nq * d * 2 + nq * k * 8
     achieved = nbytes / (fam[dom][2] / 1000.0) / 1e9
@@ -350,7 +362,7 @@ def run_c3(rt, steps, warmup, cpu_s) -> dict:
     return {
         "workload": "c3_q8_l2_smallest1000", "shape": {"q": nq, "n": n, "d": d, "k": k},
         "semantics": "reference l2DistanceRows on the dequantized q8 values (ids and scores bit-exact)",
-        "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0,
+        "value": nq * n / step_s, "unit": "candidates/s", "ms_per_step": step_s * 1000.0, "timed_steps": nt,
         "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK, "scan_us_per_step": fam[dom][2] * 1000.0,
@@ -411,7 +423,7 @@ def run_c4(rt, steps, warmup, cpu_s) -> dict:
         rt.score_topk(cands, "dot", emb, k, out=(ids, sc, None), quantized=True)
 
     fams = ["embed", "embed_transpose", "embed_finalize", "mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
-    step_s, fam, dev_ms = _timed(rt, step, steps, warmup, fams)
+    step_s, fam, dev_ms, nt = _timed(rt, step, steps, warmup, fams, min_timed_s=MIN_TIMED_S)
     flops_a = 2.0 * b * t * d * e
     ops_b = 2.0 * b * n * d
     emb_t = flops_a / (fam["embed"][1] / 1000.0) / 1e12
@@ -422,7 +434,7 @@ def run_c4(rt, steps, warmup, cpu_s) -> dict:
         "workload": "c4_embed_q8proj_then_q8dot_top50", "shape": {"q": b, "t": t, "d": d, "n": n, "k": k},
         "semantics": "BASELINE's q8 dot formula (query codes round(q*127), int32 accumulation)",
         "value": b * n / step_s, "unit": "candidates/s (end to end, embed included)",
-        "ms_per_step": step_s * 1000.0, "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
+        "ms_per_step": step_s * 1000.0, "timed_steps": nt, "device_ms_per_step": dev_ms, "kernels": _kernels(fam),
         "embed": {"tokens_per_s_kernel": b * t / (fam["embed"][1] / 1000.0),
                   "roofline": {"bound": "mfma", "achieved": emb_t, "peak": F16_PEAK, "unit": "TFLOP/s",
                                "frac": emb_t / F16_PEAK, "avg_launch_us": fam["embed"][1] * 1000.0}},
@@ -484,14 +496,15 @@ def run_enc(rt, steps, warmup, cpu_s) -> dict:
     out = rt.empty((b, d), np.uint16)
     fams = ["encoder_gather", "encoder_gemm", "encoder_attention", "encoder_softmax", "encoder_layernorm",
             "normalize", "mean_pool", "encoder_out"]
-    step_s, fam, dev_ms = _timed(rt, lambda: rt.encoder_pooled(td, md, tcd, tsd, dev, out=out), steps, warmup, fams)
+    step_s, fam, dev_ms, nt = _timed(rt, lambda: rt.encoder_pooled(td, md, tcd, tsd, dev, out=out), steps, warmup,
+                                     fams, min_timed_s=MIN_TIMED_S)
     r = b * t
     gemm_flops = 2.0 * r * d * d * 4 + 2.0 * r * d * h * 2
     attn_flops = 2.0 * 2.0 * b * t * t * d
     gemm_us = fam["encoder_gemm"][2] * 1000.0
     return {
         "workload": "enc_encoder_trainable_q8_pooled", "shape": {"b": b, "t": t, "vocab": vocab, "d": d, "h": h},
-        "value": r / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0, "device_ms_per_step": dev_ms,
+        "value": r / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0, "timed_steps": nt, "device_ms_per_step": dev_ms,
         "kernels": _kernels(fam),
         "roofline": {"bound": "mfma", "kernel": "enc_gemm_mfma_kernel (f32 MFMA 32x32x2, 64x64 tiles; q/k/v/o, "
                                                 "ffn_up, projection)",
@@ -513,9 +526,9 @@ def run_c0(rt, args) -> dict:
     ids = rt.empty((args.sets, K), np.int32)
     sc = rt.empty((args.sets, K), np.float32)
     # the headline: exactly W untimed warmup steps, then K timed ones
-    step_s, fam, dev_ms = _timed(rt, lambda: rt.score_topk(cands, "dot", q_dev, K, out=(ids, sc, None),
-                                                           quantized=True),
-                                 args.steps, args.warmup, ["q8_scan"], min_warm_s=0.0)
+    step_s, fam, dev_ms, _ = _timed(rt, lambda: rt.score_topk(cands, "dot", q_dev, K, out=(ids, sc, None),
+                                                              quantized=True),
+                                    args.steps, args.warmup, ["q8_scan"], min_warm_s=0.0)
     # one fused launch per step: the uninstrumented run's device time per
     # step (two HIP events around the K timed steps) bounds the kernel's
     # duration; the per-launch event figure is the other bound
@@ -529,8 +542,8 @@ def run_c0(rt, args) -> dict:
     q1 = rt.to_device(queries[:1])
     one = rt.bind_q8(codes[0], scales[0])
     ids1 = rt.empty((1, K), np.int32)
-    single_s, _, _ = _timed(rt, lambda: rt.score_topk(one, "dot", q1, K, out=(ids1, None, None), quantized=True),
-                            200, 5, [])
+    single_s, _, _, _ = _timed(rt, lambda: rt.score_topk(one, "dot", q1, K, out=(ids1, None, None), quantized=True),
+                               200, 5, [])
     line = {
         "metric": "candidates scored/sec (q8 dot + top-k, BASELINE config 0 shape)",
         "value": args.sets * N / step_s,
