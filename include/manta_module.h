@@ -8,7 +8,8 @@
  *   manta_module_decode_json   <- mantaartifact.DecodeJSON (artifact/manta/module.go:494-505)
  *   manta_module_decode_mll    <- mantaartifact.DecodeMLL  (artifact/manta/mll.go:291-305)
  *   manta_module_encode_json   <- mantaartifact.EncodeJSON (module.go:486-492)
- *   manta_module_encode_mll    <- mantaartifact.EncodeMLL  (mll.go:94-289; see the function)
+ *   manta_module_encode_mll    <- the XMTA / HEAD / STRG part of mantaartifact.EncodeMLL
+ *                                 (mll.go:94-289); not a full replacement (see the function)
  *   manta_module_validate      <- (*Module).Validate       (module.go:255-424)
  *   manta_module_validate_*    <- validateScoreEntry (runtime/score_model.go:276-324),
  *                                 validateRetrievalEntry (runtime/retrieval_model.go:274-330),
@@ -57,9 +58,14 @@ const char* manta_module_name(const MantaModule* m);
 int manta_module_encode_json(const MantaModule* m, char** out, size_t* len, char** err);
 /* A container holding the module: HEAD (name, description "Manta module
  * artifact", artifact_version, supported_backends, capabilities, param /
- * entry / kernel counts), STRG, the typed DIMS / TYPE / PARM / ENTR / TNSR /
- * SCHM tables written empty, and XMTA with the MLLMetadata JSON -- what
- * DecodeMLL reads.  *out is malloc'd (manta_module_free_buffer). */
+ * entry / kernel counts), STRG, and XMTA with the MLLMetadata JSON -- what
+ * DecodeMLL reads, so a container written here decodes to the same module
+ * there and here.  It differs from EncodeMLL's output: the typed DIMS /
+ * TYPE / PARM / ENTR / TNSR / SCHM tables are written empty and the BUFF /
+ * KRNL sections are left out (their layout belongs to the unvendored mll
+ * codec and no reference container carries them filled), so a tool that
+ * reads the typed tables sees none.  *out is malloc'd
+ * (manta_module_free_buffer). */
 int manta_module_encode_mll(const MantaModule* m, void** out, size_t* len, char** err);
 void manta_module_free_buffer(void* p);
 
@@ -149,7 +155,14 @@ typedef struct MantaRocmProgram MantaRocmProgram;
 int manta_rocm_program_load(MantaRocm* rt, const MantaModule* m, MantaRocmProgram** out, char** err);
 void manta_rocm_program_destroy(MantaRocmProgram* p);
 /* Bind a param's weight (WeightBinding): a device tensor or bound candidates
- * named after the param; the caller keeps the memory alive. */
+ * named after the param; the caller keeps the memory alive.  Steps read the
+ * bound memory on every run, except matmul: an f16 or q8 [K, N] weight with
+ * K % 32 == 0 and N % 128 == 0 is copied once, here, into the transposed f16
+ * operand the pipelined GEMM reads (owned by the program), as the CUDA
+ * backend uploads its resident matmul params once at Load
+ * (bindResidentMatMulParams, runtime/backends/cuda/cuda.go:129-169).  A
+ * weight changed in place after bind must therefore be bound again: binding
+ * the same name replaces the copy. */
 int manta_rocm_program_bind(MantaRocmProgram* p, const MantaRocmValue* value, char** err);
 /* MANTA_ROCM_OK when every step of `entry` runs on device, else
  * MANTA_ROCM_UNSUPPORTED naming the first step that does not (the caller

@@ -33,16 +33,14 @@ struct Value {
     std::vector<Value> items;
     std::vector<std::pair<std::string, Value>> members;
 
-    // Last member named `key` (exact match), else the last ASCII
-    // case-insensitive match (Unmarshal's field matching), else null.
+    // The last member, in document order, whose name is `key` or equals it
+    // under ASCII case folding, else null: Unmarshal maps every such key to
+    // the same struct field and each one overwrites it, so the last wins.
     const Value* get(const char* key) const {
-        const Value* exact = nullptr;
-        const Value* folded = nullptr;
-        for (const auto& m : members) {
-            if (m.first == key) exact = &m.second;
-            else if (fold_equal(m.first, key)) folded = &m.second;
-        }
-        return exact ? exact : folded;
+        const Value* last = nullptr;
+        for (const auto& m : members)
+            if (m.first == key || fold_equal(m.first, key)) last = &m.second;
+        return last;
     }
     static bool fold_equal(const std::string& a, const char* b) {
         size_t n = strlen(b);

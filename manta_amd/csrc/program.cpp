@@ -13,22 +13,28 @@
 //                    candidate pack kernel for rows of bound q8 / q4
 //                    candidates (docs gathered by top-k indices)
 //   pack_candidates  ids, scores and gathered rows as one candidate_pack
-//   matmul           the f16 MFMA GEMM (f32 out)
+//   matmul           the f16 MFMA GEMM for f16 / q8 operands, the f32 MFMA
+//                    GEMM for f32 ones, batched products per sequence
+//                    (f32 out)
 //   topk             the device top-k over an f32 score matrix
 //   dequant          the value relabelled f16, as the reference's clone
+//   transpose        the last two axes swapped (kernels_exec transpose)
 //   launch_kernel    the kernel's body ops in order (executeKernel,
 //                    tensor_ops.go:476-516): dot / cosine / l2_distance on
 //                    bound candidates with the reference's arithmetic,
-//                    normalize / rmsnorm, mean_pool (masked or not)
+//                    normalize / rmsnorm, mean_pool (masked or not),
+//                    softmax and layernorm over rows, gelu, and the
+//                    element-wise binary_add / _sub / _mul / _div
 //   return           the entry's outputs
 //
 // A score kernel whose only consumers are one topk step and gathers of the
 // scores by that topk's indices is not materialized: the topk step runs the
 // fused score + top-k (manta_rocm_score_topk, whose scores are the
 // reference's bit for bit) and the gathers take its top scores.  Steps and
-// ops outside this set (transpose, softmax, layernorm, kv_cache, image
-// ops, ...) return MANTA_ROCM_UNSUPPORTED: the Go backend runs such entries
-// through ExecuteSymbolic with per-kernel dispatch instead.
+// ops outside this set (kv_cache, image ops, ...) return
+// MANTA_ROCM_UNSUPPORTED (manta_rocm_program_supports names the first such
+// step): the Go backend runs such entries through ExecuteSymbolic with
+// per-kernel dispatch instead.
 //
 // Values live in device memory owned by the program: one buffer per
 // allocation site of an entry, reused (and grown) by later runs of the same

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -534,15 +535,15 @@ int manta_rocm_pack_grid(const float* x, int64_t n, int64_t d, int bits, int8_t*
         return MANTA_ROCM_OK;
     }
     // a grid per row (e.g. rows packed per row and dequantized)
-    bool rows_ok = true;
+    std::atomic<bool> rows_ok{true};  // shared by the workers: any row off its grid stops them all
     parallel_rows(n, [&](int64_t a, int64_t b) {
-        for (int64_t r = a; r < b && rows_ok; r++) {
+        for (int64_t r = a; r < b && rows_ok.load(std::memory_order_relaxed); r++) {
             const float sr = manta::grid_scale(x + r * d, d, levels, codes + r * d);
-            if (sr < 0.0f) rows_ok = false;
+            if (sr < 0.0f) rows_ok.store(false, std::memory_order_relaxed);
             scales[r] = sr;
         }
     });
-    if (rows_ok) {
+    if (rows_ok.load()) {
         *grid = 1;
         return MANTA_ROCM_OK;
     }

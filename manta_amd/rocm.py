@@ -255,6 +255,17 @@ class Runtime:
         (ids, scores or None, accumulators or None) device arrays."""
         nq = self._query_rows(cands, queries)
         ids, sc, acc = out
+        # the kernels write nq x k entries through these pointers: a buffer
+        # of another shape or element size would be written out of bounds
+        for name, arr, dt, need in (("ids", ids, np.int32, True), ("scores", sc, np.float32, False),
+                                    ("acc", acc, np.int64, False)):
+            if arr is None:
+                if need:
+                    raise ValueError("score_topk_noalloc: ids output is required")
+                continue
+            if tuple(arr.shape) != (nq, k) or np.dtype(arr.dtype) != np.dtype(dt):
+                raise ValueError("score_topk_noalloc: %s must be (%d, %d) %s, got %s %s"
+                                 % (name, nq, k, np.dtype(dt).name, tuple(arr.shape), np.dtype(arr.dtype).name))
         call("manta_rocm_score_topk_noalloc", self.handle, cands.handle, C.c_int(self._op(op, quantized)),
              C.c_int(_lib.SMALLEST if smallest else _lib.LARGEST), queries.ptr, C.c_int64(nq), C.c_int64(k),
              ids.ptr, _ptr(sc), _ptr(acc))

@@ -371,6 +371,44 @@ def test_program_outputs_reused_across_runs(rt):
             assert out["ids"].tolist() == first["ids"].tolist()
 
 
+def test_rebind_refreshes_prepared_weight(rt):
+    """A [K, N] matmul weight is copied into the GEMM's operand when it is
+    bound, as the CUDA backend's resident matmul params are uploaded once at
+    Load (cuda.go:129-169): a weight changed in place keeps the bound copy
+    until it is bound again, and binding it again gives the new weight's
+    results (those of a program that never saw the old one)."""
+    b, t, vocab, d, e = 3, 16, 200, 64, 128  # K % 32 == 0, N % 128 == 0: prepared at bind
+    table = synth.normal_f16(37, 0, vocab, d, 0.02)
+    p1 = synth.normal_f16(37, 1, d, e, 1.0 / 8.0)
+    p2 = synth.normal_f16(37, 2, d, e, 1.0 / 8.0)
+    tokens = synth.uniform_i32(37, 3, b * t, 0, vocab).reshape(b, t)
+
+    def run(p):
+        return p.run("embed_pooled_batch", {"tokens": tokens})["result"]
+
+    def fresh(proj):
+        p = program(rt, "tiny_embed_pooled")
+        p.bind("token_embedding", table)
+        p.bind("projection", proj)
+        return run(p)
+
+    want1, want2 = fresh(p1), fresh(p2)
+    assert not np.array_equal(want1, want2)
+    p = program(rt, "tiny_embed_pooled")
+    p.bind("token_embedding", table)
+    dev = rt.to_device(p1)
+    p.bind("projection", dev)
+    np.testing.assert_array_equal(run(p), want1)
+    dev.upload(p2)  # changed in place, not bound again: the bound copy stays
+    np.testing.assert_array_equal(run(p), want1)
+    p.bind("projection", dev)
+    np.testing.assert_array_equal(run(p), want2)
+    # the oracle agrees with the new weight's result within the GEMM's bound
+    x = orc.gather_rows(orc.f16_to_f32(table), tokens.reshape(-1))
+    yr = orc.normalize_rows(orc.matmul(x, orc.f16_to_f32(p2))).reshape(b, t, e)
+    assert np.max(np.abs(want2 - orc.mean_pool_masked(yr, np.ones((b, t), np.int32)))) < 2e-5
+
+
 def _encoder_case(seed, b, t, vocab, d, h):
     rng = np.random.default_rng(seed)
     tokens = rng.integers(0, vocab, size=(b, t), dtype=np.int32)

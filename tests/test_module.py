@@ -200,6 +200,14 @@ def test_json_decoding_rules():
     assert got["name"] == "tiny_score"
     assert got["params"][0]["binding"] == "weights/docs"
     assert "unknown_field" not in got
+    # an exact key followed by a case-folded one: Unmarshal assigns both to
+    # the field in document order, so the folded one (last) wins
+    text = json.dumps(fixture("tiny_score")).replace('"name": "tiny_score"',
+                                                     '"name": "tiny_score", "NAME": "renamed"', 1)
+    assert json.loads(Module.from_json(text).to_json())["name"] == "renamed"
+    text = json.dumps(fixture("tiny_score")).replace('"name": "tiny_score"',
+                                                     '"NAME": "renamed", "name": "tiny_score"', 1)
+    assert json.loads(Module.from_json(text).to_json())["name"] == "tiny_score"
     # Go's HTML-safe escaping on output
     m = fixture("ref_demo")
     m["kernels"][0]["variants"][0]["source"] = "a<b>&c "

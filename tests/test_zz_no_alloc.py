@@ -71,3 +71,24 @@ def test_noalloc_refuses_a_call_past_its_scratch_and_recovers():
         np.testing.assert_array_equal(out2[0].download(), ids.download())
         np.testing.assert_array_equal(out2[1].download(), sc.download())
         cands.close()
+
+
+def test_noalloc_checks_output_shapes_before_the_call():
+    print("noalloc output checks", flush=True)
+    with rocm.Runtime(0) as rt:
+        q, codes, scales = _case(4, 3, 3000, 64, 1)
+        cands = rt.bind_q8(codes, scales)
+        qd = rt.to_device(q)
+        for out in ((rt.empty((3, 9), np.int32), None, None),           # k too small
+                    (rt.empty((2, 10), np.int32), None, None),          # too few queries
+                    (rt.empty((3, 10), np.int64), None, None),          # wrong element size
+                    (rt.empty((3, 10), np.int32), rt.empty((3, 10), np.float64), None),
+                    (rt.empty((3, 10), np.int32), None, rt.empty((3, 10), np.int32)),
+                    (None, None, None)):
+            with pytest.raises(ValueError, match="score_topk_noalloc"):
+                rt.score_topk_noalloc(cands, "dot", qd, 10, out, quantized=True)
+        out = (rt.empty((3, 10), np.int32), None, None)
+        rt.score_topk_noalloc(cands, "dot", qd, 10, out, quantized=True)
+        ids, _, _ = rt.score_topk(cands, "dot", qd, 10, quantized=True)
+        np.testing.assert_array_equal(out[0].download(), ids.download())
+        cands.close()
