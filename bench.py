@@ -226,11 +226,16 @@ def run_c1(rt, steps, warmup, cpu_s) -> dict:
         "workload": "c1_embed_f16", "shape": {"b": b, "t": t, "vocab": table.shape[0], "d": d, "e": e},
         "value": b * t / step_s, "unit": "tokens/s", "ms_per_step": step_s * 1000.0, "timed_steps": nt,
         "device_ms_per_step": dev_ms,
-        "roofline": {"bound": "mfma", "kernel": "embed_gemm4_kernel (f16 MFMA 32x32x16, 128x96 tiles, LDS transpose "
-                                                "reads of the projection, finalize fused)",
+        "roofline": {"bound": "mfma", "kernel": "embed_gemm7_kernel (f16 MFMA 32x32x16; 128 rows x 96 columns per "
+                                                "workgroup, one round of loads: table rows gathered straight to "
+                                                "registers, projection slice direct to LDS and read as stored through "
+                                                "transpose reads; finalize fused)",
                      "achieved": achieved, "peak": F16_PEAK, "unit": "TFLOP/s", "frac": achieved / F16_PEAK,
                      "avg_launch_us": k_ms * 1000.0, "event_timed_launch_us": fam["embed"][1] * 1000.0,
                      "flops_per_launch": flops,
+                     "bytes_per_launch": b * t * (4 + 4 + d * 2) + d * e * 2 + b * e * 2,
+                     "traffic": profiled_traffic("embed_gemm7_c1_embed_f16.md"),
+                     "traffic_source": "profiles/embed_gemm7_c1_embed_f16.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                      "note": "flops counted over all B*T positions (masked ones included), as the reference computes them"},
         "finalize_us": fam["embed_finalize"][1] * 1000.0,
         "transpose_us": fam["embed_transpose"][1] * 1000.0,
@@ -305,6 +310,9 @@ def run_c2(rt, steps, warmup, cpu_s) -> dict:
                      "scan_us_per_step": fam[dom][2] * 1000.0, "ops_per_step": ops,
                      "executed_i8_frac": ops / (fam[dom][2] / 1000.0) / 1e12 / I8_PEAK,
                      "hbm_GB_s": achieved, "hbm_frac": achieved / HBM_PEAK, "shadow_bytes_per_step": nbytes,
+                     "traffic": profiled_traffic("mq8_shadow_c2_q4_cosine_top100.md", "traffic_bytes_per_step"),
+                     "traffic_source": "profiles/mq8_shadow_c2_q4_cosine_top100.md (rocprofv3 --pmc FETCH_SIZE, "
+                                       "WRITE_SIZE; all scan passes of a step)",
                      "note": "all threshold passes of the scan together cover the N rows once; survivors are "
                              "rescored with the exact 16-bit-query q4 score in mq_select, and the best "
                              "k + k/16 with the reference arithmetic in ref_finish; step_frac prices the whole "
@@ -440,6 +448,10 @@ def run_c4(rt, steps, warmup, cpu_s) -> dict:
                                "frac": emb_t / F16_PEAK, "avg_launch_us": fam["embed"][1] * 1000.0}},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": sc_t, "peak": I8_PEAK, "unit": "TOP/s",
                      "frac": sc_t / I8_PEAK, "scan_us_per_step": fam[dom][2] * 1000.0, "ops_per_step": ops_b,
+                     "bytes_per_step": n * (d + 4) + b * d * 2 + b * k * 8,
+                     "traffic": profiled_traffic("mq8_scan_c4_dot_top50.md", "traffic_bytes_per_step"),
+                     "traffic_source": "profiles/mq8_scan_c4_dot_top50.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
+                                       "all scan passes of a step)",
                      "note": "all threshold passes of the scan together cover the N rows once"},
         **c4_cpu(tokens, mask, table, pcodes, cs, codes, scales, k, cpu_s),
     }

@@ -292,6 +292,13 @@ hipError_t launch_embed_gemm3(const EmbedArgs& a, bool gather, bool pool, hipStr
 // The pooled embed of embed_gemm3 with 128-row x 96-column tiles
 // (tiles_per_seq = ceil(T / 128); same requirements, P and tickets).
 hipError_t launch_embed_gemm4(const EmbedArgs& a, hipStream_t s);
+// The same pooled embed with every operand loaded in one round (the
+// projection slice to LDS, the gathered rows to registers): N == 384,
+// K % 64 == 0, K <= 512; tiles_per_seq = ceil(T / 128); P holds
+// [batches*tiles_per_seq][N] partial sums followed by [batches*tiles_per_seq]
+// unmasked counts.
+bool embed_gemm7_supported(const EmbedArgs& a);
+hipError_t launch_embed_gemm7(const EmbedArgs& a, hipStream_t s);
 // Pooled embed with the projection pre-transposed (launch_embed_transpose_b)
 // for N == 384, K % 32 == 0, T in {64, 128, 256} and batches*T a multiple of
 // 256: 256-row workgroups of whole sequences finish their embeddings in one

@@ -915,6 +915,246 @@ hipError_t launch_embed_gemm4(const EmbedArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Pooled embed for small batches (C1: 64 sequences of 128 tokens), one round
+// of loads per workgroup.  Grid: 128-row tiles x 4 column slices of 96 (256
+// workgroups at C1: one per CU, and workgroups that all start within about a
+// microsecond -- a grid four times larger takes about 5 us just to start).
+// A workgroup loads everything it multiplies at once, as its first act: the
+// tokens and mask of its rows, then the 128 gathered table rows straight
+// into VGPRs (a wave's 32 rows, the whole of K: K/4 registers a lane) and
+// the projection slice (all K rows x 192 bytes of [K][N], read as stored)
+// direct to LDS.  Table row loads are made contiguous by numbering k inside
+// each 64-k block so that MFMA step s (0..3) of k-half h takes k = 32h + 8s
+// + 0..7: lane (row r, half h) holds table[r][64b + 32h .. +31] for block b,
+// 64 bytes, and the projection's transpose reads address the same k rows.
+// The mask of the lane's row is loaded with its token, so after the MFMAs
+// the pooling needs no further load (a wave ballot gives every lane the
+// liveness of its 16 accumulator rows).  Each workgroup publishes its masked
+// column sums (and the tile's unmasked count) to P; the last workgroup of a
+// sequence adds them in tile order, pools, normalizes and writes the f16
+// embedding.  (Splitting K instead of rows across the 4 waves reads the
+// projection from LDS once instead of four times, but needs 351 registers a
+// lane for 12 accumulator tiles and measured slower: 12.7 against 10.6 us.)
+constexpr int E7_WM = 128, E7_WN = 96, E7_BROW = E7_WN * 2;
+
+template <int NB>
+__global__ __launch_bounds__(256) void embed_gemm7_kernel(EmbedArgs a, int xcd_map) {
+    constexpr int K = NB * 64;
+    constexpr int NBL = K * E7_BROW / 1024;  // 1 KB wave loads of the projection slice
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [K][96] f16
+    __shared__ float rowv[E3_N];
+    __shared__ float colw[4][E7_WN];
+    __shared__ double dred[4];
+    __shared__ int ired[4];
+    __shared__ int last;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    int64_t tile;
+    int slice;
+    if (xcd_map) {
+        // workgroups are dealt to the 8 XCDs round robin: the 4 slices of a
+        // tile go to one XCD, so the table rows one slice reads are in that
+        // XCD's L2 for the other three
+        const int64_t x = blockIdx.x, y = x >> 3;
+        slice = (int)(y & 3);
+        tile = (y >> 2) * 8 + (x & 7);
+    } else {
+        slice = (int)(blockIdx.x & 3);
+        tile = blockIdx.x >> 2;
+    }
+    const int64_t seq = tile / a.tiles_per_seq;
+    const int64_t t0 = (tile % a.tiles_per_seq) * E7_WM;
+    const int nb0 = slice * E7_WN;
+
+    // This lane's row (32 * wave + lane % 32 of the tile, k-half lane / 32):
+    // its token and mask first -- the only loads anything waits for before
+    // the rest are issued (a compiler-placed wait for them would otherwise
+    // also wait for the direct-to-LDS loads, which it cannot count).
+    const int l32 = lane & 31, hf = lane >> 5;
+    int64_t src = 0;
+    bool live_row = false;
+    {
+        const int64_t t = t0 + 32 * wave + l32;
+        if (t < a.T) {
+            const int idx = a.tokens[seq * a.T + t];
+            live_row = !a.mask || a.mask[seq * a.T + t] != 0;
+            if (idx >= 0 && idx < a.vocab) src = idx;
+            else if (hf == 0 && slice == 0) report_gather_error(a.err, seq * a.T + t, idx);
+        }
+    }
+    // bit r of the word: row r of the wave's 32 is unmasked (both k-halves
+    // of a row hold the same flag)
+    const uint32_t livew = (uint32_t)__ballot(live_row);
+    const uint8_t* arow = (const uint8_t*)a.table + src * K * 2 + 64 * hf;
+    h8 av[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int s = 0; s < 4; s++) av[b][s] = *(const h8*)(arow + 128 * b + 16 * s);
+    // then the projection slice, rows 0 .. K-1 packed at 192 bytes (16-byte
+    // pieces: a wave load covers 5 1/3 rows), in flight with the row loads
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
+    const uint8_t* bsrc = (const uint8_t*)a.B + nb0 * 2;
+#pragma unroll
+    for (int u0 = 0; u0 < NBL; u0 += 4) {
+        const int u = u0 + wave;
+        if (u < NBL) {
+            const int x = u * 1024 + lane * 16;
+            eg_lds_load16(bsrc + (int64_t)(x / E7_BROW) * E3_N * 2 + x % E7_BROW,
+                          __builtin_amdgcn_readfirstlane(base + u * 1024));
+        }
+    }
+    // the direct-to-LDS loads are not tracked by the compiler: every wave
+    // retires its own (and the row loads before them), then the barrier
+    // makes all of them visible
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // MFMA step i = 4b + s; its projection fragments (one per 32-column
+    // tile) are read from LDS one step ahead, so the transpose reads of step
+    // i+1 are in flight under the three MFMAs of step i
+    const int G = lane >> 4, s16 = lane & 15;
+    const uint8_t* bt = smem + (32 * (G >> 1) + (s16 >> 2)) * E7_BROW + (16 * (G & 1) + 4 * (s16 & 3)) * 2;
+    auto frag = [&](int i, int cb) {
+        const uint8_t* p = bt + (64 * (i >> 2) + 8 * (i & 3)) * E7_BROW + cb * 64;
+        const v4s lo = lds_read_tr16(p);
+        const v4s hi = lds_read_tr16(p + 4 * E7_BROW);
+        return __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    f16v acc[3];
+#pragma unroll
+    for (int cb = 0; cb < 3; cb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[cb][r] = 0.0f;
+    h8 bcur[3], bnext[3];
+#pragma unroll
+    for (int cb = 0; cb < 3; cb++) bcur[cb] = frag(0, cb);
+#pragma unroll
+    for (int i = 0; i < 4 * NB; i++) {
+        if (i + 1 < 4 * NB) {
+#pragma unroll
+            for (int cb = 0; cb < 3; cb++) bnext[cb] = frag(i + 1, cb);
+        }
+#pragma unroll
+        for (int cb = 0; cb < 3; cb++)
+            acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i >> 2][i & 3], bcur[cb], acc[cb], 0, 0, 0);
+#pragma unroll
+        for (int cb = 0; cb < 3; cb++) bcur[cb] = bnext[cb];
+    }
+
+    // column sums of the wave's unmasked rows (accumulator r of lane l is row
+    // 8*(r/4) + 4*(l/32) + r%4), then of the 4 waves in order
+#pragma unroll
+    for (int cb = 0; cb < 3; cb++) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if ((livew >> (8 * (r >> 2) + 4 * hf + (r & 3))) & 1u) sum += acc[cb][r];
+        sum += __shfl_xor(sum, 32);
+        if (hf == 0) colw[wave][cb * 32 + l32] = sum;
+    }
+    if (lane == 0) ired[wave] = __popc(livew);
+    __syncthreads();
+    const int tcount = ired[0] + ired[1] + ired[2] + ired[3];  // unmasked rows of the tile
+    const int64_t ntiles = a.batches * a.tiles_per_seq;
+    unsigned int* pdst = (unsigned int*)(a.P + tile * E3_N + nb0);
+    unsigned int* cdst = (unsigned int*)(a.P + ntiles * E3_N);
+    if (tid < E7_WN) {
+        const float v = ((colw[0][tid] + colw[1][tid]) + colw[2][tid]) + colw[3][tid];
+        __hip_atomic_store(pdst + tid, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0 && slice == 0 && a.tiles_per_seq > 1)
+        __hip_atomic_store(cdst + tile, (unsigned)tcount, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // publication order as embed_gemm4_kernel: agent-scope atomic stores
+    // retired by s_waitcnt vmcnt(0), barrier, then the ticket
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(&a.tickets[seq], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(4 * a.tiles_per_seq - 1);
+    __syncthreads();
+    if (!last) return;
+    // the sequence's unmasked count: this tile's own when the sequence is one
+    // tile, else the published counts of its tiles
+    int count = tcount;
+    if (a.tiles_per_seq > 1) {
+        int c = 0;
+        for (int i = lane; i < a.tiles_per_seq; i += 64)
+            c += (int)__hip_atomic_load(cdst + seq * a.tiles_per_seq + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+        count = c;
+    }
+    const float inv = count ? 1.0f / (float)count : 0.0f;
+    const unsigned int* psrc = (const unsigned int*)(a.P + seq * a.tiles_per_seq * E3_N);
+    double ss = 0.0;
+    for (int c = tid; c < E3_N; c += 256) {
+        // 8 tiles' partials in flight at a time, added in tile order
+        float v = 0.0f;
+        for (int s0 = 0; s0 < a.tiles_per_seq; s0 += 8) {
+            unsigned int pv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                pv[u] = s0 + u < a.tiles_per_seq
+                            ? __hip_atomic_load(psrc + (s0 + u) * E3_N + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : 0u;
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (s0 + u < a.tiles_per_seq) v += __uint_as_float(pv[u]);
+        }
+        v = count ? v * inv : 0.0f;
+        rowv[c] = v;
+        ss += (double)v * (double)v;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) dred[wave] = ss;
+    __syncthreads();
+    const float norm = (float)__builtin_sqrt(dred[0] + dred[1] + dred[2] + dred[3]);
+    for (int c = tid; c < E3_N; c += 256) {
+        float v = rowv[c];
+        if (norm != 0.0f) v = v / norm;
+        a.out[seq * E3_N + c] = f2h(v);
+    }
+    if (tid == 0) __hip_atomic_store(&a.tickets[seq], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+bool embed_gemm7_supported(const EmbedArgs& a) {
+    return a.N == E3_N && a.K % 64 == 0 && a.K >= 64 && a.K <= 512;
+}
+
+hipError_t launch_embed_gemm7(const EmbedArgs& a, hipStream_t s) {
+    const int64_t tiles = a.batches * a.tiles_per_seq;
+    const unsigned grid = (unsigned)(tiles * 4);
+    const int xcd = tiles % 8 == 0 ? 1 : 0;
+    const size_t lds = (size_t)a.K * E7_BROW;
+#define MANTA_EG7(NB)                                                                                    \
+    case NB: {                                                                                           \
+        static bool attr = false;                                                                        \
+        if (!attr) {                                                                                     \
+            hipError_t e = hipFuncSetAttribute((const void*)embed_gemm7_kernel<NB>,                      \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,               \
+                                               (int)(NB * 64 * E7_BROW));                                \
+            if (e != hipSuccess) return e;                                                               \
+            attr = true;                                                                                 \
+        }                                                                                                \
+        hipLaunchKernelGGL(embed_gemm7_kernel<NB>, dim3(grid), dim3(256), lds, s, a, xcd);               \
+        return hipGetLastError();                                                                        \
+    }
+    switch (a.K / 64) {
+        MANTA_EG7(1)
+        MANTA_EG7(2)
+        MANTA_EG7(3)
+        MANTA_EG7(4)
+        MANTA_EG7(5)
+        MANTA_EG7(6)
+        MANTA_EG7(7)
+        MANTA_EG7(8)
+    }
+#undef MANTA_EG7
+    return hipErrorInvalidValue;
+}
+
 // Pooled embed for large batches of short sequences (T = 64, 128 or 256):
 // one workgroup of 8 waves = 256 rows (whole sequences) x all N = 384
 // columns, each wave 64 rows x 192 columns (2 x 6 tiles of

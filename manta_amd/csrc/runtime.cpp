@@ -1755,15 +1755,18 @@ int manta_rocm_embed_pooled(MantaRocm* rt, const int32_t* tokens, const int32_t*
     }
     if (!prepared && manta::embed_gemm3_supported(a, q8b) && b <= kTickets) {
         // one launch: 128-row x 96-column tiles, the last tile of each
-        // sequence finishes it
+        // sequence finishes it (every operand in one round of loads when K
+        // allows, else a K ring)
         a.tiles_per_seq = (int)((t + 127) / 128);
-        if (b * a.tiles_per_seq > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: batch too large");
-        rc = ensure_workspace(rt, align_up((size_t)(b * a.tiles_per_seq * e) * sizeof(float), 256), err);
+        if (b * a.tiles_per_seq * 4 > 0x7FFFFFFF) return fail(err, MANTA_ROCM_UNSUPPORTED, "embed: batch too large");
+        const bool one_round = manta::embed_gemm7_supported(a);
+        rc = ensure_workspace(rt, align_up((size_t)(b * a.tiles_per_seq * (e + 1)) * sizeof(float), 256), err);
         if (rc) return rc;
         a.P = (float*)rt->ws;
         a.tickets = rt->tickets;
         a.out = out;
-        LAUNCH_TRY(manta::launch_embed_gemm4(a, rt->stream), "embed");
+        if (one_round) LAUNCH_TRY(manta::launch_embed_gemm7(a, rt->stream), "embed");
+        else LAUNCH_TRY(manta::launch_embed_gemm4(a, rt->stream), "embed");
         rt->gather_pending = true;
         return MANTA_ROCM_OK;
     }

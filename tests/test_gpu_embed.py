@@ -126,6 +126,33 @@ def test_embed_ragged_and_empty_sequences(rt, d, e):
     assert _cos_rows(got[1:], want32[1:]).min() >= 0.9999
 
 
+@pytest.mark.parametrize("b,t,d", [(3, 9, 64), (5, 200, 256), (16, 128, 384), (2, 300, 512), (9, 257, 192),
+                                   (4, 70, 160), (3, 40, 96)])
+def test_embed_one_round_shapes(rt, b, t, d):
+    """The small-batch pooled embed (f16 projection, e = 384) at K its
+    one-round kernel takes (64 to 512: one to eight 64-k blocks), K it
+    leaves to the ring kernel (96, 160), sequences longer than
+    one 128-row tile (published per-tile counts), ragged masks, and both
+    workgroup orders (a tile count that is a multiple of 8 or not)."""
+    e, v = 384, 700
+    tokens = synth.uniform_i32(17, b, b * t, 0, v).reshape(b, t)
+    lengths = synth.uniform_i32(17, 100 + b, b, 1, t + 1)
+    lengths[0] = t
+    mask = (np.arange(t)[None, :] < lengths[:, None]).astype(np.int32)
+    table = synth.normal_f16(17, 1, v, d, 0.02)
+    proj = synth.normal_f16(17, 2, d, e, 1.0 / np.sqrt(d))
+    got = orc.f16_to_f32(rt.embed_pooled(rt.to_device(tokens), rt.to_device(mask), rt.to_device(table),
+                                         rt.to_device(proj)).download())
+    want16, want32 = orc.embed(tokens, mask, table, proj_f16=proj)
+    assert _cos_rows(got, want32).min() >= 0.9999
+    ulp = np.spacing(np.abs(orc.f16_to_f32(want16)).astype(np.float16)).astype(np.float32)
+    assert np.all(np.abs(got - orc.f16_to_f32(want16)) <= 2 * ulp + 1e-7)
+    # a second call on the same runtime (the tickets were reset) agrees bit for bit
+    again = orc.f16_to_f32(rt.embed_pooled(rt.to_device(tokens), rt.to_device(mask), rt.to_device(table),
+                                           rt.to_device(proj)).download())
+    np.testing.assert_array_equal(again, got)
+
+
 @pytest.mark.parametrize("d,e", [(64, 64), (384, 384)])
 def test_embed_out_of_range_token(rt, d, e):
     tokens, mask, table, proj = synth.config1(b=4, t=32, vocab=100, d=d, e=e)
