@@ -107,8 +107,8 @@ struct RefArgs {
     int smallest;
     int k;
     int kp;                     // scan rows per query (k <= kp <= n)
-    const int32_t* cand_ids;    // [nq][kp] the scan's best rows, best first
-    const float* cand_scores;   // [nq][kp] their scan scores
+    const int32_t* cand_ids;    // [nq][kp] the scan's best rows, in any order but the worst last
+    const float* cand_scores;   // [nq][kp] their scan scores (position kp-1: the worst)
     float e_qd;                 // relative error bound of the scan's q^.d' term
     float maxdn;                // max over rows of |d'|, as stored
     float maxdd;                // max over rows of |d'|^2, as stored
@@ -196,6 +196,7 @@ struct MqSelectArgs {
     const float* qbound;        // [nq][2] the shadow margin m and factor f
     int d;
     int op;
+    int unsorted;               // final pass: ids / scores in any order, the k-th best (the worst kept) last
 };
 
 // Launch shape of the scan kernel for an op, K steps (pitch / 32) and query count.

@@ -412,6 +412,7 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     __shared__ int wpos, wpos2;
     __shared__ int cmax_s;
     __shared__ unsigned long long minkey;
+    __shared__ int kpos;
     __shared__ int qh_s[PM == 2 ? kMaxQueryDim / 4 : 1];
     __shared__ int ql_s[PM == 2 ? kMaxQueryDim / 4 : 1];
     const int tid = threadIdx.x;
@@ -725,7 +726,20 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
         __syncthreads();
     }
     const uint64_t kth = fill == k ? (uint64_t)minkey : 0ull;
-    if (a.out_ids) {
+    if (a.out_ids && a.unsorted && fill == k) {
+        // final pass for a caller that re-sorts (the reference finish): the
+        // kept keys in buffer order, except that the k-th best goes last, so
+        // position k-1 still holds the worst kept score
+        for (int i = tid; i < fill; i += NT)
+            if (buf[i] == kth) kpos = i;
+        __syncthreads();
+        const int p = kpos;
+        for (int i = tid; i < k; i += NT) {
+            const uint64_t key = buf[i == k - 1 ? p : (i == p ? k - 1 : i)];
+            a.out_ids[(int64_t)q * k + i] = (int32_t)key_index(key);
+            if (a.out_scores) a.out_scores[(int64_t)q * k + i] = key_score(key, a.smallest);
+        }
+    } else if (a.out_ids) {
         // final pass: ids and scores in (value, index) order
         const int S = next_pow2(fill < 2 ? 2 : fill);
         for (int i = fill + tid; i < S; i += NT) buf[i] = 0;

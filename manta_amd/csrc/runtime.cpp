@@ -1050,7 +1050,7 @@ hipError_t launch_mq_pass(const MqPlan& p, int dop, const manta::MqArgs& a, int 
 // Encode queries to the global digit planes, then run the multi-query passes.
 int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, const uint16_t* q, int64_t nq,
            int64_t k, const MqPlan& p, float* out_scores, int32_t* out_ids, float* out_topk_scores,
-           char** err) {
+           char** err, bool any_order = false) {
     // query planes: E8 codes or E16 digits, one row per query, as wide as a
     // q8 row (pitch) or a q4 row in elements (d); the shadow scan's E8
     // codes are as wide as a shadow row, its E16 planes [nq][d]
@@ -1140,6 +1140,7 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, cons
     sa.qbound = qb;
     sa.d = (int)c->d;
     sa.op = dop;
+    sa.unsorted = any_order ? 1 : 0;
     for (size_t i = 0; i < p.passes.size(); i++) {
         const MqPass& ps = p.passes[i];
         a.row_begin = ps.begin;
@@ -1200,13 +1201,16 @@ namespace {
 // multi-query passes, or the streaming scan with its fused top-k.  With a
 // caller's scratch (sc) the call allocates nothing: the streaming scan only,
 // its keys and tickets in sc.
+// any_order: the caller re-sorts the k rows (the reference finish), so the
+// multi-query passes may return them in any order with the k-th best last.
 int scan_topk(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, const uint16_t* q, int64_t nq,
-              int64_t k, int32_t* out_ids, float* out_scores, int64_t* out_acc, manta_rt::Scratch* sc, char** err) {
+              int64_t k, int32_t* out_ids, float* out_scores, int64_t* out_acc, manta_rt::Scratch* sc, char** err,
+              bool any_order = false) {
     if (!sc && q4_shadow_wanted(c, dop, nq, k)) ensure_q4_shadow(rt, c);
     const MqPlan plan = sc ? MqPlan() : mq_plan(c, dop, nq, k, true);
     const int e16 = dop != manta::OP_DOT ? 1 : 0;
     if (plan.use) {
-        int rc = run_mq(rt, c, dop, order, q, nq, k, plan, nullptr, out_ids, out_scores, err);
+        int rc = run_mq(rt, c, dop, order, q, nq, k, plan, nullptr, out_ids, out_scores, err, any_order && !out_acc);
         if (rc) return rc;
         if (out_acc)
             LAUNCH_TRY(manta::launch_q8_rescore((const int8_t*)c->codes, c->pitch, 0, c->n, (int)c->d, q, out_ids,
@@ -1263,7 +1267,9 @@ int ref_topk(MantaRocm* rt, const MantaRocmCandidates* c, const ScoreOp& so, int
         uint64_t* cand_keys = cv.take<uint64_t>((size_t)nq * kp);
         redo = cv.take<int>((size_t)nq);
         redo_tau = cv.take<uint64_t>((size_t)nq);
-        rc = scan_topk(rt, c, so.scan, order, q, nq, kp, cand_ids, cand_scores, nullptr, sc, err);
+        // (in any order: ref_finish sorts the rescored keys and reads only the
+        // kp-th, worst, scan score)
+        rc = scan_topk(rt, c, so.scan, order, q, nq, kp, cand_ids, cand_scores, nullptr, sc, err, true);
         if (rc) return rc;
         manta::RefArgs ra{};
         ra.fmt = fmt;
