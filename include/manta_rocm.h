@@ -124,7 +124,10 @@ int manta_rocm_device_count(int* out, char** err);
  * `device`, creates the runtime's stream. */
 int manta_rocm_create(int device, MantaRocm** out, char** err);
 
-/* Replaces mantaCudaRuntimeDestroy (native_linux.go:171-189). */
+/* Replaces mantaCudaRuntimeDestroy (native_linux.go:171-189).  Candidate
+ * sets still bound on the runtime lose their device memory with it; their
+ * handles stay valid only for manta_rocm_unbind, which then frees the handle
+ * alone. */
 void manta_rocm_destroy(MantaRocm* rt);
 
 /* Replaces mantaCudaFreeCString (native_linux.go:620-624). */
@@ -212,6 +215,8 @@ int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16
  * (runtime/weight_file.go:93-104, 247-367) for candidate stores. */
 int manta_rocm_bind_packed(MantaRocm* rt, const struct MantaMll* container, MantaRocmCandidates** out,
                            char** err);
+/* Free a candidate set: its device memory (unless its runtime was destroyed
+ * first, which released it) and the handle. */
 void manta_rocm_unbind(MantaRocmCandidates* cands);
 int manta_rocm_candidates_info(const MantaRocmCandidates* cands, int* format, int64_t* sets,
                                int64_t* n, int64_t* d);

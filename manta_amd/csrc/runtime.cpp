@@ -20,6 +20,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <set>
 #include <string>
 #include <thread>
 #include <vector>
@@ -61,6 +62,9 @@ struct MantaRocm {
     std::map<std::string, std::pair<uint64_t, double>> totals;
     // span timing (manta_rocm_span): events around a run of launches
     hipEvent_t span_ev[2] = {nullptr, nullptr};
+    // candidate sets bound on this runtime and not yet unbound: destroy
+    // releases their device memory and detaches them
+    std::set<MantaRocmCandidates*> bound;
 };
 
 struct MantaRocmCandidates {
@@ -386,6 +390,14 @@ void manta_rocm_destroy(MantaRocm* rt) {
     if (rt->ws_ref) (void)hipFree(rt->ws_ref);
     if (rt->err_word) (void)hipFree(rt->err_word);
     if (rt->tickets) (void)hipFree(rt->tickets);
+    // candidate sets still bound: their device memory goes with the runtime,
+    // their handles stay valid for manta_rocm_unbind (which then frees only
+    // the handle)
+    for (MantaRocmCandidates* c : rt->bound) {
+        free_candidates_memory(c);
+        c->rt = nullptr;
+    }
+    rt->bound.clear();
     if (rt->own_stream) (void)hipStreamDestroy(rt->own_stream);
     delete rt;
 }
@@ -625,6 +637,7 @@ int manta_rocm_bind_q8_rows(MantaRocm* rt, const int8_t* codes, const float* sca
     }
     rt->stats.bytes_uploaded += c->bytes;
     rt->stats.candidate_bytes += c->bytes;
+    rt->bound.insert(c);
     *out = c;
     return MANTA_ROCM_OK;
 }
@@ -706,6 +719,7 @@ int manta_rocm_bind_q4_blocks(MantaRocm* rt, const uint8_t* packed, const uint16
     }
     rt->stats.bytes_uploaded += c->bytes;
     rt->stats.candidate_bytes += c->bytes;
+    rt->bound.insert(c);
     *out = c;
     return MANTA_ROCM_OK;
 }
@@ -716,8 +730,10 @@ void manta_rocm_unbind(MantaRocmCandidates* cands) {
         (void)hipSetDevice(cands->rt->device);
         (void)hipStreamSynchronize(cands->rt->stream);
         cands->rt->stats.candidate_bytes -= std::min<uint64_t>(cands->rt->stats.candidate_bytes, cands->bytes);
+        cands->rt->bound.erase(cands);
+        free_candidates_memory(cands);
     }
-    free_candidates_memory(cands);
+    // (a set whose runtime was destroyed first has no device memory left)
     delete cands;
 }
 
