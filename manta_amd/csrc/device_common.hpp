@@ -69,6 +69,22 @@ __device__ __forceinline__ float fdiv_rn(float a, float b) { return __fdiv_rn(a,
 // -fhip-fp32-correctly-rounded-divide-sqrt is the correctly rounded sequence.
 __device__ __forceinline__ float fsqrt_rn(float a) { return __builtin_sqrtf(a); }
 
+// geluTensor: 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))), f32 with the
+// tanh in f64.
+__device__ __forceinline__ float gelu_value(float v) {
+    const float cubic = fmul_rn(fmul_rn(v, v), v);
+    const float inner = fmul_rn(0.7978845608f, fadd_rn(v, fmul_rn(0.044715f, cubic)));
+    return fmul_rn(fmul_rn(0.5f, v), fadd_rn(1.0f, (float)tanh((double)inner)));
+}
+// The same formula with the tanh in f32 (the device library's tanhf): for the
+// encoder's f16 weight GEMMs, whose operands are rounded to f16 anyway, so the
+// f64 tanh buys nothing there and costs most of the FFN up-projection.
+__device__ __forceinline__ float gelu_value_f32(float v) {
+    const float cubic = fmul_rn(fmul_rn(v, v), v);
+    const float inner = fmul_rn(0.7978845608f, fadd_rn(v, fmul_rn(0.044715f, cubic)));
+    return fmul_rn(fmul_rn(0.5f, v), fadd_rn(1.0f, tanhf(inner)));
+}
+
 // Records an out-of-range gather index.  The reference's gather loops stop
 // at the first bad index in position order (tensor_ops.go:751-979), so the
 // lowest position must win however the threads race: the word holds

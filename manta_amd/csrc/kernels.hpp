@@ -272,6 +272,8 @@ struct EmbedArgs {
     unsigned long long* err;    // first out-of-range gather index
     unsigned int* tickets;      // [batches] zero between calls (single-pass pooled kernel)
     uint16_t* out;              // f16 [batches][N] embeddings (single-pass pooled kernel)
+    uint16_t* Y16;              // plain matmul of embed_gemm2: f16 [M][N] output instead of Y (or nullptr)
+    int gelu;                   // with Y16: geluTensor (tanh in f32) applied to each value before the f16 rounding
 };
 
 hipError_t launch_embed_gemm(const EmbedArgs& a, bool gather, bool q8b, bool pool, hipStream_t s);
@@ -315,13 +317,17 @@ hipError_t launch_mean_pool_masked(const float* x, const int32_t* mask, int64_t 
 hipError_t launch_normalize_rows(float* x, int64_t rows, int64_t cols, hipStream_t s);
 
 // encoder steps (kernels_encoder.hip)
+// x16 / y16 / C16 (optional): the same values rounded to f16 as well, the
+// left operand of the f16 weight GEMMs
 hipError_t launch_enc_gather_q8(const int32_t* tok, int64_t rows, const int8_t* codes, const float* scales,
-                                int64_t vocab, int d, float* x, unsigned long long* err, hipStream_t s);
+                                int64_t vocab, int d, float* x, unsigned long long* err, hipStream_t s,
+                                uint16_t* x16 = nullptr);
 hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B, const float* bscale, int64_t sB,
-                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s, bool gelu = false);
+                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s, bool gelu = false,
+                           uint16_t* C16 = nullptr);
 hipError_t launch_enc_softmax_rows(float* x, int64_t rows, int cols, hipStream_t s);
 hipError_t launch_enc_add_layernorm(const float* a, const float* b, float* y, int64_t rows, int cols,
-                                    hipStream_t s);
+                                    hipStream_t s, uint16_t* y16 = nullptr);
 hipError_t launch_enc_to_f16(const float* x, int64_t n, uint16_t* out, hipStream_t s);
 hipError_t launch_enc_gelu(float* x, int64_t n, hipStream_t s);
 

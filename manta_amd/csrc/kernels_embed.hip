@@ -373,7 +373,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void e
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int64_t m = m0 + rb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-                    if (m < a.M) a.Y[m * a.N + n] = Q8B ? acc[rb][cb][r] * cs : acc[rb][cb][r];
+                    if (m >= a.M) continue;
+                    const float v = Q8B ? acc[rb][cb][r] * cs : acc[rb][cb][r];
+                    if (a.Y16) a.Y16[m * a.N + n] = f2h(a.gelu ? gelu_value_f32(v) : v);
+                    else a.Y[m * a.N + n] = v;
                 }
         }
         return;

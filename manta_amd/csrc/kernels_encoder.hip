@@ -36,7 +36,8 @@ __device__ __forceinline__ float wave_max_f32(float v) {
 __global__ __launch_bounds__(256) void enc_gather_q8_kernel(const int32_t* __restrict__ tok, int64_t rows,
                                                             const int8_t* __restrict__ codes,
                                                             const float* __restrict__ scales, int64_t vocab, int d,
-                                                            float* __restrict__ x, unsigned long long* err) {
+                                                            float* __restrict__ x, unsigned long long* err,
+                                                            uint16_t* __restrict__ x16) {
     const int64_t total = rows * d;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
         const int64_t r = i / d;
@@ -44,16 +45,10 @@ __global__ __launch_bounds__(256) void enc_gather_q8_kernel(const int32_t* __res
         const int id = tok[r];
         const bool ok = id >= 0 && (int64_t)id < vocab;
         if (!ok && c == 0) report_gather_error(err, r, id);
-        x[i] = ok ? fmul_rn((float)codes[(int64_t)id * d + c], scales[id]) : 0.0f;
+        const float v = ok ? fmul_rn((float)codes[(int64_t)id * d + c], scales[id]) : 0.0f;
+        x[i] = v;
+        if (x16) x16[i] = f2h(v);
     }
-}
-
-// geluTensor: 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))), f32 with the
-// tanh in f64.
-__device__ __forceinline__ float gelu_value(float v) {
-    const float cubic = fmul_rn(fmul_rn(v, v), v);
-    const float inner = fmul_rn(0.7978845608f, fadd_rn(v, fmul_rn(0.044715f, cubic)));
-    return fmul_rn(fmul_rn(0.5f, v), fadd_rn(1.0f, (float)tanh((double)inner)));
 }
 
 // C[b] = A[b] (M x K, row-major, batch stride sA) times B:
@@ -73,7 +68,7 @@ __global__ __launch_bounds__(256) void enc_gemm_mfma_kernel(const float* __restr
                                                             const void* __restrict__ Bv,
                                                             const float* __restrict__ bscale, int64_t sB,
                                                             float* __restrict__ C, int64_t sC, int M, int N, int K,
-                                                            int gelu) {
+                                                            int gelu, uint16_t* __restrict__ C16) {
     typedef float v16f __attribute__((ext_vector_type(16)));
     __shared__ float As[16][64 + 4];
     __shared__ float Bs[16][64 + 4];
@@ -161,7 +156,11 @@ __global__ __launch_bounds__(256) void enc_gemm_mfma_kernel(const float* __restr
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int gm = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (gm < M && gn < N) c[(int64_t)gm * N + gn] = gelu ? gelu_value(acc[r]) : acc[r];
+        if (gm < M && gn < N) {
+            const float v = gelu ? gelu_value(acc[r]) : acc[r];
+            c[(int64_t)gm * N + gn] = v;
+            if (C16) C16[bt * sC + (int64_t)gm * N + gn] = f2h(v);
+        }
     }
 }
 
@@ -192,7 +191,7 @@ __global__ __launch_bounds__(256) void enc_softmax_rows_kernel(float* __restrict
 template <bool ADD>
 __global__ __launch_bounds__(256) void enc_add_layernorm_kernel(const float* __restrict__ a,
                                                                 const float* __restrict__ b, float* __restrict__ y,
-                                                                int64_t rows, int cols) {
+                                                                int64_t rows, int cols, uint16_t* __restrict__ y16) {
     const int lane = threadIdx.x & 63;
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
@@ -210,7 +209,11 @@ __global__ __launch_bounds__(256) void enc_add_layernorm_kernel(const float* __r
     }
     const float var = fdiv_rn(wave_sum_f32(v), (float)cols);
     const float inv = (float)(1.0 / sqrt((double)var + 1e-5));
-    for (int c = lane; c < cols; c += 64) yr[c] = fmul_rn(fsub_rn(in(c), mean), inv);
+    for (int c = lane; c < cols; c += 64) {
+        const float o = fmul_rn(fsub_rn(in(c), mean), inv);
+        yr[c] = o;
+        if (y16) y16[r * cols + c] = f2h(o);
+    }
 }
 
 // geluTensor in place, element by element.
@@ -231,14 +234,16 @@ static unsigned grid_for(int64_t n) {
 }
 
 hipError_t launch_enc_gather_q8(const int32_t* tok, int64_t rows, const int8_t* codes, const float* scales,
-                                int64_t vocab, int d, float* x, unsigned long long* err, hipStream_t s) {
+                                int64_t vocab, int d, float* x, unsigned long long* err, hipStream_t s,
+                                uint16_t* x16) {
     hipLaunchKernelGGL(enc_gather_q8_kernel, dim3(grid_for(rows * d)), dim3(256), 0, s, tok, rows, codes, scales,
-                       vocab, d, x, err);
+                       vocab, d, x, err, x16);
     return hipGetLastError();
 }
 
 hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B, const float* bscale, int64_t sB,
-                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s, bool gelu) {
+                           float* C, int64_t sC, int M, int N, int K, int batches, hipStream_t s, bool gelu,
+                           uint16_t* C16) {
     if (M <= 0 || N <= 0 || K <= 0 || batches <= 0 || batches > 65535 || (M + 63) / 64 > 65535)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)batches);
@@ -250,10 +255,10 @@ hipError_t launch_enc_gemm(int bmode, const float* A, int64_t sA, const void* B,
     do {                                                                                                        \
         if (vec)                                                                                                \
             hipLaunchKernelGGL((enc_gemm_mfma_kernel<BM, true>), grid, dim3(256), 0, s, A, sA, B, bscale, sB, C, \
-                               sC, M, N, K, gelu ? 1 : 0);                                                                    \
+                               sC, M, N, K, gelu ? 1 : 0, C16);                                                               \
         else                                                                                                    \
             hipLaunchKernelGGL((enc_gemm_mfma_kernel<BM, false>), grid, dim3(256), 0, s, A, sA, B, bscale, sB,   \
-                               C, sC, M, N, K, gelu ? 1 : 0);                                                                 \
+                               C, sC, M, N, K, gelu ? 1 : 0, C16);                                                            \
     } while (0)
     if (bmode == 0) MANTA_ENC_GEMM(0);
     else if (bmode == 1) MANTA_ENC_GEMM(1);
@@ -268,14 +273,14 @@ hipError_t launch_enc_softmax_rows(float* x, int64_t rows, int cols, hipStream_t
 }
 
 hipError_t launch_enc_add_layernorm(const float* a, const float* b, float* y, int64_t rows, int cols,
-                                    hipStream_t s) {
+                                    hipStream_t s, uint16_t* y16) {
     if (rows <= 0 || cols <= 0) return hipSuccess;
     if (b)
         hipLaunchKernelGGL(enc_add_layernorm_kernel<true>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a, b, y,
-                           rows, cols);
+                           rows, cols, y16);
     else
         hipLaunchKernelGGL(enc_add_layernorm_kernel<false>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a, b,
-                           y, rows, cols);
+                           y, rows, cols, y16);
     return hipGetLastError();
 }
 

@@ -1670,10 +1670,23 @@ int manta_rocm_encoder_pooled_layers(MantaRocm* rt, const int32_t* tokens, const
     if (b > 65535 || rows > 0x7FFFFFFF || d > 0x7FFFFFFF || h > 0x7FFFFFFF || t > 0x7FFFFFFF ||
         (rows + 63) / 64 > 65535)
         return fail(err, MANTA_ROCM_UNSUPPORTED, "encoder: shape too large");
+    // The weight GEMMs run on the f16 matrix cores when d and h are multiples
+    // of 128 (embed_gemm2: the q8 weights widened exactly to f16 [N][K],
+    // their column scales applied after the f32 accumulation; the left
+    // operands rounded to f16 by the steps that produce them), else on the
+    // f32 matrix cores (enc_gemm_mfma_kernel).  The attention products stay
+    // f32.
+    const bool f16w = d % 128 == 0 && h % 128 == 0 && d <= 4096 && h <= 8192;
     // x, q, k, v, mixed [rows, d]; scores [b, t, t]; ffn [rows, h]; pooled [b, d]
+    // (f16 path: x16, k16, mx16 [rows, d], ffn16 [rows, h], the six weights as f16 [N][K])
     const size_t rd = (size_t)rows * (size_t)d;
-    const size_t need = 5 * (rd * 4 + 256) + (size_t)b * t * t * 4 + 256 + (size_t)rows * h * 4 + 256 +
-                        (size_t)b * d * 4 + 256;
+    const size_t wsz[6] = {(size_t)d * d, (size_t)d * d, (size_t)d * d, (size_t)d * d, (size_t)d * h, (size_t)h * d};
+    const size_t ffn_f32 = f16w ? 1 : (size_t)rows * h;  // the f16 path keeps ffn in f16 only
+    size_t need = 5 * (rd * 4 + 256) + (size_t)b * t * t * 4 + 256 + ffn_f32 * 4 + 256 + (size_t)b * d * 4 + 256;
+    if (f16w) {
+        need += 3 * (rd * 2 + 256) + (size_t)rows * h * 2 + 256;
+        for (size_t z : wsz) need += z * 2 + 256;
+    }
     int rc = ensure_workspace(rt, need, err);
     if (rc) return rc;
     Carver cv(rt->ws);
@@ -1683,31 +1696,79 @@ int manta_rocm_encoder_pooled_layers(MantaRocm* rt, const int32_t* tokens, const
     float* v = cv.take<float>(rd);
     float* mx = cv.take<float>(rd);
     float* sc = cv.take<float>((size_t)b * t * t);
-    float* ffn = cv.take<float>((size_t)rows * h);
+    float* ffn = cv.take<float>(ffn_f32);
     float* pooled = cv.take<float>((size_t)b * d);
+    uint16_t *x16 = nullptr, *k16 = nullptr, *mx16 = nullptr, *ffn16 = nullptr, *wt[6] = {};
+    if (f16w) {
+        x16 = cv.take<uint16_t>(rd);
+        k16 = cv.take<uint16_t>(rd);
+        mx16 = cv.take<uint16_t>(rd);
+        ffn16 = cv.take<uint16_t>((size_t)rows * h);
+        for (int i = 0; i < 6; i++) wt[i] = cv.take<uint16_t>(wsz[i]);
+    }
     const int R = (int)rows, D = (int)d, H = (int)h, T = (int)t;
     const int64_t td = (int64_t)t * d, tt = (int64_t)t * t;
     hipStream_t s = rt->stream;
-    LAUNCH_TRY(manta::launch_enc_gather_q8(tokens, rows, w->token_codes, w->token_scales, vocab, D, x, rt->err_word, s),
+    // out = in16 [R, K] x weight i (f16 [N][K], column scales) on f16 MFMA:
+    // f32 out, or f16 out with gelu applied (ffn_up)
+    auto wgemm = [&](int i, const uint16_t* in16, int K, int N, float* out, uint16_t* out16, bool gelu) {
+        manta::EmbedArgs ea{};
+        ea.A = in16;
+        ea.M = R;
+        ea.K = K;
+        ea.N = N;
+        ea.colscale = w->col_scales[i];
+        ea.Y = out;
+        ea.Y16 = out16;
+        ea.gelu = gelu ? 1 : 0;
+        return manta::launch_embed_gemm2(ea, false, true, false, wt[i], s);
+    };
+    if (f16w) {
+        const int kn[6][2] = {{D, D}, {D, D}, {D, D}, {D, D}, {D, H}, {H, D}};
+        for (int i = 0; i < 6; i++) {
+            manta::EmbedArgs ea{};
+            ea.K = kn[i][0];
+            ea.N = kn[i][1];
+            ea.B = w->codes[i];
+            LAUNCH_TRY(manta::launch_embed_transpose_b(ea, true, wt[i], s), "embed_transpose");
+        }
+    }
+    LAUNCH_TRY(manta::launch_enc_gather_q8(tokens, rows, w->token_codes, w->token_scales, vocab, D, x, rt->err_word, s,
+                                           x16),
                "encoder_gather");
     rt->gather_pending = true;
     for (int64_t layer = 0; layer < layers; layer++) {
     if (layer > 0) std::swap(x, mx);  // this block's hidden input is the last block's encoded output
-    LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[0], w->col_scales[0], 0, q, 0, R, D, D, 1, s), "encoder_gemm");
-    LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[1], w->col_scales[1], 0, k, 0, R, D, D, 1, s), "encoder_gemm");
-    LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[2], w->col_scales[2], 0, v, 0, R, D, D, 1, s), "encoder_gemm");
+    if (f16w) {
+        LAUNCH_TRY(wgemm(0, x16, D, D, q, nullptr, false), "encoder_gemm");
+        LAUNCH_TRY(wgemm(1, x16, D, D, k, nullptr, false), "encoder_gemm");
+        LAUNCH_TRY(wgemm(2, x16, D, D, v, nullptr, false), "encoder_gemm");
+    } else {
+        LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[0], w->col_scales[0], 0, q, 0, R, D, D, 1, s), "encoder_gemm");
+        LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[1], w->col_scales[1], 0, k, 0, R, D, D, 1, s), "encoder_gemm");
+        LAUNCH_TRY(manta::launch_enc_gemm(1, x, 0, w->codes[2], w->col_scales[2], 0, v, 0, R, D, D, 1, s), "encoder_gemm");
+    }
     // scores[b] = q[b] @ transpose(k[b]); softmax over each row of t
     LAUNCH_TRY(manta::launch_enc_gemm(2, q, td, k, nullptr, td, sc, tt, T, T, D, (int)b, s), "encoder_attention");
     LAUNCH_TRY(manta::launch_enc_softmax_rows(sc, rows, T, s), "encoder_softmax");
-    LAUNCH_TRY(manta::launch_enc_gemm(0, sc, tt, v, nullptr, td, mx, td, T, D, T, (int)b, s), "encoder_attention");
+    LAUNCH_TRY(manta::launch_enc_gemm(0, sc, tt, v, nullptr, td, mx, td, T, D, T, (int)b, s, false, mx16),
+               "encoder_attention");
     // attended = mixed @ attn_o (into q); attn_hidden = layernorm(attended + x) (into k)
-    LAUNCH_TRY(manta::launch_enc_gemm(1, mx, 0, w->codes[3], w->col_scales[3], 0, q, 0, R, D, D, 1, s), "encoder_gemm");
-    LAUNCH_TRY(manta::launch_enc_add_layernorm(q, x, k, rows, D, s), "encoder_layernorm");
-    LAUNCH_TRY(manta::launch_enc_gemm(1, k, 0, w->codes[4], w->col_scales[4], 0, ffn, 0, R, H, D, 1, s, true),
-               "encoder_gemm");
-    // projected = gelu @ projection (into v); encoded = layernorm(projected + attn_hidden) (into mx)
-    LAUNCH_TRY(manta::launch_enc_gemm(1, ffn, 0, w->codes[5], w->col_scales[5], 0, v, 0, R, D, H, 1, s), "encoder_gemm");
-    LAUNCH_TRY(manta::launch_enc_add_layernorm(v, k, mx, rows, D, s), "encoder_layernorm");
+    if (f16w) LAUNCH_TRY(wgemm(3, mx16, D, D, q, nullptr, false), "encoder_gemm");
+    else LAUNCH_TRY(manta::launch_enc_gemm(1, mx, 0, w->codes[3], w->col_scales[3], 0, q, 0, R, D, D, 1, s), "encoder_gemm");
+    LAUNCH_TRY(manta::launch_enc_add_layernorm(q, x, k, rows, D, s, k16), "encoder_layernorm");
+    // projected = gelu @ projection (into v); encoded = layernorm(projected + attn_hidden) (into mx, and its
+    // f16 copy into x16, the next block's input)
+    if (f16w) {
+        LAUNCH_TRY(wgemm(4, k16, D, H, nullptr, ffn16, true), "encoder_gemm");
+        LAUNCH_TRY(wgemm(5, ffn16, H, D, v, nullptr, false), "encoder_gemm");
+    } else {
+        LAUNCH_TRY(manta::launch_enc_gemm(1, k, 0, w->codes[4], w->col_scales[4], 0, ffn, 0, R, H, D, 1, s, true),
+                   "encoder_gemm");
+        LAUNCH_TRY(manta::launch_enc_gemm(1, ffn, 0, w->codes[5], w->col_scales[5], 0, v, 0, R, D, H, 1, s),
+                   "encoder_gemm");
+    }
+    LAUNCH_TRY(manta::launch_enc_add_layernorm(v, k, mx, rows, D, s, x16), "encoder_layernorm");
     }
     LAUNCH_TRY(manta::launch_normalize_rows(mx, rows, d, s), "normalize");
     LAUNCH_TRY(manta::launch_mean_pool_masked(mx, mask, b, t, d, pooled, s), "mean_pool");

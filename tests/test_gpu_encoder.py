@@ -49,7 +49,9 @@ def _want(tokens, mask, tcodes, tscales, packed):
 
 
 @pytest.mark.parametrize("b,t,vocab,d,h", [(6, 16, 50, 64, 128), (5, 24, 70, 96, 160), (3, 1, 9, 32, 64),
-                                           (8, 64, 300, 384, 1536),
+                                           # d and h multiples of 128: the weight GEMMs on f16 MFMA (the
+                                           # second with 120 rows, not a multiple of the 64-row tiles)
+                                           (8, 64, 300, 384, 1536), (3, 40, 100, 128, 384),
                                            # d, h and t not multiples of 16: the scalar staging path of the
                                            # q8-weight and transposed-K GEMMs, with their bounds-checked K tails
                                            (4, 24, 40, 40, 72)])
