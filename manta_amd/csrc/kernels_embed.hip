@@ -1182,6 +1182,10 @@ __global__ __launch_bounds__(512) void embed_gemm5_kernel(EmbedArgs a, const uin
     const int rg = wave & 3, cg = wave >> 2;
     const int64_t row0 = (int64_t)blockIdx.x * E5_WM;  // first row of b*T
     const int K = a.K;
+    // The mask of the wave's 64 rows (row 64*rg + lane of the tile; the mask
+    // is [b][T], so its index is the row of b*T), loaded with the tokens so
+    // the pooling after the K loop needs no global load.
+    const bool live_row = !a.mask || a.mask[row0 + 64 * rg + lane] != 0;
 
     const uint8_t* asrc[2];
 #pragma unroll
@@ -1201,6 +1205,11 @@ __global__ __launch_bounds__(512) void embed_gemm5_kernel(EmbedArgs a, const uin
         const int c = (lane & 3) ^ ((n >> 2) & 3);
         bsrc[u] = (const uint8_t*)Bt + (int64_t)n * K * 2 + c * 16;
     }
+    const uint64_t livew = __ballot(live_row);  // bit l: row 64*rg + l is unmasked
+    // column scales of the six output columns this lane sums (q8 projection)
+    float cscale[6];
+#pragma unroll
+    for (int cb = 0; cb < 6; cb++) cscale[cb] = Q8B ? a.colscale[192 * cg + 32 * cb + (lane & 31)] : 1.0f;
     const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
     auto issue = [&](int kc, int st) {
         const uint32_t sa = __builtin_amdgcn_readfirstlane(base + st * E5_STAGE + wave * 2 * 1024);
@@ -1258,42 +1267,38 @@ __global__ __launch_bounds__(512) void embed_gemm5_kernel(EmbedArgs a, const uin
     float* part = (float*)smem;                 // [4][384]
     float* rowv = part + 4 * E5_N;              // [4][384]
     const int64_t T = a.T;
-    const int64_t seq_w = (row0 + 64 * rg) / T;
-    const int64_t tw = (row0 + 64 * rg) % T;
-    bool live[2][16];
-#pragma unroll
-    for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int64_t t = tw + 32 * rb + 8 * (r >> 2) + 4 * hf + (r & 3);
-            live[rb][r] = !a.mask || a.mask[seq_w * T + t] != 0;
-        }
+    // A wave whose 64 rows are all unmasked adds without the selects (the
+    // same additions in the same order).
+    const bool all_live = livew == ~0ull;
 #pragma unroll
     for (int cb = 0; cb < 6; cb++) {
         float sum = 0.0f;
+        if (all_live) {
 #pragma unroll
-        for (int rb = 0; rb < 2; rb++)
+            for (int rb = 0; rb < 2; rb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++)
-                if (live[rb][r]) sum += acc[rb][cb][r];
+                for (int r = 0; r < 16; r++) sum += acc[rb][cb][r];
+        } else {
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    if ((livew >> (32 * rb + 8 * (r >> 2) + 4 * hf + (r & 3))) & 1u) sum += acc[rb][cb][r];
+        }
         sum += __shfl_xor(sum, 32);
         const int n = 192 * cg + 32 * cb + l32;
-        if (hf == 0) part[rg * E5_N + n] = Q8B ? sum * a.colscale[n] : sum;
+        if (hf == 0) part[rg * E5_N + n] = Q8B ? sum * cscale[cb] : sum;
     }
+    if (cg == 0 && lane == 0) ired[rg] = __popcll(livew);  // unmasked rows of row group rg
     __syncthreads();
     // 128 threads per sequence (at most 4 sequences of the tile)
     const int S = (int)(E5_WM / T);
     const int sl = tid >> 7, j = tid & 127;
     const int gps = (int)(T / 64);  // row groups per sequence
     const int64_t seq = row0 / T + sl;
-    int cnt = 0;
+    int count = 0;
     if (sl < S)
-        for (int64_t t = j; t < T; t += 128) cnt += (!a.mask || a.mask[seq * T + t] != 0) ? 1 : 0;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off);
-    if (lane == 0) ired[wave] = cnt;
-    __syncthreads();
-    const int count = sl < S ? ired[2 * sl] + ired[2 * sl + 1] : 0;
+        for (int g2 = 0; g2 < gps; g2++) count += ired[sl * gps + g2];
     const float inv = count ? 1.0f / (float)count : 0.0f;
     double ss = 0.0;
     if (sl < S) {
