@@ -1270,9 +1270,14 @@ int ref_topk(MantaRocm* rt, const MantaRocmCandidates* c, const ScoreOp& so, int
     if (c->ref_ranked) {
         // a margin of rows past the k-th: ties and near-ties of the scan
         // scores across the kp-th row are what would send a query to the
-        // full rescan
-        const int64_t kp = std::min<int64_t>(std::min<int64_t>(c->n, kMaxDeviceK),
-                                             k + std::max<int64_t>(8, k / 32));
+        // full rescan.  A margin that would just pass a power of two stops
+        // there (at least 8 rows): the finish sorts next_pow2(kp) keys, and
+        // 1024 of them take one per thread where 1031 would take two.
+        int64_t margin = k + std::max<int64_t>(8, k / 32);
+        int64_t p2 = 1;
+        while (p2 < k) p2 <<= 1;
+        if (p2 >= k + 8 && p2 < margin) margin = p2;
+        const int64_t kp = std::min<int64_t>(std::min<int64_t>(c->n, kMaxDeviceK), margin);
         const size_t need = (size_t)nq * kp * 16 + (size_t)nq * 12 + 2048;
         char* base = nullptr;
         int rc = sc ? take_buffer(rt, sc, need, (void**)&base, err) : ensure_ref_workspace(rt, need, err);
