@@ -14,6 +14,8 @@ Pins:
   retrieval_model.go:11,55) and the entry and param names the example
   programs declare (examples/score_bundle.manta:1,5;
   examples/encoder_trainable_q8.manta:1-9,37; examples/packed_candidates.manta:1).
+* HEAD f64 values (kind 3, in no example): IEEE 754 binary64 little-endian,
+  bit for bit, on entries rewritten with chosen bit patterns.
 * Error behaviour of readAuthoredManifestMLL
   (runtime/authored_manifest_mll.go:197-270).
 """
@@ -131,3 +133,49 @@ def test_errors_follow_the_reference_reader():
         mll.read_authored_manifest(data, "embedding_manifest")
     with pytest.raises(MantaRocmError, match="manifest version"):
         mll.read_authored_manifest(data, "score_manifest", "manta/score-manifest/v9")
+
+
+# HEAD values of kind 3 (f64, authoredFloat) occur in no example container, so
+# their decoding is pinned by IEEE 754 binary64 itself: an I64 entry of a
+# container written here is rewritten into kind 3 holding chosen bit patterns,
+# and each must decode to the double those 8 little-endian bytes are
+# (struct '<d'), bit for bit.  A big-endian read, a read as an integer
+# converted to double, or a narrowing through f32 fails one of them.
+F64_PATTERNS = [1.0, -2.5, -0.0, 5e-324, 2.2250738585072014e-308, 1.7976931348623157e308,
+                float("inf"), float("-inf"), 3.141592653589793, 1.0000000000000002, 0.1]
+
+
+def _head_entries(head: bytes):
+    """(offset of the kind byte, kind) of every HEAD entry: 30 header bytes
+    with the entry count at 28, then key u32, kind u8 and a 1, 8, 8 or 4
+    byte value (bool, i64, f64, string id)."""
+    count = head[28] | head[29] << 8
+    at, out = 30, []
+    for _ in range(count):
+        kind = head[at + 4]
+        out.append((at + 4, kind))
+        at += 5 + {1: 1, 2: 8, 3: 8, 4: 4}[kind]
+    return out
+
+
+@pytest.mark.parametrize("x", F64_PATTERNS + ["nan"])
+def test_head_f64_values_decode_as_little_endian_binary64(tmp_path, x):
+    import struct
+    import numpy as np
+    p = tmp_path / "f.mll"
+    mll.write_packed(p, np.zeros((2, 32), np.int8), np.ones(2, np.float32), name="f")
+    data = bytearray(open(p, "rb").read())
+    with mll.MllFile(bytes(data)) as f:
+        head = f.section("HEAD")
+    base = bytes(data).index(head)
+    ents = _head_entries(head)
+    at, kind = next((a, k) for a, k in ents if k == mll.I64)
+    raw = struct.pack("<Q", 0x7FF8000000000123) if x == "nan" else struct.pack("<d", x)
+    data[base + at] = mll.F64
+    data[base + at + 1:base + at + 9] = raw
+    with mll.MllFile(bytes(data), verify=False) as f:
+        _, _, entries = f.head()
+    i = [a for a, _ in ents].index(at)
+    name, k, got = entries[i]
+    assert k == mll.F64
+    assert struct.pack("<d", got) == raw
