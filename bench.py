@@ -276,7 +276,7 @@ def run_c2(rt, steps, warmup, cpu_s) -> dict:
     qd = rt.to_device(queries)
     ids = rt.empty((nq, k), np.int32)
     sc = rt.empty((nq, k), np.float32)
-    fams = ["mq_scan", "mq_select", "q4_scan", "topk_merge", "query_encode", "mq_clear", "ref_rescore", "ref_finish", "ref_scan"]
+    fams = ["mq_scan", "mq_select", "q4_scan", "topk_merge", "query_encode", "ref_rescore", "ref_finish", "ref_scan"]
     step_s, fam, dev_ms, nt = _timed(rt, lambda: rt.score_topk(cands, "cosine", qd, k, out=(ids, sc, None)),
                                      steps, warmup, fams, min_timed_s=MIN_TIMED_S)
     # the presets' step after top-k: candidate ids, packed rows and scales of
@@ -359,7 +359,7 @@ def run_c3(rt, steps, warmup, cpu_s) -> dict:
     qd = rt.to_device(queries)
     ids = rt.empty((nq, k), np.int32)
     sc = rt.empty((nq, k), np.float32)
-    fams = ["mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear", "ref_rescore", "ref_finish", "ref_scan"]
+    fams = ["mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "ref_rescore", "ref_finish", "ref_scan"]
     step_s, fam, dev_ms, nt = _timed(rt, lambda: rt.score_topk(cands, "l2_distance", qd, k, smallest=True,
                                                                out=(ids, sc, None)), steps, warmup, fams,
                                      min_timed_s=MIN_TIMED_S)
@@ -430,7 +430,7 @@ def run_c4(rt, steps, warmup, cpu_s) -> dict:
         rt.embed_pooled(td, md, tbd, pp, csd, out=emb)
         rt.score_topk(cands, "dot", emb, k, out=(ids, sc, None), quantized=True)
 
-    fams = ["embed", "embed_transpose", "embed_finalize", "mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode", "mq_clear"]
+    fams = ["embed", "embed_transpose", "embed_finalize", "mq_scan", "mq_select", "q8_scan", "topk_merge", "query_encode"]
     step_s, fam, dev_ms, nt = _timed(rt, step, steps, warmup, fams, min_timed_s=MIN_TIMED_S)
     flops_a = 2.0 * b * t * d * e
     ops_b = 2.0 * b * n * d

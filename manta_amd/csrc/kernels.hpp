@@ -47,8 +47,11 @@ struct ScanArgs {
     int wave_lists;           // 1: k <= 64 top lists held in registers (coalesced q8 kernel only)
 };
 
+// Query codes for the batched paths (one workgroup per query).  With tau
+// and bcnt given it also resets the threshold passes' per-query state
+// (tau[q] = 0, bcnt[q] = 0) before the first pass, saving a launch.
 hipError_t launch_query_encode(const uint16_t* q, int nq, int d, int pitch, int e16, int8_t* c8,
-                               int8_t* hi, int8_t* lo, QConst* qc, hipStream_t s);
+                               int8_t* hi, int8_t* lo, QConst* qc, uint64_t* tau, int* bcnt, hipStream_t s);
 
 // Error bounds of the int8 shadow of a q4 matrix: maxima over its rows of
 // E_r = |x_r - t_r e_r| and F_r = t_r |e_r| (x_r the dequantized q4 row, e_r
@@ -72,8 +75,10 @@ hipError_t launch_q4_shadow_build(const uint8_t* packed, const uint16_t* scales,
 // qa = maxabs/127, E16 digit planes in the q4 order hi/lo [nq][d], E16
 // constants qc, and per query the margin m and factor f of shadow_bound for
 // op (OP_COSINE or OP_DOT): qb[2q] = m, qb[2q+1] = f.
+// tau / bcnt as for launch_query_encode.
 hipError_t launch_query_encode_shadow(const uint16_t* q, int nq, int d, int spitch, int op, const ShadowInfo* info,
-                                      int8_t* c8, int8_t* hi, int8_t* lo, QConst* qc, float* qb, hipStream_t s);
+                                      int8_t* c8, int8_t* hi, int8_t* lo, QConst* qc, float* qb, uint64_t* tau,
+                                      int* bcnt, hipStream_t s);
 hipError_t launch_q8_scan(int op, const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s);
 // Pitches served by the coalesced q8 kernel (the others use the row-per-lane one).
 bool q8_scan_coalesced(int pitch);
@@ -232,7 +237,6 @@ hipError_t launch_mq8_scan(const MqShape& sh, const MqArgs& a, dim3 grid, size_t
 int mq_select_threads(int64_t expect_keys);
 size_t mq_select_lds(int threads, int R);
 hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s);
-hipError_t launch_mq_clear(uint64_t* tau, int* bcnt, int nq, hipStream_t s);
 
 // Candidate pack after top-k (kernels_topk.hip).
 struct PackArgs {

@@ -760,16 +760,6 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     }
 }
 
-// Reset the per-query pass state before a call (a fill kernel, not a memset
-// node, so a captured graph replays it reliably).
-__global__ void mq_clear_kernel(uint64_t* tau, int* bcnt, int nq) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < nq) {
-        tau[i] = 0ull;
-        bcnt[i] = 0;
-    }
-}
-
 // ----------------------------------------------------------------- hosts
 
 // Register budget: NA*KS*4 VGPRs of resident A fragments plus the staged
@@ -885,11 +875,6 @@ hipError_t launch_mq_select(const MqSelectArgs& a, int threads, hipStream_t s) {
         launch_mq_select_pm<2>(a, threads, lds, s);
     else
         launch_mq_select_pm<0>(a, threads, lds, s);
-    return hipGetLastError();
-}
-
-hipError_t launch_mq_clear(uint64_t* tau, int* bcnt, int nq, hipStream_t s) {
-    hipLaunchKernelGGL(mq_clear_kernel, dim3((nq + 255) / 256), dim3(256), 0, s, tau, bcnt, nq);
     return hipGetLastError();
 }
 

@@ -96,7 +96,8 @@ __device__ inline void encode_query_block(const uint16_t* __restrict__ qrow, int
 __global__ __launch_bounds__(256) void query_encode_kernel(const uint16_t* __restrict__ q, int d, int pitch,
                                                            int e16, int8_t* __restrict__ c8,
                                                            int8_t* __restrict__ hi, int8_t* __restrict__ lo,
-                                                           QConst* __restrict__ qc) {
+                                                           QConst* __restrict__ qc, uint64_t* __restrict__ tau,
+                                                           int* __restrict__ bcnt) {
     __shared__ QueryLds L;
     const int qi = blockIdx.x;
     // e16: 0 = E8 codes, 1 = E16 digit planes, 2 = E16 planes in the q4 nibble order
@@ -109,7 +110,12 @@ __global__ __launch_bounds__(256) void query_encode_kernel(const uint16_t* __res
             c8[(int64_t)qi * pitch + c] = L.c8[c];
         }
     }
-    if (threadIdx.x == 0) qc[qi] = L.qc;
+    if (threadIdx.x == 0) {
+        qc[qi] = L.qc;
+        // the threshold passes start from no threshold and no kept keys
+        if (tau) tau[qi] = 0ull;
+        if (bcnt) bcnt[qi] = 0;
+    }
 }
 
 // Shadow-scan query encoding (one workgroup per query): the E16 planes in
@@ -125,7 +131,8 @@ __global__ __launch_bounds__(256) void query_encode_shadow_kernel(const uint16_t
                                                                   int op, const ShadowInfo* __restrict__ info,
                                                                   int8_t* __restrict__ c8, int8_t* __restrict__ hi,
                                                                   int8_t* __restrict__ lo, QConst* __restrict__ qc,
-                                                                  float* __restrict__ qb) {
+                                                                  float* __restrict__ qb, uint64_t* __restrict__ tau,
+                                                                  int* __restrict__ bcnt) {
     __shared__ QueryLds L;
     __shared__ double g2s[4];
     __shared__ long long sss[4];
@@ -169,6 +176,8 @@ __global__ __launch_bounds__(256) void query_encode_shadow_kernel(const uint16_t
     __syncthreads();
     if (tid == 0) {
         qc[qi] = L.qc;
+        if (tau) tau[qi] = 0ull;
+        if (bcnt) bcnt[qi] = 0;
         const double G = __builtin_sqrt(g2s[0] + g2s[1] + g2s[2] + g2s[3]);
         const double qn = __builtin_sqrt((double)(sss[0] + sss[1] + sss[2] + sss[3])) * (double)qs;
         const double up = 1.0 + 9.5367431640625e-7;
@@ -631,16 +640,17 @@ __global__ __launch_bounds__(256) void q8_rescore_acc_kernel(const int8_t* __res
 // ----------------------------------------------------------------- hosts
 
 hipError_t launch_query_encode(const uint16_t* q, int nq, int d, int pitch, int e16, int8_t* c8,
-                               int8_t* hi, int8_t* lo, QConst* qc, hipStream_t s) {
-    hipLaunchKernelGGL(query_encode_kernel, dim3(nq), dim3(256), 0, s, q, d, pitch, e16, c8, hi, lo, qc);
+                               int8_t* hi, int8_t* lo, QConst* qc, uint64_t* tau, int* bcnt, hipStream_t s) {
+    hipLaunchKernelGGL(query_encode_kernel, dim3(nq), dim3(256), 0, s, q, d, pitch, e16, c8, hi, lo, qc, tau, bcnt);
     return hipGetLastError();
 }
 
 hipError_t launch_query_encode_shadow(const uint16_t* q, int nq, int d, int spitch, int op, const ShadowInfo* info,
-                                      int8_t* c8, int8_t* hi, int8_t* lo, QConst* qc, float* qb, hipStream_t s) {
+                                      int8_t* c8, int8_t* hi, int8_t* lo, QConst* qc, float* qb, uint64_t* tau,
+                                      int* bcnt, hipStream_t s) {
     if (d % 32 != 0 || d > kMaxQueryDim || spitch < d) return hipErrorInvalidValue;
     hipLaunchKernelGGL(query_encode_shadow_kernel, dim3(nq), dim3(256), 0, s, q, d, spitch, op, info, c8, hi, lo, qc,
-                       qb);
+                       qb, tau, bcnt);
     return hipGetLastError();
 }
 

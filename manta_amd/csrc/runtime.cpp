@@ -1092,11 +1092,12 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, cons
     float* qb = cv.take<float>((size_t)nq * 2);
     if (p.shadow) {
         LAUNCH_TRY(manta::launch_query_encode_shadow(q, (int)nq, (int)c->d, width, dop, c->shadow_info, c8, hi, lo,
-                                                     qc, qb, rt->stream),
+                                                     qc, qb, topk ? tau : nullptr, topk ? bcnt : nullptr, rt->stream),
                    "query_encode");
     } else {
         const int e16 = p.q4 ? 2 : (dop != manta::OP_DOT ? 1 : 0);
-        LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, width, e16, c8, hi, lo, qc, rt->stream),
+        LAUNCH_TRY(manta::launch_query_encode(q, (int)nq, (int)c->d, width, e16, c8, hi, lo, qc,
+                                              topk ? tau : nullptr, topk ? bcnt : nullptr, rt->stream),
                    "query_encode");
     }
     manta::MqArgs a{};
@@ -1132,7 +1133,7 @@ int run_mq(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, cons
         LAUNCH_TRY(launch_mq_pass(p, dop, a, ps.R, rt->stream), "mq_scan");
         return MANTA_ROCM_OK;
     }
-    LAUNCH_TRY(manta::launch_mq_clear(tau, bcnt, (int)nq, rt->stream), "mq_clear");
+    // (tau and bcnt were reset by the query encoding above)
     manta::MqSelectArgs sa{};
     sa.regions = reg;
     sa.counts = cnt;
