@@ -970,35 +970,25 @@ __global__ __launch_bounds__(256) void embed_gemm7_kernel(EmbedArgs a, int xcd_m
     const int64_t t0 = (tile % a.tiles_per_seq) * E7_WM;
     const int nb0 = slice * E7_WN;
 
-    // This lane's row (32 * wave + lane % 32 of the tile, k-half lane / 32):
-    // its token and mask first -- the only loads anything waits for before
-    // the rest are issued (a compiler-placed wait for them would otherwise
-    // also wait for the direct-to-LDS loads, which it cannot count).
+    // This lane's row (32 * wave + lane % 32 of the tile, k-half lane / 32).
+    // Its token id goes first, by an asm load, then the projection slice's
+    // direct-to-LDS loads (they need no token, so they travel during the
+    // token's latency: 0.2 us a call on C1), then one explicit wait that
+    // counts them and retires only the token (loads complete in order; a
+    // compiler-placed wait could not count the asm loads and would wait for
+    // all of them), then the row loads and the mask.
     const int l32 = lane & 31, hf = lane >> 5;
     int64_t src = 0;
     bool live_row = false;
-    {
-        const int64_t t = t0 + 32 * wave + l32;
-        if (t < a.T) {
-            const int idx = a.tokens[seq * a.T + t];
-            live_row = !a.mask || a.mask[seq * a.T + t] != 0;
-            if (idx >= 0 && idx < a.vocab) src = idx;
-            else if (hf == 0 && slice == 0) report_gather_error(a.err, seq * a.T + t, idx);
-        }
-    }
-    // bit r of the word: row r of the wave's 32 is unmasked (both k-halves
-    // of a row hold the same flag)
-    const uint32_t livew = (uint32_t)__ballot(live_row);
-    const uint8_t* arow = (const uint8_t*)a.table + src * K * 2 + 64 * hf;
-    h8 av[NB][4];
-#pragma unroll
-    for (int b = 0; b < NB; b++)
-#pragma unroll
-        for (int s = 0; s < 4; s++) av[b][s] = *(const h8*)(arow + 128 * b + 16 * s);
-    // then the projection slice, rows 0 .. K-1 packed at 192 bytes (16-byte
-    // pieces: a wave load covers 5 1/3 rows), in flight with the row loads
+    const int64_t tt = t0 + 32 * wave + l32;
+    const int64_t tix = seq * a.T + (tt < a.T ? tt : a.T - 1);  // clamped in range
+    int idx_raw;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(idx_raw) : "v"(a.tokens + tix) : "memory");
     const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
     const uint8_t* bsrc = (const uint8_t*)a.B + nb0 * 2;
+    constexpr int NBW = (NBL + 3) / 4;  // projection loads of wave 0 (the others issue as many or one fewer)
+    // the projection slice, rows 0 .. K-1 packed at 192 bytes (16-byte
+    // pieces: a wave load covers 5 1/3 rows)
 #pragma unroll
     for (int u0 = 0; u0 < NBL; u0 += 4) {
         const int u = u0 + wave;
@@ -1008,10 +998,34 @@ __global__ __launch_bounds__(256) void embed_gemm7_kernel(EmbedArgs a, int xcd_m
                           __builtin_amdgcn_readfirstlane(base + u * 1024));
         }
     }
+    // the token load is older than this wave's projection loads, of which
+    // all may still be outstanding (NBW, or NBW - 1 for the waves that issue
+    // one fewer); idx_raw is an operand so nothing reads it before the wait
+    if (NBL % 4 == 0 || wave < NBL % 4)
+        asm volatile("s_waitcnt vmcnt(%1)" : "+v"(idx_raw) : "n"(NBW) : "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(%1)" : "+v"(idx_raw) : "n"(NBW - 1 > 0 ? NBW - 1 : 0) : "memory");
+    {
+        if (tt < a.T) {
+            const int idx = idx_raw;
+            if (idx >= 0 && idx < a.vocab) src = idx;
+            else if (hf == 0 && slice == 0) report_gather_error(a.err, seq * a.T + tt, idx);
+        }
+    }
+    const uint8_t* arow = (const uint8_t*)a.table + src * K * 2 + 64 * hf;
+    h8 av[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int s = 0; s < 4; s++) av[b][s] = *(const h8*)(arow + 128 * b + 16 * s);
+    if (tt < a.T) live_row = !a.mask || a.mask[seq * a.T + tt] != 0;
     // the direct-to-LDS loads are not tracked by the compiler: every wave
     // retires its own (and the row loads before them), then the barrier
     // makes all of them visible
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    // bit r of the word: row r of the wave's 32 is unmasked (both k-halves
+    // of a row hold the same flag)
+    const uint32_t livew = (uint32_t)__ballot(live_row);
 
     // MFMA step i = 4b + s; its projection fragments (one per 32-column
     // tile) are read from LDS one step ahead, so the transpose reads of step
