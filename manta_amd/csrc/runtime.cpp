@@ -41,6 +41,7 @@ struct TimedLaunch {
 
 struct MantaRocm {
     int device = 0;
+    int cus = 256;  // compute units of the device (hipDeviceAttributeMultiprocessorCount)
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     void* ws = nullptr;
@@ -360,6 +361,11 @@ int manta_rocm_create(int device, MantaRocm** out, char** err) {
         return hip_fail(err, "hipStreamCreate", e);
     }
     rt->stream = rt->own_stream;
+    {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+            rt->cus = cus;
+    }
     // the allocation-free entry point's scratch address on this device
     manta_rt::noalloc_init(device);
     e = hipMalloc((void**)&rt->err_word, sizeof(unsigned long long));
@@ -803,13 +809,14 @@ int check_score_args(const MantaRocmCandidates* c, int op_in, const void* q, int
     return MANTA_ROCM_OK;
 }
 
-// Rounds of 256 rows per workgroup: aim for about 2048 workgroups (8 per
-// CU), with at most 64 rounds.
-// Rounds of 256 rows per scan workgroup: about 512 workgroups in all (two per
-// CU, one resident generation), so each streams a long contiguous range and
-// the per-workgroup prologue and top-k publication are paid rarely.
-int choose_rounds(int64_t tiles, int64_t nq) {
-    int64_t r = (tiles * nq + 511) / 512;
+// Rounds of 256 rows per scan workgroup, for about `wgs` workgroups in all,
+// so each streams a long contiguous range and the per-workgroup prologue and
+// top-k publication are paid rarely.  The fused top-k takes one workgroup
+// per CU (C0's 32 problems: 82.3 us a launch against 85.1 with two per CU,
+// 97.6 with one per two CUs and 99.2 with 1.25 per CU); the score matrix
+// keeps two per CU.
+int choose_rounds(int64_t tiles, int64_t nq, int64_t wgs) {
+    int64_t r = (tiles * nq + wgs - 1) / wgs;
     // small calls are latency-bound: two rounds halve the parts the last
     // workgroup merges (one 65536 x 256 query: 17.8 against 19.2 us a call;
     // four and eight rounds measured 18.7 and 22.3)
@@ -1204,7 +1211,7 @@ int manta_rocm_score(MantaRocm* rt, const MantaRocmCandidates* c, int op, const 
     const MqPlan plan = mq_plan(c, so.scan, nq, 0, false);
     if (plan.use) return run_mq(rt, c, so.scan, MANTA_ROCM_LARGEST, q, nq, 0, plan, out, nullptr, nullptr, err);
     ScanArgs a = scan_args(c, q);
-    a.rounds = choose_rounds(tiles, nq);
+    a.rounds = choose_rounds(tiles, nq, 512);
     a.out_scores = out;
     const int64_t parts = (tiles + a.rounds - 1) / a.rounds;
     return launch_scan(rt, c, so.scan, a, dim3((unsigned)parts, (unsigned)nq), 0, err);
@@ -1235,7 +1242,7 @@ int scan_topk(MantaRocm* rt, const MantaRocmCandidates* c, int dop, int order, c
                        "q8_rescore");
         return MANTA_ROCM_OK;
     }
-    StreamTopk st = stream_topk_shape(c, nq, k, choose_rounds((c->n + 255) / 256, nq));
+    StreamTopk st = stream_topk_shape(c, nq, k, choose_rounds((c->n + 255) / 256, nq, rt->cus));
     uint64_t* partial = nullptr;
     int rc = take_buffer(rt, sc, (size_t)nq * st.parts * k * 8, (void**)&partial, err);
     if (rc) return rc;
