@@ -47,21 +47,30 @@ __global__ __launch_bounds__(256) void ref_rescore_kernel(RefArgs a, uint64_t* _
     const int q = blockIdx.y;
     const int d = a.d;
     const uint16_t* qrow = a.queries + (int64_t)q * d;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const bool has = i < a.kp;
+    const int32_t id = has ? a.cand_ids[(int64_t)q * a.kp + i] : -1;
     for (int c = threadIdx.x; c < d; c += 256) qf[c] = h2f(qrow[c]);
     __syncthreads();
-    if (OP == OP_COSINE && threadIdx.x == 0) sqn_s = ref_sqrt_norm(qf, d);
-    __syncthreads();
-    const double sqn = OP == OP_COSINE ? sqn_s : 0.0;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= a.kp) return;
-    const int32_t id = a.cand_ids[(int64_t)q * a.kp + i];
-    uint64_t key = 0;
-    if (id >= 0 && (int64_t)id < a.n) {
-        const float s = ref_row_score<FMT, OP>(a.codes, a.scales, a.sqd, (int64_t)q * a.set_stride + id, a.pitch, d,
-                                               qf, sqn);
-        key = make_key(s, (uint32_t)id, a.smallest);
+    // cosine: the query's f64 norm (a sequential sum) on the last thread,
+    // which holds no candidate unless all 256 do, while the others sum theirs
+    if (OP == OP_COSINE && threadIdx.x == 255) sqn_s = ref_sqrt_norm(qf, d);
+    const bool ok = id >= 0 && (int64_t)id < a.n;
+    const int64_t row = (int64_t)q * a.set_stride + (ok ? id : 0);
+    RefAcc<OP> acc;
+    double dn = 0.0;
+    if (ok) {
+        if (OP == OP_COSINE) dn = a.sqd[row];
+        if (FMT == 8)
+            acc = ref_acc_q8<OP>(qf, (const int8_t*)a.codes + row * a.pitch, ((const float*)a.scales)[row], d);
+        else
+            acc = ref_acc_q4<OP>(qf, (const uint8_t*)a.codes + row * a.pitch,
+                                 (const uint16_t*)a.scales + row * (d / 32), d);
     }
-    keys[(int64_t)q * a.kp + i] = key;
+    if (OP == OP_COSINE) __syncthreads();  // sqn_s is published
+    if (!has) return;
+    const double sqn = OP == OP_COSINE ? sqn_s : 0.0;
+    keys[(int64_t)q * a.kp + i] = ok ? make_key(acc.finish(sqn, dn), (uint32_t)id, a.smallest) : 0ull;
 }
 
 // One workgroup per query: sort the candidates' reference keys, take the

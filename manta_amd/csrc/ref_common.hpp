@@ -144,18 +144,25 @@ struct RefAcc {
 };
 
 // Reference score of q8 row `row` (pitch bytes, 16-byte aligned, d codes,
-// f32 scale s) against the f32 query qf[0..d).  The row's bytes are loaded
-// 128 at a time (eight 16-byte loads in flight) ahead of the sequential sum.
+// f32 scale s) against the f32 query qf[0..d): ref_acc_q8 runs the
+// sequential sum, ref_score_q8 also finishes it.  The row's bytes arrive 128
+// at a time (eight 16-byte loads), the next 128 loaded while the current
+// ones are summed.
 template <int OP>
-__device__ inline float ref_score_q8(const float* qf, const int8_t* row, float s, int d, double sqn, double sqd) {
+__device__ __forceinline__ RefAcc<OP> ref_acc_q8(const float* qf, const int8_t* row, float s, int d) {
     RefAcc<OP> acc;
-    for (int c0 = 0; c0 < d; c0 += 128) {
-        v4i w[8];
+    // (loads past the row's last 16 bytes re-read them: no branch between
+    // the loads, so they all go out at once; those values are never used)
+    const int last = (d - 1) & ~15;
+    v4i w[8], wn[8];
+    auto load = [&](v4i (&dst)[8], int c0) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) w[j] = c0 + 16 * j < d ? *(const v4i*)(row + c0 + 16 * j) : v4i{0, 0, 0, 0};
+        for (int j = 0; j < 8; j++) dst[j] = *(const v4i*)(row + (c0 + 16 * j < last ? c0 + 16 * j : last));
+    };
+    auto sum = [&](const v4i (&g)[8], int c0) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int ws[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+            const int ws[4] = {g[j].x, g[j].y, g[j].z, g[j].w};
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int c = c0 + 16 * j + e;
@@ -164,37 +171,71 @@ __device__ inline float ref_score_q8(const float* qf, const int8_t* row, float s
                 acc.add(qf[c], fmul_rn((float)code, s));
             }
         }
+    };
+    // two buffers in turn, so a sum waits only for its own group's loads
+    load(w, 0);
+    for (int c0 = 0; c0 < d; c0 += 256) {
+        if (c0 + 128 < d) load(wn, c0 + 128);
+        sum(w, c0);
+        if (c0 + 128 >= d) break;
+        if (c0 + 256 < d) load(w, c0 + 256);
+        sum(wn, c0 + 128);
     }
-    return acc.finish(sqn, sqd);
+    return acc;
+}
+template <int OP>
+__device__ inline float ref_score_q8(const float* qf, const int8_t* row, float s, int d, double sqn, double sqd) {
+    return ref_acc_q8<OP>(qf, row, s, d).finish(sqn, sqd);
 }
 
 // Reference score of a q4 row (d/2 bytes of nibbles, low nibble first, and
-// d/32 f16 block scales; d % 32 == 0), four blocks loaded at a time.
+// d/32 f16 block scales; d % 32 == 0): the sum (ref_acc_q4) and the finished
+// score (ref_score_q4).  Blocks arrive four at a time, the next four loaded
+// while the current ones are summed.
 template <int OP>
-__device__ inline float ref_score_q4(const float* qf, const uint8_t* prow, const uint16_t* srow, int d, double sqn,
-                                     double sqd) {
+__device__ __forceinline__ RefAcc<OP> ref_acc_q4(const float* qf, const uint8_t* prow, const uint16_t* srow, int d) {
     RefAcc<OP> acc;
     const int nb = d / 32;
-    for (int b0 = 0; b0 < nb; b0 += 4) {
-        v4i w[4];
-        float sb[4];
+    v4i w[4], wn[4];
+    uint16_t sb[4], sbn[4];  // raw f16 scales: converted where used, so a
+                             // prefetch is never waited for early
+    // (blocks past the row's last re-read it: no branch between the loads)
+    auto load = [&](v4i (&dw)[4], uint16_t (&ds)[4], int b0) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            w[j] = b0 + j < nb ? ((const v4i*)prow)[b0 + j] : v4i{0, 0, 0, 0};
-            sb[j] = b0 + j < nb ? h2f(srow[b0 + j]) : 0.0f;
+            const int b = b0 + j < nb ? b0 + j : nb - 1;
+            dw[j] = ((const v4i*)prow)[b];
+            ds[j] = srow[b];
         }
+    };
+    auto sum = [&](const v4i (&g)[4], const uint16_t (&gs)[4], int b0) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             if (b0 + j >= nb) break;
-            const int ws[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+            const int ws[4] = {g[j].x, g[j].y, g[j].z, g[j].w};
+            const float sj = h2f(gs[j]);
 #pragma unroll
             for (int e = 0; e < 32; e++) {
                 const int code = (ws[e >> 3] << (28 - 4 * (e & 7))) >> 28;
-                acc.add(qf[(b0 + j) * 32 + e], fmul_rn((float)code, sb[j]));
+                acc.add(qf[(b0 + j) * 32 + e], fmul_rn((float)code, sj));
             }
         }
+    };
+    // two buffers in turn, so a sum waits only for its own blocks' loads
+    load(w, sb, 0);
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+        if (b0 + 4 < nb) load(wn, sbn, b0 + 4);
+        sum(w, sb, b0);
+        if (b0 + 4 >= nb) break;
+        if (b0 + 8 < nb) load(w, sb, b0 + 8);
+        sum(wn, sbn, b0 + 4);
     }
-    return acc.finish(sqn, sqd);
+    return acc;
+}
+template <int OP>
+__device__ inline float ref_score_q4(const float* qf, const uint8_t* prow, const uint16_t* srow, int d, double sqn,
+                                     double sqd) {
+    return ref_acc_q4<OP>(qf, prow, srow, d).finish(sqn, sqd);
 }
 
 // ------------------------------------------------------------ error bounds
