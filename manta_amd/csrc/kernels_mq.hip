@@ -420,6 +420,8 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     const int q = blockIdx.x;
     const int k = a.k;
 
+    // the previous best's count travels with the region counts (one round trip)
+    int fill = __builtin_amdgcn_readfirstlane(a.bcnt[q]);
     // exclusive prefix of the pass's region counts, and their maximum
     int carry = 0, cmax = 0;
     if (tid == 0) cmax_s = 0;
@@ -448,8 +450,35 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     if (lane == 0 && cmax > 0) atomicMax(&cmax_s, cmax);
     if (tid == 0) pre[a.R] = M;
 
-    int fill = a.bcnt[q];
-    for (int i = tid; i < fill; i += NT) buf[i] = a.best[(int64_t)q * k + i];
+    const uint64_t* regq = a.regions + (int64_t)q * a.rc;  // region w at regq + w*nq*rc
+    // When the previous best and the whole pass fit the buffer at once, both
+    // go straight to LDS with direct-to-LDS dword loads (lane l of a wave
+    // instruction writes dword l after the instruction's base; lanes past a
+    // region's end are masked off), every region's in the same round: no
+    // registers hold them and no load waits for another.  Wave w takes
+    // regions w, w + NW, ...; 64 dwords (32 entries) per instruction.
+    const bool direct = M <= LCAP - fill && M >= 4 * a.R;  // dense regions (sparse ones: one round below)
+    if (direct) {
+        __syncthreads();  // pre[] complete
+        const uint32_t lb = __builtin_amdgcn_readfirstlane(
+            (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem);
+        const uint32_t* bsrc = (const uint32_t*)(a.best + (int64_t)q * k);
+        for (int o = 64 * wave; o < 2 * fill; o += 64 * NW)
+            if (o + lane < 2 * fill) lds_load4(bsrc + o + lane, __builtin_amdgcn_readfirstlane(lb + 4 * o));
+        for (int w = wave; w < a.R; w += NW) {
+            const int p0 = __builtin_amdgcn_readfirstlane(pre[w]);
+            const int c2 = 2 * (__builtin_amdgcn_readfirstlane(pre[w + 1]) - p0);
+            const uint32_t* src = (const uint32_t*)(regq + (int64_t)w * a.nq * a.rc);
+            const uint32_t dst = lb + 8 * (uint32_t)(fill + p0);
+            for (int o = 0; o < c2; o += 64)
+                if (o + lane < c2) lds_load4(src + o + lane, __builtin_amdgcn_readfirstlane(dst + 4 * o));
+        }
+        // the loads are invisible to the compiler's wait counting: every wave
+        // retires its own, then the barrier publishes all of them
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+        for (int i = tid; i < fill; i += NT) buf[i] = a.best[(int64_t)q * k + i];
+    }
     __syncthreads();
     // regions holding 4 to 64 entries on average and at most: gather region
     // by region (sparser regions take fewer rounds of loads entry by entry)
@@ -492,7 +521,6 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
         fill = k;
     };
 
-    const uint64_t* regq = a.regions + (int64_t)q * a.rc;  // region w at regq + w*nq*rc
     const float qmax = PM == 1 ? a.qconst[q].a : 0.0f;
     if (PM == 2) {
         // the query's E16 digit planes, read by every rescoring below
@@ -555,7 +583,16 @@ __global__ __launch_bounds__(NT) void mq_select_kernel(MqSelectArgs a) {
     for (int base = 0; base < M;) {
         const int take = (M - base) < (LCAP - fill) ? (M - base) : (LCAP - fill);
         int added = take;  // keys this batch leaves in buf (fewer after pruning)
-        if (by_region) {
+        if (direct) {
+            // the pass's entries are in place: pairs become keys there
+            if (PM == 1 || (PM == 2 && prune)) {
+                for (int i = tid; i < take; i += NT) {
+                    const uint64_t x = buf[fill + i];
+                    buf[fill + i] = PM == 1 ? dot_pair_key(x, qmax, a.smallest)
+                                            : make_key(__uint_as_float((uint32_t)(x >> 32)), (uint32_t)x, a.smallest);
+                }
+            }
+        } else if (by_region) {
             // Wave w takes regions w, w + NW, ...; lane l moves entry l of
             // each, 8 regions' loads in flight at once.  Entries outside the
             // batch [base, base + take) stay for a later batch.
