@@ -280,6 +280,64 @@ __device__ inline void finish_wave_lists(const ScanArgs& a, uint64_t list, uint6
     __syncthreads();
     if (!S.last) return;
     const uint64_t* src = a.partial + (int64_t)qi * per_q;
+    // Many parts (a single query's call: 128 parts of k): the k-th largest
+    // part head is a floor of the final k-th key (the k best heads are k
+    // distinct keys), only the k parts whose heads reach it hold keys at or
+    // above it, and those k^2 or fewer candidates take their place by rank
+    // (each counts the candidates above it) instead of one insertion each.
+    // Fewer than k keys in the parts' heads: the lists below.
+    if (a.k <= 16 && (int)gridDim.x >= a.k && gridDim.x <= 256) {
+        __shared__ uint64_t heads[256];
+        __shared__ uint64_t floor_s;
+        __shared__ int ncand;
+        const int t = (int)threadIdx.x, P = (int)gridDim.x, k = a.k;
+        uint64_t mk[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            mk[j] = (t < P && j < k) ? __hip_atomic_load(src + (int64_t)t * k + j, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                     : 0ull;
+        heads[t] = mk[0];  // a part's list is sorted: its first key is its best
+        if (t == 0) {
+            floor_s = 0ull;
+            ncand = 0;
+        }
+        __syncthreads();
+        if (t < P && mk[0]) {
+            int rank = 0;
+            for (int i = 0; i < P; i++) rank += heads[i] > mk[0] ? 1 : 0;
+            if (rank == k - 1) floor_s = mk[0];  // keys are distinct: one thread
+        }
+        __syncthreads();
+        const uint64_t fl = floor_s;
+        if (fl) {
+            int cnt = 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) cnt += mk[j] >= fl ? 1 : 0;  // (empty slots are 0 < fl)
+            if (t < P && cnt) {
+                int pos = atomicAdd(&ncand, cnt);
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    if (mk[j] >= fl) buf[pos++] = mk[j];
+            }
+            __syncthreads();
+            const int nc = ncand;  // k <= nc <= k^2 <= blockDim.x
+            const uint64_t mine = t < nc ? buf[t] : 0ull;
+            int rank = 0;
+            if (t < nc)
+                for (int i = 0; i < nc; i++) rank += buf[i] > mine ? 1 : 0;
+            __syncthreads();  // every read of buf is done
+            if (t < nc && rank < k) buf[rank] = mine;
+            __syncthreads();
+            if (t < k) {
+                const uint64_t key = buf[t];
+                a.out_ids[(int64_t)qi * k + t] = (int32_t)key_index(key);
+                if (a.out_topk_scores) a.out_topk_scores[(int64_t)qi * k + t] = key_score(key, a.smallest);
+            }
+            if (t == 0) __hip_atomic_store(&a.tickets[qi], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
     list = 0;
     thr = 0;
     // batches of 64 keys go to the waves in turn; B batches per wave in flight
