@@ -280,6 +280,29 @@ __device__ inline void finish_wave_lists(const ScanArgs& a, uint64_t list, uint6
     __syncthreads();
     if (!S.last) return;
     const uint64_t* src = a.partial + (int64_t)qi * per_q;
+    // Up to one part key per thread (C0's 32-problem launch: 8 parts of 10):
+    // every key counts the keys above it and the k best land at their ranks,
+    // no insertions on the launch's last step.
+    if (per_q <= (int64_t)blockDim.x) {
+        __shared__ uint64_t res[64];  // k <= 64 on the list path
+        const int t = (int)threadIdx.x, n = (int)per_q, k = a.k;
+        const uint64_t mine = t < n ? __hip_atomic_load(src + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        buf[t] = mine;
+        if (t < 64) res[t] = 0ull;
+        __syncthreads();
+        int rank = 0;
+        if (mine)
+            for (int i = 0; i < n; i++) rank += buf[i] > mine ? 1 : 0;
+        if (mine && rank < k) res[rank] = mine;  // keys are distinct: so are their ranks
+        __syncthreads();
+        if (t < k) {
+            const uint64_t key = res[t];
+            a.out_ids[(int64_t)qi * k + t] = key ? (int32_t)key_index(key) : -1;
+            if (a.out_topk_scores) a.out_topk_scores[(int64_t)qi * k + t] = key ? key_score(key, a.smallest) : 0.0f;
+        }
+        if (t == 0) __hip_atomic_store(&a.tickets[qi], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     // Many parts (a single query's call: 128 parts of k): the k-th largest
     // part head is a floor of the final k-th key (the k best heads are k
     // distinct keys), only the k parts whose heads reach it hold keys at or
