@@ -392,13 +392,30 @@ __device__ __forceinline__ void wave_list_offer(uint64_t key, uint64_t& list, ui
 }
 
 // Merge the lists of all waves of the workgroup into wave 0's (whole
-// workgroup; buf holds blockDim.x keys of LDS).  Ends with a barrier.
+// workgroup; buf holds blockDim.x keys of LDS, at least the waves' k each).
+// By rank: the waves' k entries go to buf side by side, each held key
+// counts the held keys above it (LDS broadcast reads, no dependent steps),
+// and the k best land at their ranks, already sorted (C0: 81.1 -> 80.7 us a
+// 32-problem launch, one query's call 15.76 -> 15.26 us, against inserting
+// the other waves' keys into wave 0's list one at a time).  Ends with a
+// barrier.
 __device__ inline void wave_lists_merge(uint64_t& list, uint64_t& thr, int k, uint64_t* buf) {
+    __shared__ uint64_t wres[64];  // k <= 64 on the list path
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    buf[threadIdx.x] = lane < k ? list : 0ull;
+    const int n = (int)(blockDim.x >> 6) * k;
+    if (lane < k) buf[wave * k + lane] = list;
+    if (threadIdx.x < 64) wres[threadIdx.x] = 0ull;
+    __syncthreads();
+    const int t = (int)threadIdx.x;
+    const uint64_t mine = t < n ? buf[t] : 0ull;
+    int rank = 0;
+    if (mine)
+        for (int j = 0; j < n; j++) rank += buf[j] > mine ? 1 : 0;
+    if (mine && rank < k) wres[rank] = mine;  // keys are distinct: so are their ranks
     __syncthreads();
     if (wave == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++) wave_list_offer(buf[w * 64 + lane], list, thr, k);
+        list = lane < k ? wres[lane] : 0ull;
+        thr = readlane_u64(list, k - 1);
     }
     __syncthreads();
 }
