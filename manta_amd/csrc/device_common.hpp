@@ -391,6 +391,34 @@ __device__ __forceinline__ void wave_list_offer(uint64_t key, uint64_t& list, ui
     }
 }
 
+// The first offer to an empty list: the batch's keys take their places by
+// rank (each lane counts the batch keys above its own through this wave's 64
+// LDS slots, wbuf), so lane i ends holding the i-th largest with no chain of
+// insertions.  The lanes trade values through wbuf: LDS operations of one
+// wave run in order in the hardware, and the empty asm statements with a
+// memory clobber keep the compiler from answering a read from the thread's
+// own earlier store (another lane's store sits in between).
+__device__ __forceinline__ void wave_list_first_fill(uint64_t key, uint64_t& list, uint64_t& thr, int k,
+                                                     uint64_t* wbuf) {
+    const int lane = threadIdx.x & 63;
+    wbuf[lane] = key;
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    int rank = 0;
+    if (key)
+        for (int j = 0; j < 64; j++) rank += wbuf[j] > key ? 1 : 0;
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    wbuf[lane] = 0ull;
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    if (key) wbuf[rank] = key;  // keys are distinct: so are their ranks
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    list = wbuf[lane];
+    thr = readlane_u64(list, k - 1);
+}
+
 // Merge the lists of all waves of the workgroup into wave 0's (whole
 // workgroup; buf holds blockDim.x keys of LDS, at least the waves' k each).
 // By rank: the waves' k entries go to buf side by side, each held key

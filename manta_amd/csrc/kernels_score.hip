@@ -505,6 +505,7 @@ template <int OP, int L, int C, bool LISTS>
 __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
     extern __shared__ uint64_t topk_keys[];
     __shared__ ScanTopkLds S;
+    __shared__ uint64_t ff_keys[LISTS ? 256 : 1];  // the lists' first fill, 64 keys a wave
     constexpr int PITCH = 16 * L * C;
     constexpr int JS0 = C == 1 ? 16 : (C == 2 ? 8 : 4);  // rows per load step (<= 16 loads)
     constexpr int JS = JS0 < L ? JS0 : L;
@@ -591,7 +592,12 @@ __global__ __launch_bounds__(256) void q8_scan_kernel(ScanArgs a) {
         float score = 0.0f;
         if (valid) score = q8_epilogue<OP>(my_hi, my_lo, sc, kq, dn, d2);
         if (LISTS) {
-            wave_list_offer(valid ? make_key(score, (uint32_t)row, a.smallest) : 0ull, list, thr, a.k);
+            const uint64_t key = valid ? make_key(score, (uint32_t)row, a.smallest) : 0ull;
+            // (the lists start empty: the first round fills them by rank,
+            // in LDS of its own -- a wave that finishes early may already be
+            // merging through topk_keys)
+            if (r == 0) wave_list_first_fill(key, list, thr, a.k, ff_keys + wave * 64);
+            else wave_list_offer(key, list, thr, a.k);
             continue;
         }
         const uint64_t tau = a.out_scores ? 0ull : S.st.tau;
@@ -744,6 +750,8 @@ bool q8_scan_coalesced(int pitch) {
 template <int OP>
 static hipError_t launch_q8_op(const ScanArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     const int chunks = a.pitch / 16;
+    // the list path's merges use 64 LDS keys per wave
+    if (a.wave_lists && !a.out_scores && lds < 256 * sizeof(uint64_t)) return hipErrorInvalidValue;
 #define MANTA_Q8(LL, CC)                                                                           \
     if (chunks == (LL) * (CC)) {                                                                   \
         if (a.wave_lists && !a.out_scores)                                                         \
